@@ -1,0 +1,235 @@
+"""Benchmark of the decode hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+
+Default workload (the headline line): single-token fp16 GEMV at the Llama-3-8B
+FFN shapes, W 14336x4096 and 4096x14336, W ~ N(0, 0.02^2), x fp16 ~ N(0, 1),
+fp32 accumulation. One step = one GEMV of each shape (an FFN's worth of
+weights, 234,991,616 algorithmic bytes). Weights rotate over enough copies
+(> 512 MiB) that the 256 MiB Infinity Cache cannot serve them, and all inputs
+are resident in HBM before the timed region. The timed region is bracketed by
+torch.cuda.synchronize() and measured with events on the launch stream.
+
+The line also carries, in "detail", the other legs of the headline metric
+measured the same way: int8 block-32 GEMV at the same shapes and decode
+attention at L = 32768 (32 Q / 8 KV heads, head_dim 128). "cpu_baseline" is the
+C oracle's fp16 GEMV (OpenMP over the host cores) on the 14336x4096 matrix.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+PEAK_HBM_GBS = 8000.0
+ROTATE_MIN_BYTES = 600 * 2**20
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _events_time(fn, steps: int, warmup: int) -> float:
+    """Average ms per call of fn(i) over `steps` calls after `warmup` calls."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fn(warmup + i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _copies(nbytes: int) -> int:
+    return max(3, math.ceil(ROTATE_MIN_BYTES / nbytes))
+
+
+def gemv_f16_leg(steps: int, warmup: int, dev) -> dict:
+    import torch
+
+    from gemmagemini4hackathon2026_10_2425_amd import ops
+
+    shapes = [(14336, 4096), (4096, 14336)]
+    R = _copies(14336 * 4096 * 2)
+    mats = {s: [ops.fill_normal(s, torch.float16, 7, 100 + i, 0.02, dev) for i in range(R)] for s in shapes}
+    xs = {s: ops.fill_normal((s[1],), torch.float16, 7, 90, 1.0, dev) for s in shapes}
+    ys = {s: torch.empty(s[0], dtype=torch.float32, device=dev) for s in shapes}
+    nbytes = {s: s[0] * s[1] * 2 + s[1] * 2 + s[0] * 4 for s in shapes}
+    per = {}
+    for s in shapes:
+        ms = _events_time(lambda i, s=s: ops.matvec_f16(mats[s][i % R], xs[s], ys[s]), steps, warmup)
+        per[s] = ms
+    ms_step = _events_time(
+        lambda i: [ops.matvec_f16(mats[s][i % R], xs[s], ys[s]) for s in shapes], steps, warmup
+    )
+    step_bytes = sum(nbytes.values())
+    return {
+        "ms_per_step": ms_step,
+        "gbs": step_bytes / ms_step / 1e6,
+        "step_bytes": step_bytes,
+        "per_shape": {f"{m}x{k}": {"us": per[(m, k)] * 1e3, "bytes": nbytes[(m, k)],
+                                   "gbs": nbytes[(m, k)] / per[(m, k)] / 1e6} for (m, k) in shapes},
+        "copies": R,
+    }
+
+
+def gemv_q8_leg(steps: int, warmup: int, dev) -> dict:
+    import numpy as np
+    import torch
+
+    from gemmagemini4hackathon2026_10_2425_amd import ops
+    from gemmagemini4hackathon2026_10_2425_amd.quant import quantize_q8b32
+
+    out = {}
+    for M, K in [(14336, 4096), (4096, 14336)]:
+        W = ops.fill_normal((M, K), torch.float16, 7, 300, 0.02, dev).cpu().numpy()
+        q, s = quantize_q8b32(W)
+        nb = M * K + M * (K // 32) * 2 + K * 2 + M * 4
+        R = _copies(nb)
+        qd = [torch.from_numpy(q).to(dev) for _ in range(R)]
+        sd = [torch.from_numpy(s).to(dev) for _ in range(R)]
+        x = ops.fill_normal((K,), torch.float16, 7, 91, 1.0, dev)
+        y = torch.empty(M, dtype=torch.float32, device=dev)
+        ms = _events_time(lambda i: ops.matvec_q8b32(qd[i % R], sd[i % R], x, y), steps, warmup)
+        out[f"{M}x{K}"] = {"us": ms * 1e3, "bytes": nb, "gbs": nb / ms / 1e6, "frac": nb / ms / 1e6 / PEAK_HBM_GBS}
+        del qd, sd, W, q, s
+        np.random.default_rng(0)
+    return out
+
+
+def attention_leg(steps: int, warmup: int, dev, L: int = 32768) -> dict:
+    import torch
+
+    from gemmagemini4hackathon2026_10_2425_amd import ops
+
+    nh, nkv, hd = 32, 8, 128
+    max_ctx = L
+    kv_bytes = 2 * nkv * max_ctx * hd * 2
+    R = _copies(kv_bytes)
+    ks = [ops.fill_normal((nkv, max_ctx, hd), torch.float16, 8, 10 + i, 1.0, dev) for i in range(R)]
+    vs = [ops.fill_normal((nkv, hd, max_ctx), torch.float16, 8, 50 + i, 1.0, dev) for i in range(R)]
+    q = ops.fill_normal((nh * hd,), torch.float32, 8, 1, 1.0, dev)
+    out = torch.empty(nh * hd, dtype=torch.float32, device=dev)
+    ws = ops.attention_workspace(nh, nkv, hd, max_ctx, dev)
+    ms = _events_time(lambda i: ops.attention(q, ks[i % R], vs[i % R], L, nh, out=out, workspace=ws), steps, warmup)
+    nb = 4096 * L + nh * hd * 4 * 2
+    return {"L": L, "us": ms * 1e3, "bytes": nb, "gbs": nb / ms / 1e6, "frac": nb / ms / 1e6 / PEAK_HBM_GBS}
+
+
+def cpu_baseline(seconds: float = 12.0) -> dict:
+    """The C oracle's fp16 GEMV (fp64 sums, OpenMP) on the 14336x4096 matrix."""
+    import numpy as np
+
+    from oracle import native
+
+    M, K = 14336, 4096
+    W = native.fill_normal((M, K), np.float16, 7, 100, 0.02)
+    x = native.fill_normal((K,), np.float16, 7, 90, 1.0).astype(np.float32)
+    native.matvec_f16(W, x)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        native.matvec_f16(W, x)
+        n += 1
+    dt = time.perf_counter() - t0
+    nb = M * K * 2 + K * 2 + M * 4
+    return {
+        "value": nb * n / dt / 1e9,
+        "unit": "GB/s",
+        "cores": native.num_threads(),
+        "kind": "port",
+        "sample": f"{n} calls of the 14336x4096 fp16 GEMV in {dt:.1f} s (C oracle, fp64 sums, "
+        f"{native.num_threads()} OpenMP threads; host has {os.cpu_count()} CPUs)",
+    }
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="gemv_f16", choices=["gemv_f16", "gemv_q8", "attention", "all"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-detail", action="store_true", help="skip the int8 / attention detail legs")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build has no multi-GPU path)",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    detail = {}
+    if args.workload in ("gemv_q8", "attention"):
+        leg = gemv_q8_leg(args.steps, args.warmup, dev) if args.workload == "gemv_q8" else \
+            attention_leg(args.steps, args.warmup, dev)
+        print(json.dumps({"workload": args.workload, **leg}))
+        return 0
+
+    log("fp16 GEMV leg")
+    g = gemv_f16_leg(args.steps, args.warmup, dev)
+    if not args.no_detail:
+        log("int8 GEMV leg")
+        detail["gemv_q8b32"] = gemv_q8_leg(args.steps, args.warmup, dev)
+        log("attention leg")
+        detail["attention_L32768"] = attention_leg(args.steps, args.warmup, dev)
+        torch.cuda.empty_cache()
+    detail["gemv_f16"] = g["per_shape"]
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline leg")
+        cpu = cpu_baseline()
+    line = {
+        "metric": "GEMV/attention HBM GB/s (% of peak); decode tok/s, Gemma-2B shape, 1 GPU",
+        "value": round(g["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (counter-based N(0, 0.02^2) weights, N(0, 1) activations)",
+        "config": {
+            "workload": "single-token fp16 GEMV, Llama-3-8B FFN shapes 14336x4096 + 4096x14336, fp32 accumulate",
+            "weights_rotated_copies": g["copies"],
+            "step_bytes": g["step_bytes"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_kernel<fp16 W, fp16 x> (both FFN shapes)",
+            "achieved": round(g["gbs"], 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(g["gbs"] / PEAK_HBM_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "detail": detail,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

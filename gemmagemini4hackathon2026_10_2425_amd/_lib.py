@@ -1,0 +1,124 @@
+"""ctypes binding of libmxdecode.so (the C ABI declared in include/mxdecode.h).
+
+The library is loaded from this package directory; nothing here falls back to
+another implementation: if the library is missing or fails to load, every
+call raises. Return codes map to exceptions:
+    MXD_ERR_INVALID_ARG, MXD_ERR_UNSUPPORTED, MXD_ERR_WORKSPACE -> MxdValueError
+    MXD_ERR_HIP, MXD_ERR_ALLOC                                  -> MxdRuntimeError
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_char_p, c_float, c_int, c_size_t, c_uint64, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libmxdecode.so"
+
+MXD_OK = 0
+MXD_ERR_INVALID_ARG = -1
+MXD_ERR_UNSUPPORTED = -2
+MXD_ERR_HIP = -3
+MXD_ERR_WORKSPACE = -4
+MXD_ERR_ALLOC = -5
+
+MXD_F32, MXD_F16 = 0, 1
+MXD_W_F16, MXD_W_Q8B32 = 0, 1
+MXD_EPI_STORE, MXD_EPI_ADD, MXD_EPI_GELU_MUL = 0, 1, 2
+MXD_ACT_GELU_TANH, MXD_ACT_SILU = 0, 1
+
+_ERR_NAMES = {
+    MXD_ERR_INVALID_ARG: "MXD_ERR_INVALID_ARG",
+    MXD_ERR_UNSUPPORTED: "MXD_ERR_UNSUPPORTED",
+    MXD_ERR_HIP: "MXD_ERR_HIP",
+    MXD_ERR_WORKSPACE: "MXD_ERR_WORKSPACE",
+    MXD_ERR_ALLOC: "MXD_ERR_ALLOC",
+}
+
+
+class MxdError(Exception):
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} -> {_ERR_NAMES.get(code, code)}: {msg}")
+        self.code = code
+
+
+class MxdValueError(MxdError, ValueError):
+    pass
+
+
+class MxdRuntimeError(MxdError, RuntimeError):
+    pass
+
+
+P = c_void_p
+# name -> (restype, argtypes); must match include/mxdecode.h one for one.
+SIGNATURES: dict[str, tuple] = {
+    "mxd_last_error": (c_char_p, []),
+    "mxd_abi_version": (c_int, []),
+    "mxd_set_tunable": (c_int, [c_char_p, c_int]),
+    "mxd_fill_normal": (c_int, [P, c_int, c_uint64, c_uint64, c_uint64, c_float, P]),
+    "mxd_gemv_f32": (c_int, [P, P, P, c_int, c_int, P]),
+    "mxd_matvec_f16": (c_int, [P, P, c_int, P, c_int, c_int, c_int, P, P]),
+    "mxd_matvec_q8b32": (c_int, [P, P, P, c_int, P, c_int, c_int, c_int, P, P]),
+    "mxd_matvec_gate_up": (c_int, [c_int, P, P, P, P, P, c_int, P, c_int, c_int, c_int, P]),
+    "mxd_rmsnorm": (c_int, [P, P, P, c_int, c_int, c_int, c_float, c_int, P]),
+    "mxd_embed": (c_int, [P, P, c_int, c_int, P, c_int, c_float, c_int, P]),
+    "mxd_f32_to_f16": (c_int, [P, P, c_size_t, P]),
+    "mxd_rope_kv": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),
+    "mxd_attention_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "mxd_attention": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, P, c_size_t, P]),
+    "mxd_argmax_workspace_size": (c_size_t, [c_int]),
+    "mxd_argmax": (c_int, [P, P, c_int, c_int, P, c_size_t, P]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libmxdecode.so once. torch is imported first when available so the
+    library binds to the HIP runtime torch already loaded (same soname)."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m gemmagemini4hackathon2026_10_2425_amd.build`"
+            )
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def last_error() -> str:
+    return (load().mxd_last_error() or b"").decode(errors="replace")
+
+
+def call(name: str, *args) -> int:
+    """Call an int-returning entry point; raise on a negative status."""
+    fn = getattr(load(), name)
+    rc = fn(*args)
+    if rc != MXD_OK:
+        msg = last_error()
+        cls = MxdRuntimeError if rc in (MXD_ERR_HIP, MXD_ERR_ALLOC) else MxdValueError
+        raise cls(name, rc, msg)
+    return rc
+
+
+def query(name: str, *args) -> int:
+    """Call a size-returning entry point (no status code)."""
+    return getattr(load(), name)(*args)
+
+
+def set_tunable(name: str, value: int) -> None:
+    call("mxd_set_tunable", name.encode(), int(value))

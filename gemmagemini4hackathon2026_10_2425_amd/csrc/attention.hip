@@ -1,0 +1,324 @@
+// Single-query (decode) attention over a contiguous fp16 KV cache, split over
+// the key axis (flash-decoding) and run on the matrix cores.
+//
+// Reference semantics (KL/kernels.metal:235-305): scores = scale * q . k_j in
+// fp32, max-subtracted softmax in fp32, out = sum_j p_j v_j / sum_j p_j, GQA
+// head mapping kvh = h / (n_heads / n_kv_heads). The reference keeps every
+// score in threadgroup memory (context capped at 4096) and re-reads K/V once
+// per query head; here:
+//
+//  * grid = (key splits, kv heads); a workgroup of 4 waves owns one kv head and
+//    one split; each wave walks 32-key blocks of the split with an online
+//    (running max / running sum) softmax in fp32.
+//  * the G = n_heads / n_kv_heads query heads of the group ride in the columns
+//    of one 16x16x32 fp16 MFMA, so each K and V element is loaded once for all
+//    of them: S^T[key][col] = K[key][:] . Q^T[:][col].
+//  * fp32 accuracy from fp16 matrix cores: q is split into hi = fp16(q) and
+//    lo = fp16(q - hi) in columns c and c + G (2G <= 16); the score of head c is
+//    the sum of the two columns (products of fp16 values are exact in fp32).
+//    P is split the same way for the P.V product, so out keeps ~22 bits.
+//  * the S^T accumulator layout (lane = column, 4 rows per lane group) is
+//    already the A-operand layout of the P.V MFMA once the key rows are
+//    permuted at load time, so P never leaves registers.
+//  * K loads are 16-byte rows of [kvh][ctx][hd]; V is cached transposed,
+//    [kvh][hd][ctx], so the P.V B operand (8 consecutive keys of one dim) is one
+//    16-byte load too.
+//  * splits write unnormalised (O, max, sum) partials, merged by a second
+//    kernel with the log-sum-exp rule; one split writes the output directly.
+#include "common.hpp"
+
+namespace {
+
+constexpr int ATT_WAVES = 4;
+constexpr int ATT_THREADS = ATT_WAVES * 64;
+constexpr int BLK = 32;  // keys per wave step
+constexpr float LOG2E = 1.4426950408889634f;
+
+struct AttnArgs {
+    const float* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    float* out;
+    float* ws_o;   // [n_splits][n_heads][HD]
+    float* ws_ml;  // [n_splits][n_heads][2]
+    const int32_t* pos_dev;
+    int n_heads, n_kv, G, max_ctx, n_keys, split;
+    float qscale;  // scale * log2(e): scores live in the log2 domain
+};
+
+// Keys visible to the query: n_keys, or *pos_dev + 1 read on the device (clamped
+// to the cache so a bad position can never address past it).
+__device__ __forceinline__ int n_keys_of(const AttnArgs& a) {
+    const int n = a.pos_dev ? a.pos_dev[0] + 1 : a.n_keys;
+    return max(0, min(n, a.max_ctx));
+}
+
+template <int HD>
+__global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
+    constexpr int NC = HD / 32;  // MFMA k-chunks over head_dim for Q.K
+    constexpr int ND = HD / 16;  // 16-wide dim tiles for P.V
+    __shared__ float sm_o[ATT_WAVES][8][HD];
+    __shared__ float sm_m[ATT_WAVES][8];
+    __shared__ float sm_l[ATT_WAVES][8];
+
+    const int n = n_keys_of(a);
+    const int split = blockIdx.x, kvh = blockIdx.y;
+    const int k_begin = split * a.split;
+    if (k_begin >= n) return;
+    const int k_end = min(k_begin + a.split, n);
+    const int nblk = (k_end - k_begin + BLK - 1) / BLK;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, g = lane >> 4;
+    const int G = a.G;
+
+    // Q^T operand: column col holds hi (col < G) or lo (G <= col < 2G) parts of
+    // head (kvh*G + col % G); k-slot (g, j) of chunk c is dim 32c + 8g + j.
+    h8_t qop[NC];
+    {
+        const bool live = col < 2 * G;
+        const int head = kvh * G + (live ? col % G : 0);
+        const float* qh = a.q + (size_t)head * HD;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const f4_t q0 = *reinterpret_cast<const f4_t*>(qh + 32 * c + 8 * g);
+            const f4_t q1 = *reinterpret_cast<const f4_t*>(qh + 32 * c + 8 * g + 4);
+            const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float v = qv[j] * a.qscale;
+                const _Float16 hi = (_Float16)v;
+                const _Float16 lo = (_Float16)(v - (float)hi);
+                qop[c][j] = !live ? (_Float16)0.0f : (col < G ? hi : lo);
+            }
+        }
+    }
+
+    const uint16_t* kbase = a.k + (size_t)kvh * a.max_ctx * HD;
+    const uint16_t* vbase = a.v + (size_t)kvh * HD * a.max_ctx;
+
+    float m_run = -INFINITY, l_run = 0.0f;
+    f4_t o[ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d) o[d] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int b = wave; b < nblk; b += ATT_WAVES) {
+        const int key0 = k_begin + b * BLK;
+        // ---- loads: K rows permuted so that S^T row 4g'+i of tile t is key
+        // key0 + 8g' + 4t + i; V^T rows give keys key0 + 8g .. +7 of one dim.
+        h8_t kop[2][NC];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int key = key0 + 8 * (col >> 2) + 4 * t + (col & 3);
+            const uint16_t* kr = kbase + (size_t)key * HD + 8 * g;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) kop[t][c] = *reinterpret_cast<const h8_t*>(kr + 32 * c);
+        }
+        h8_t vop[ND];
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+            vop[d] = *reinterpret_cast<const h8_t*>(vbase + (size_t)(16 * d + col) * a.max_ctx + key0 + 8 * g);
+
+        // ---- scores (log2 domain)
+        float s[8];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[t][c], qop[c], acc, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[4 * t + i] = acc[i];
+        }
+        const bool tail = key0 + BLK > n;
+        float mb = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            s[j] += __shfl_xor(s[j], G);  // hi + lo columns
+            if (tail && key0 + 8 * g + j >= n) s[j] = -INFINITY;
+            mb = fmaxf(mb, s[j]);
+        }
+        mb = fmaxf(mb, __shfl_xor(mb, 16));
+        mb = fmaxf(mb, __shfl_xor(mb, 32));
+        const float m_new = fmaxf(m_run, mb);
+        const float alpha = exp2f(m_run - m_new);
+        m_run = m_new;
+
+        h8_t pa;
+        float psum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float p = exp2f(s[j] - m_new);
+            psum += p;
+            const _Float16 hi = (_Float16)p;
+            const _Float16 lo = (_Float16)(p - (float)hi);
+            pa[j] = col < G ? hi : (col < 2 * G ? lo : (_Float16)0.0f);
+        }
+        l_run = l_run * alpha + psum;
+
+        // ---- rescale O rows (row 4g+i belongs to head slot 4g+i) and add P.V
+        float ar[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * g + i);
+        if (tail) {
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (key0 + 8 * g + j >= n) vop[d][j] = (_Float16)0.0f;
+        }
+#pragma unroll
+        for (int d = 0; d < ND; ++d) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[d][i] *= ar[i];
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vop[d], o[d], 0, 0, 0);
+        }
+    }
+
+    // ---- per-wave results: l summed over the 4 lane groups; O hi + lo rows.
+    l_run += __shfl_xor(l_run, 16);
+    l_run += __shfl_xor(l_run, 32);
+    if (lane < G) {
+        sm_m[wave][lane] = m_run;
+        sm_l[wave][lane] = l_run;
+    }
+    // Row h (hi) and row h + G (lo) of O -> head h.
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+        const int dim = 16 * d + col;
+        if (G >= 4) {
+            const int mask = G == 4 ? 16 : 32;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float other = __shfl_xor(o[d][i], mask);
+                const int h = 4 * g + i;
+                if (h < G) sm_o[wave][h][dim] = o[d][i] + other;
+            }
+        } else if (g == 0) {
+            if (G == 2) {
+                sm_o[wave][0][dim] = o[d][0] + o[d][2];
+                sm_o[wave][1][dim] = o[d][1] + o[d][3];
+            } else {
+                sm_o[wave][0][dim] = o[d][0] + o[d][1];
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- merge the 4 waves (and write the split's partial or the output)
+    const int n_active = (n + a.split - 1) / a.split;
+    for (int idx = threadIdx.x; idx < G * HD; idx += ATT_THREADS) {
+        const int h = idx / HD, dim = idx - h * HD;
+        float M = sm_m[0][h];
+#pragma unroll
+        for (int w = 1; w < ATT_WAVES; ++w) M = fmaxf(M, sm_m[w][h]);
+        float so = 0.0f, sl = 0.0f;
+#pragma unroll
+        for (int w = 0; w < ATT_WAVES; ++w) {
+            const float f = exp2f(sm_m[w][h] - M);
+            so += f * sm_o[w][h][dim];
+            sl += f * sm_l[w][h];
+        }
+        const int head = kvh * G + h;
+        if (n_active == 1) {
+            a.out[(size_t)head * HD + dim] = so / sl;
+        } else {
+            a.ws_o[((size_t)split * a.n_heads + head) * HD + dim] = so;
+            if (dim == 0) {
+                a.ws_ml[((size_t)split * a.n_heads + head) * 2 + 0] = M;
+                a.ws_ml[((size_t)split * a.n_heads + head) * 2 + 1] = sl;
+            }
+        }
+    }
+}
+
+// out[h] = sum_s 2^(M_s - M) O_s / sum_s 2^(M_s - M) L_s over the active splits.
+template <int HD>
+__global__ void __launch_bounds__(HD) attn_merge_kernel(AttnArgs a) {
+    const int n = n_keys_of(a);
+    const int n_active = (n + a.split - 1) / a.split;
+    if (n_active <= 1) return;
+    const int head = blockIdx.x, dim = threadIdx.x;
+    float M = -INFINITY;
+    for (int s = 0; s < n_active; ++s) M = fmaxf(M, a.ws_ml[((size_t)s * a.n_heads + head) * 2]);
+    float so = 0.0f, sl = 0.0f;
+    for (int s = 0; s < n_active; ++s) {
+        const size_t base = (size_t)s * a.n_heads + head;
+        const float f = exp2f(a.ws_ml[base * 2] - M);
+        so += f * a.ws_o[base * HD + dim];
+        sl += f * a.ws_ml[base * 2 + 1];
+    }
+    a.out[(size_t)head * HD + dim] = so / sl;
+}
+
+int target_splits(int n_kv) { return (2 * 256 + n_kv - 1) / n_kv; }
+
+int split_keys(int max_keys, int n_kv) {
+    const int t = target_splits(n_kv);
+    int split = (max_keys + t - 1) / t;
+    split = (split + 127) / 128 * 128;
+    return split < 128 ? 128 : split;
+}
+
+}  // namespace
+
+extern "C" size_t mxd_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim, int max_ctx) {
+    (void)max_ctx;
+    if (n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0) return 0;
+    const size_t splits = (size_t)target_splits(n_kv_heads);
+    return splits * n_heads * (head_dim + 2) * sizeof(float);
+}
+
+extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint16_t* vcache, float* out, int n_heads,
+                             int n_kv_heads, int head_dim, int max_ctx, int n_keys, const int32_t* pos_dev,
+                             float scale, void* workspace, size_t ws_bytes, mxd_stream_t stream) {
+    MXD_REQUIRE(q && kcache && vcache && out, MXD_ERR_INVALID_ARG, "mxd_attention: null pointer");
+    MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, MXD_ERR_INVALID_ARG,
+                "mxd_attention: n_heads=%d must be a positive multiple of n_kv_heads=%d", n_heads, n_kv_heads);
+    const int G = n_heads / n_kv_heads;
+    MXD_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, MXD_ERR_UNSUPPORTED,
+                "mxd_attention: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", G);
+    MXD_REQUIRE(head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED, "mxd_attention: head_dim %d (128 or 256)",
+                head_dim);
+    MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_attention: max_ctx=%d must be a positive multiple of 32", max_ctx);
+    MXD_REQUIRE(pos_dev || (n_keys >= 1 && n_keys <= max_ctx), MXD_ERR_INVALID_ARG,
+                "mxd_attention: n_keys=%d outside [1, max_ctx=%d]", n_keys, max_ctx);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kcache) |
+                         reinterpret_cast<uintptr_t>(vcache);
+    MXD_REQUIRE((al & 15) == 0, MXD_ERR_UNSUPPORTED, "mxd_attention: q, kcache, vcache must be 16-byte aligned");
+
+    const int split = split_keys(pos_dev ? max_ctx : n_keys, n_kv_heads);
+    const int n_splits = ((pos_dev ? max_ctx : n_keys) + split - 1) / split;
+    const size_t need = (size_t)n_splits * n_heads * (head_dim + 2) * sizeof(float);
+    MXD_REQUIRE(n_splits == 1 || (workspace && ws_bytes >= need), MXD_ERR_WORKSPACE,
+                "mxd_attention: workspace of %zu bytes needed (got %zu)", need, ws_bytes);
+    MXD_REQUIRE(!workspace || (reinterpret_cast<uintptr_t>(workspace) & 15) == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_attention: workspace must be 16-byte aligned");
+
+    AttnArgs a;
+    a.q = q;
+    a.k = kcache;
+    a.v = vcache;
+    a.out = out;
+    a.ws_o = static_cast<float*>(workspace);
+    a.ws_ml = workspace ? static_cast<float*>(workspace) + (size_t)n_splits * n_heads * head_dim : nullptr;
+    a.pos_dev = pos_dev;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv_heads;
+    a.G = G;
+    a.max_ctx = max_ctx;
+    a.n_keys = n_keys;
+    a.split = split;
+    a.qscale = scale * LOG2E;
+
+    hipStream_t s = mxd::as_stream(stream);
+    const dim3 grid(n_splits, n_kv_heads);
+    if (head_dim == 128) {
+        hipLaunchKernelGGL(attn_split_kernel<128>, grid, dim3(ATT_THREADS), 0, s, a);
+        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(n_heads), dim3(128), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(attn_split_kernel<256>, grid, dim3(ATT_THREADS), 0, s, a);
+        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(n_heads), dim3(256), 0, s, a);
+    }
+    return mxd::check_launch("mxd_attention");
+}

@@ -1,0 +1,113 @@
+// Shared device helpers and host-side error plumbing for libmxdecode.
+//
+// Everything here is written for gfx950 (CDNA4): 64-lane wavefronts, DPP row
+// operations for the first reduction steps, ds_bpermute for the cross-row ones.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/mxdecode.h"
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Host-side error state (thread-local), shared by every entry point.
+// ---------------------------------------------------------------------------
+namespace mxd {
+
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Maps the last launch status to an MXD code, recording the HIP message.
+int check_launch(const char* what);
+
+inline hipStream_t as_stream(mxd_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Tunables (mirrors the reference's `--define NAME=VALUE` kernel knobs).
+int tunable(const char* name, int fallback);
+
+}  // namespace mxd
+
+#define MXD_REQUIRE(cond, code, ...)                 \
+    do {                                             \
+        if (!(cond)) return mxd::fail((code), __VA_ARGS__); \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+namespace mxd {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wavefront; every lane receives the total.
+// Steps: swap pairs, swap pair-of-pairs (quad_perm), rotate 4 and 8 inside
+// each 16-lane row (DPP), then combine the four rows with bpermute.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f32<0x124>(v);  // row_ror:4
+    v += dpp_f32<0x128>(v);  // row_ror:8
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_f32<0xB1>(v));
+    v = fmaxf(v, dpp_f32<0x4E>(v));
+    v = fmaxf(v, dpp_f32<0x124>(v));
+    v = fmaxf(v, dpp_f32<0x128>(v));
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+
+__device__ __forceinline__ float h2f(uint16_t b) {
+    _Float16 h;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+
+__device__ __forceinline__ uint16_t f2h_bits(float f) {
+    _Float16 h = (_Float16)f;  // round to nearest even
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+__device__ __forceinline__ h2_t as_h2(uint32_t u) {
+    h2_t h;
+    __builtin_memcpy(&h, &u, 4);
+    return h;
+}
+
+// Four signed int8 values packed in a dword -> two half2 holding the exact
+// integers. q ^ 0x80 is the unsigned byte q + 128; 0x6400 | b is the fp16
+// value 1024 + b, so subtracting 1152 leaves q exactly.
+__device__ __forceinline__ void i8x4_to_h2x2(uint32_t w, h2_t& lo, h2_t& hi) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x07010700u);
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x07030702u);
+    const h2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    lo = as_h2(a) - bias;
+    hi = as_h2(b) - bias;
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+    // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), accurate tanh.
+    return 0.5f * x * (1.0f + tanhf(0.7978845608028654f * (x + 0.044715f * x * x * x)));
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+}  // namespace mxd

@@ -1,0 +1,353 @@
+// Matrix-vector products for single-token decode: fp32, fp16 and int8
+// block-32 weights, with store / residual-add / gelu*aux epilogues and the
+// fused gate-up (GLU) variant.
+//
+// Layout of the work (gfx950): a workgroup owns NR consecutive output rows and
+// NW wavefronts. The K axis is cut into chunks of 64 lanes x 16 bytes (one
+// coalesced 1 KiB wave load per row); wave w takes chunks w, w+NW, ... so the
+// NW waves of a workgroup stream adjacent KiBs of the same rows. Each wave keeps
+// U chunks x NR rows (x NMAT matrices) of loads in flight before doing any
+// math, reduces with DPP + bpermute, and the NW partial sums of a row are added
+// in a fixed order through LDS, so results are deterministic run to run.
+//
+// Reference semantics: matvec_f16 / matvec_gate_up_* (KG/kernels.metal:159-234,
+// KL/kernels.metal:106-173): fp32 accumulation of float(w) * x.
+#include "common.hpp"
+
+namespace {
+
+enum { WF_F32 = 2 };
+
+template <int WF> struct WT;
+template <> struct WT<MXD_W_F16> { static constexpr int EPL = 8; };    // 8 halfs in 16 B
+template <> struct WT<MXD_W_Q8B32> { static constexpr int EPL = 16; }; // 16 int8 in 16 B
+template <> struct WT<WF_F32> { static constexpr int EPL = 4; };       // 4 floats in 16 B
+
+struct GemvArgs {
+    const void* W[2];
+    const uint16_t* S[2];
+    const void* x;
+    float* y;
+    const float* aux;
+    int M, K;
+};
+
+// EPL activation values starting at column c.
+template <typename XT, int EPL> struct XFrag;
+
+template <int EPL> struct XFrag<float, EPL> {
+    float v[EPL];
+    __device__ __forceinline__ void load(const void* x, int c) {
+        const float* p = static_cast<const float*>(x) + c;
+#pragma unroll
+        for (int i = 0; i < EPL / 4; ++i) {
+            const f4_t t = *reinterpret_cast<const f4_t*>(p + 4 * i);
+            v[4 * i + 0] = t.x;
+            v[4 * i + 1] = t.y;
+            v[4 * i + 2] = t.z;
+            v[4 * i + 3] = t.w;
+        }
+    }
+};
+
+template <int EPL> struct XFrag<_Float16, EPL> {
+    h2_t v[EPL / 2];
+    __device__ __forceinline__ void load(const void* x, int c) {
+        const _Float16* p = static_cast<const _Float16*>(x) + c;
+#pragma unroll
+        for (int i = 0; i < EPL / 8; ++i) {
+            const u4_t t = *reinterpret_cast<const u4_t*>(p + 8 * i);
+            v[4 * i + 0] = mxd::as_h2(t.x);
+            v[4 * i + 1] = mxd::as_h2(t.y);
+            v[4 * i + 2] = mxd::as_h2(t.z);
+            v[4 * i + 3] = mxd::as_h2(t.w);
+        }
+    }
+};
+
+// ---- partial dot products: acc + w . x over one lane's 16 bytes -----------
+
+__device__ __forceinline__ float dot16(u4_t w, const XFrag<float, 8>& x, float acc) {  // fp16 W
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const h2_t h = mxd::as_h2(w[j]);
+        acc = fmaf((float)h.x, x.v[2 * j], acc);
+        acc = fmaf((float)h.y, x.v[2 * j + 1], acc);
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float dot16(u4_t w, const XFrag<_Float16, 8>& x, float acc) {  // fp16 W
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_fdot2(mxd::as_h2(w[j]), x.v[j], acc, false);
+    return acc;
+}
+
+__device__ __forceinline__ float dot16(u4_t w, const XFrag<float, 4>& x, float acc) {  // fp32 W
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = fmaf(__uint_as_float(w[j]), x.v[j], acc);
+    return acc;
+}
+
+// int8 weights: the sum over half a quantisation block (16 weights), unscaled.
+__device__ __forceinline__ float dot16q(u4_t w, const XFrag<_Float16, 16>& x) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        h2_t lo, hi;
+        mxd::i8x4_to_h2x2(w[j], lo, hi);
+        s = __builtin_amdgcn_fdot2(lo, x.v[2 * j], s, false);
+        s = __builtin_amdgcn_fdot2(hi, x.v[2 * j + 1], s, false);
+    }
+    return s;
+}
+
+__device__ __forceinline__ float dot16q(u4_t w, const XFrag<float, 16>& x) {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        h2_t lo, hi;
+        mxd::i8x4_to_h2x2(w[j], lo, hi);
+        s = fmaf((float)lo.x, x.v[4 * j + 0], s);
+        s = fmaf((float)lo.y, x.v[4 * j + 1], s);
+        s = fmaf((float)hi.x, x.v[4 * j + 2], s);
+        s = fmaf((float)hi.y, x.v[4 * j + 3], s);
+    }
+    return s;
+}
+
+template <int WF>
+__device__ __forceinline__ size_t welem_bytes() {
+    return WF == MXD_W_F16 ? 2 : WF == MXD_W_Q8B32 ? 1 : 4;
+}
+
+// NMAT == 1: OP is an MXD_EPI_*; NMAT == 2: OP is an MXD_ACT_* (gate, up).
+template <int WF, typename XT, int NMAT, int OP, int NR, int NW>
+__global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
+    constexpr int EPL = WT<WF>::EPL;
+    constexpr int CH = 64 * EPL;
+    constexpr int U = (8 / (NR * NMAT)) > 0 ? (8 / (NR * NMAT)) : 1;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * NR;
+    const int M = a.M, K = a.K;
+    const int nch = (K + CH - 1) / CH;
+
+    const unsigned char* wrow[NMAT][NR];
+    const uint16_t* srow[NMAT][NR];
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int row = min(r0 + r, M - 1);
+            wrow[m][r] = static_cast<const unsigned char*>(a.W[m]) + (size_t)row * K * welem_bytes<WF>();
+            srow[m][r] = WF == MXD_W_Q8B32 ? a.S[m] + (size_t)row * (K / 32) : nullptr;
+        }
+
+    float acc[NMAT][NR];
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) acc[m][r] = 0.0f;
+
+    for (int c0 = wave; c0 < nch; c0 += NW * U) {
+        u4_t wv[U][NMAT][NR];
+        uint16_t sv[U][NMAT][NR];
+        XFrag<XT, EPL> xf[U];
+        bool ok[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + u * NW;
+            const int col = c * CH + lane * EPL;
+            ok[u] = (c < nch) && (col < K);
+            if (ok[u]) {
+                xf[u].load(a.x, col);
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+                    for (int r = 0; r < NR; ++r) {
+                        wv[u][m][r] = *reinterpret_cast<const u4_t*>(wrow[m][r] + (size_t)col * welem_bytes<WF>());
+                        if (WF == MXD_W_Q8B32) sv[u][m][r] = srow[m][r][col / 32];
+                    }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (!ok[u]) continue;
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    if constexpr (WF == MXD_W_Q8B32)
+                        acc[m][r] = fmaf(dot16q(wv[u][m][r], xf[u]), mxd::h2f(sv[u][m][r]), acc[m][r]);
+                    else
+                        acc[m][r] = dot16(wv[u][m][r], xf[u], acc[m][r]);
+                }
+        }
+    }
+
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) acc[m][r] = mxd::wave_sum(acc[m][r]);
+
+    if constexpr (NW > 1) {
+        __shared__ float red[NW][NMAT][NR];
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+                for (int r = 0; r < NR; ++r) red[wave][m][r] = acc[m][r];
+        }
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                float s = red[0][m][r];
+#pragma unroll
+                for (int w = 1; w < NW; ++w) s += red[w][m][r];
+                acc[m][r] = s;
+            }
+    }
+
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int row = r0 + r;
+            if (row >= M) break;
+            if constexpr (NMAT == 2) {
+                const float g = acc[0][r], u = acc[1][r];
+                a.y[row] = (OP == MXD_ACT_SILU ? mxd::silu(g) : mxd::gelu_tanh(g)) * u;
+            } else if constexpr (OP == MXD_EPI_ADD) {
+                a.y[row] += acc[0][r];
+            } else if constexpr (OP == MXD_EPI_GELU_MUL) {
+                a.y[row] = mxd::gelu_tanh(acc[0][r]) * a.aux[row];
+            } else {
+                a.y[row] = acc[0][r];
+            }
+        }
+    }
+}
+
+// Rows per workgroup and waves per workgroup for a shape, overridable through
+// the MV_NR / MV_NW tunables.
+void pick_tiling(int M, int nch, int& nr, int& nw) {
+    nw = nch >= 16 ? 8 : nch >= 4 ? 4 : nch >= 2 ? 2 : 1;
+    nr = 8;
+    while (nr > 1 && (M + nr - 1) / nr < 2048) nr /= 2;
+    nr = mxd::tunable("MV_NR", nr);
+    nw = mxd::tunable("MV_NW", nw);
+}
+
+template <int WF, typename XT, int NMAT, int OP, int NR>
+int launch_nw(const GemvArgs& a, int nw, hipStream_t s) {
+    const dim3 grid((a.M + NR - 1) / NR);
+    switch (nw) {
+        case 1: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 1>), grid, dim3(64), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 2>), grid, dim3(128), 0, s, a); break;
+        case 4: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 4>), grid, dim3(256), 0, s, a); break;
+        case 8: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 8>), grid, dim3(512), 0, s, a); break;
+        default: return mxd::fail(MXD_ERR_INVALID_ARG, "matvec: MV_NW must be 1, 2, 4 or 8 (got %d)", nw);
+    }
+    return mxd::check_launch("matvec");
+}
+
+template <int WF, typename XT, int NMAT, int OP>
+int launch(const GemvArgs& a, hipStream_t s) {
+    constexpr int CH = 64 * WT<WF>::EPL;
+    int nr, nw;
+    pick_tiling(a.M, (a.K + CH - 1) / CH, nr, nw);
+    switch (nr) {
+        case 1: return launch_nw<WF, XT, NMAT, OP, 1>(a, nw, s);
+        case 2: return launch_nw<WF, XT, NMAT, OP, 2>(a, nw, s);
+        case 4: return launch_nw<WF, XT, NMAT, OP, 4>(a, nw, s);
+        case 8: return launch_nw<WF, XT, NMAT, OP, 8>(a, nw, s);
+        default: return mxd::fail(MXD_ERR_INVALID_ARG, "matvec: MV_NR must be 1, 2, 4 or 8 (got %d)", nr);
+    }
+}
+
+template <int WF, typename XT>
+int launch_epi(const GemvArgs& a, int epi, hipStream_t s) {
+    switch (epi) {
+        case MXD_EPI_STORE: return launch<WF, XT, 1, MXD_EPI_STORE>(a, s);
+        case MXD_EPI_ADD: return launch<WF, XT, 1, MXD_EPI_ADD>(a, s);
+        case MXD_EPI_GELU_MUL: return launch<WF, XT, 1, MXD_EPI_GELU_MUL>(a, s);
+        default: return mxd::fail(MXD_ERR_INVALID_ARG, "matvec: unknown epilogue %d", epi);
+    }
+}
+
+template <int WF, typename XT>
+int launch_act(const GemvArgs& a, int act, hipStream_t s) {
+    switch (act) {
+        case MXD_ACT_GELU_TANH: return launch<WF, XT, 2, MXD_ACT_GELU_TANH>(a, s);
+        case MXD_ACT_SILU: return launch<WF, XT, 2, MXD_ACT_SILU>(a, s);
+        default: return mxd::fail(MXD_ERR_INVALID_ARG, "matvec_gate_up: unknown activation %d", act);
+    }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int check_common(const char* fn, const void* W, const void* x, const float* y, int M, int K) {
+    MXD_REQUIRE(W && x && y, MXD_ERR_INVALID_ARG, "%s: null pointer", fn);
+    MXD_REQUIRE(M > 0 && K > 0, MXD_ERR_INVALID_ARG, "%s: M=%d K=%d must be positive", fn, M, K);
+    MXD_REQUIRE(aligned16(W) && aligned16(x), MXD_ERR_UNSUPPORTED, "%s: W and x must be 16-byte aligned", fn);
+    return MXD_OK;
+}
+
+}  // namespace
+
+extern "C" int mxd_gemv_f32(const float* W, const float* x, float* y, int M, int K, mxd_stream_t stream) {
+    if (int rc = check_common("mxd_gemv_f32", W, x, y, M, K)) return rc;
+    MXD_REQUIRE(K % 4 == 0, MXD_ERR_UNSUPPORTED, "mxd_gemv_f32: K=%d must be a multiple of 4", K);
+    GemvArgs a{{W, nullptr}, {nullptr, nullptr}, x, y, nullptr, M, K};
+    return launch<WF_F32, float, 1, MXD_EPI_STORE>(a, mxd::as_stream(stream));
+}
+
+extern "C" int mxd_matvec_f16(const uint16_t* W, const void* x, int x_dtype, float* y, int M, int K, int epilogue,
+                              const float* aux, mxd_stream_t stream) {
+    if (int rc = check_common("mxd_matvec_f16", W, x, y, M, K)) return rc;
+    MXD_REQUIRE(K % 8 == 0, MXD_ERR_UNSUPPORTED, "mxd_matvec_f16: K=%d must be a multiple of 8", K);
+    MXD_REQUIRE(epilogue != MXD_EPI_GELU_MUL || aux, MXD_ERR_INVALID_ARG, "mxd_matvec_f16: GELU_MUL needs aux");
+    GemvArgs a{{W, nullptr}, {nullptr, nullptr}, x, y, aux, M, K};
+    hipStream_t s = mxd::as_stream(stream);
+    if (x_dtype == MXD_F32) return launch_epi<MXD_W_F16, float>(a, epilogue, s);
+    if (x_dtype == MXD_F16) return launch_epi<MXD_W_F16, _Float16>(a, epilogue, s);
+    return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_matvec_f16: x_dtype %d", x_dtype);
+}
+
+extern "C" int mxd_matvec_q8b32(const int8_t* Wq, const uint16_t* scales, const void* x, int x_dtype, float* y, int M,
+                                int K, int epilogue, const float* aux, mxd_stream_t stream) {
+    if (int rc = check_common("mxd_matvec_q8b32", Wq, x, y, M, K)) return rc;
+    MXD_REQUIRE(scales, MXD_ERR_INVALID_ARG, "mxd_matvec_q8b32: null scales");
+    MXD_REQUIRE(K % 32 == 0, MXD_ERR_UNSUPPORTED, "mxd_matvec_q8b32: K=%d must be a multiple of 32", K);
+    MXD_REQUIRE(epilogue != MXD_EPI_GELU_MUL || aux, MXD_ERR_INVALID_ARG, "mxd_matvec_q8b32: GELU_MUL needs aux");
+    GemvArgs a{{Wq, nullptr}, {scales, nullptr}, x, y, aux, M, K};
+    hipStream_t s = mxd::as_stream(stream);
+    if (x_dtype == MXD_F32) return launch_epi<MXD_W_Q8B32, float>(a, epilogue, s);
+    if (x_dtype == MXD_F16) return launch_epi<MXD_W_Q8B32, _Float16>(a, epilogue, s);
+    return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_matvec_q8b32: x_dtype %d", x_dtype);
+}
+
+extern "C" int mxd_matvec_gate_up(int w_format, const void* Wg, const uint16_t* sg, const void* Wu,
+                                  const uint16_t* su, const void* x, int x_dtype, float* h, int F, int K, int act,
+                                  mxd_stream_t stream) {
+    if (int rc = check_common("mxd_matvec_gate_up", Wg, x, h, F, K)) return rc;
+    MXD_REQUIRE(Wu && aligned16(Wu), MXD_ERR_INVALID_ARG, "mxd_matvec_gate_up: Wu null or not 16-byte aligned");
+    GemvArgs a{{Wg, Wu}, {sg, su}, x, h, nullptr, F, K};
+    hipStream_t s = mxd::as_stream(stream);
+    if (w_format == MXD_W_F16) {
+        MXD_REQUIRE(K % 8 == 0, MXD_ERR_UNSUPPORTED, "mxd_matvec_gate_up: K=%d must be a multiple of 8", K);
+        if (x_dtype == MXD_F32) return launch_act<MXD_W_F16, float>(a, act, s);
+        if (x_dtype == MXD_F16) return launch_act<MXD_W_F16, _Float16>(a, act, s);
+    } else if (w_format == MXD_W_Q8B32) {
+        MXD_REQUIRE(sg && su, MXD_ERR_INVALID_ARG, "mxd_matvec_gate_up: int8 weights need scales");
+        MXD_REQUIRE(K % 32 == 0, MXD_ERR_UNSUPPORTED, "mxd_matvec_gate_up: K=%d must be a multiple of 32", K);
+        if (x_dtype == MXD_F32) return launch_act<MXD_W_Q8B32, float>(a, act, s);
+        if (x_dtype == MXD_F16) return launch_act<MXD_W_Q8B32, _Float16>(a, act, s);
+    } else {
+        return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_matvec_gate_up: weight format %d", w_format);
+    }
+    return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_matvec_gate_up: x_dtype %d", x_dtype);
+}

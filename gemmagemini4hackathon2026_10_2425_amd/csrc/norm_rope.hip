@@ -1,0 +1,150 @@
+// RMSNorm, embedding lookup, fp32->fp16 cast, and RoPE with KV-cache append.
+// These move kilobytes per decode step; they are latency-bound, so each is a
+// single small launch with no host synchronisation.
+#include "common.hpp"
+
+namespace {
+
+constexpr int NORM_THREADS = 256;
+
+// Sum over a 256-thread workgroup; every thread receives the total.
+__device__ __forceinline__ float block_sum(float v, float* scratch) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = mxd::wave_sum(v);
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float t = scratch[0];
+#pragma unroll
+    for (int w = 1; w < NORM_THREADS / 64; ++w) t += scratch[w];
+    __syncthreads();
+    return t;
+}
+
+// y = x * rsqrt(mean(x^2) + eps) * (1 + w | w), one workgroup per row
+// (KL/kernels.metal:71-96).
+template <typename YT, bool PLUS_ONE>
+__global__ void __launch_bounds__(NORM_THREADS)
+rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w, YT* __restrict__ y, int D, float eps) {
+    __shared__ float scratch[NORM_THREADS / 64];
+    const float* xr = x + (size_t)blockIdx.x * D;
+    YT* yr = y + (size_t)blockIdx.x * D;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < D; i += NORM_THREADS) ss = fmaf(xr[i], xr[i], ss);
+    ss = block_sum(ss, scratch);
+    const float scale = rsqrtf(ss / (float)D + eps);
+    for (int i = threadIdx.x; i < D; i += NORM_THREADS) {
+        const float wi = PLUS_ONE ? 1.0f + w[i] : w[i];
+        yr[i] = (YT)(xr[i] * scale * wi);
+    }
+}
+
+// x[r][i] = float(E[tokens[pos + r]][i]) * scale; ids outside [0, vocab) give
+// a zero row instead of an out-of-bounds read.
+__global__ void __launch_bounds__(256) embed_kernel(const uint16_t* __restrict__ E, const int32_t* __restrict__ tokens,
+                                                    int pos, float* __restrict__ x, int D, float scale, int vocab) {
+    const int r = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= D) return;
+    const int tok = tokens[pos + r];
+    x[(size_t)r * D + i] = (tok >= 0 && tok < vocab) ? mxd::h2f(E[(size_t)tok * D + i]) * scale : 0.0f;
+}
+
+__global__ void __launch_bounds__(256) f32_to_f16_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst,
+                                                         size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = mxd::f2h_bits(src[i]);
+}
+
+// One thread per rotation pair (i, i + hd/2) per head per row; heads run over
+// the q heads, then the kv heads (KL/kernels.metal:182-224). V goes to the
+// transposed cache [kvh][hd][max_ctx].
+__global__ void __launch_bounds__(256)
+rope_kv_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kcache, uint16_t* __restrict__ vcache,
+               const float* __restrict__ inv_freq, int n_heads, int n_kv, int hd, int max_ctx, int pos0) {
+    const int half_d = hd >> 1;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;  // pair index over heads
+    const int t = blockIdx.y;                              // row
+    const int h = i / half_d, p = i - h * half_d;
+    if (h >= n_heads + n_kv) return;
+    const int row_len = (n_heads + 2 * n_kv) * hd;
+    const int pos = pos0 + t;
+    float* row = qkv + (size_t)t * row_len;
+    float* v = row + h * hd;
+    const float ang = (float)pos * inv_freq[p];
+    float s, c;
+    sincosf(ang, &s, &c);
+    const float a = v[p], b = v[p + half_d];
+    const float ra = a * c - b * s;
+    const float rb = b * c + a * s;
+    if (h < n_heads) {
+        v[p] = ra;
+        v[p + half_d] = rb;
+    } else {
+        const int kvh = h - n_heads;
+        const size_t kbase = ((size_t)kvh * max_ctx + pos) * hd;
+        kcache[kbase + p] = mxd::f2h_bits(ra);
+        kcache[kbase + p + half_d] = mxd::f2h_bits(rb);
+        const float* vv = row + (n_heads + n_kv + kvh) * hd;
+        const size_t vbase = (size_t)kvh * hd * max_ctx + pos;
+        vcache[vbase + (size_t)p * max_ctx] = mxd::f2h_bits(vv[p]);
+        vcache[vbase + (size_t)(p + half_d) * max_ctx] = mxd::f2h_bits(vv[p + half_d]);
+    }
+}
+
+}  // namespace
+
+extern "C" int mxd_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int rows, int D, float eps,
+                           int plus_one, mxd_stream_t stream) {
+    MXD_REQUIRE(x && w && y, MXD_ERR_INVALID_ARG, "mxd_rmsnorm: null pointer");
+    MXD_REQUIRE(rows > 0 && D > 0, MXD_ERR_INVALID_ARG, "mxd_rmsnorm: rows=%d D=%d must be positive", rows, D);
+    hipStream_t s = mxd::as_stream(stream);
+    const dim3 grid(rows), block(NORM_THREADS);
+    if (y_dtype == MXD_F32) {
+        if (plus_one)
+            hipLaunchKernelGGL((rmsnorm_kernel<float, true>), grid, block, 0, s, x, w, (float*)y, D, eps);
+        else
+            hipLaunchKernelGGL((rmsnorm_kernel<float, false>), grid, block, 0, s, x, w, (float*)y, D, eps);
+    } else if (y_dtype == MXD_F16) {
+        if (plus_one)
+            hipLaunchKernelGGL((rmsnorm_kernel<_Float16, true>), grid, block, 0, s, x, w, (_Float16*)y, D, eps);
+        else
+            hipLaunchKernelGGL((rmsnorm_kernel<_Float16, false>), grid, block, 0, s, x, w, (_Float16*)y, D, eps);
+    } else {
+        return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_rmsnorm: y_dtype %d", y_dtype);
+    }
+    return mxd::check_launch("mxd_rmsnorm");
+}
+
+extern "C" int mxd_embed(const uint16_t* E, const int32_t* tokens, int pos, int rows, float* x, int D, float scale,
+                         int vocab, mxd_stream_t stream) {
+    MXD_REQUIRE(E && tokens && x, MXD_ERR_INVALID_ARG, "mxd_embed: null pointer");
+    MXD_REQUIRE(pos >= 0 && rows > 0 && D > 0 && vocab > 0, MXD_ERR_INVALID_ARG,
+                "mxd_embed: pos=%d rows=%d D=%d vocab=%d", pos, rows, D, vocab);
+    hipLaunchKernelGGL(embed_kernel, dim3((D + 255) / 256, rows), dim3(256), 0, mxd::as_stream(stream), E, tokens, pos,
+                       x, D, scale, vocab);
+    return mxd::check_launch("mxd_embed");
+}
+
+extern "C" int mxd_f32_to_f16(const float* src, uint16_t* dst, size_t n, mxd_stream_t stream) {
+    if (n == 0) return MXD_OK;
+    MXD_REQUIRE(src && dst, MXD_ERR_INVALID_ARG, "mxd_f32_to_f16: null pointer");
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)blocks), dim3(256), 0, mxd::as_stream(stream), src, dst, n);
+    return mxd::check_launch("mxd_f32_to_f16");
+}
+
+extern "C" int mxd_rope_kv(float* qkv, uint16_t* kcache, uint16_t* vcache, const float* inv_freq, int n_heads,
+                           int n_kv_heads, int head_dim, int max_ctx, int pos0, int rows, mxd_stream_t stream) {
+    MXD_REQUIRE(qkv && kcache && vcache && inv_freq, MXD_ERR_INVALID_ARG, "mxd_rope_kv: null pointer");
+    MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && rows > 0 && pos0 >= 0, MXD_ERR_INVALID_ARG,
+                "mxd_rope_kv: n_heads=%d n_kv_heads=%d rows=%d pos0=%d", n_heads, n_kv_heads, rows, pos0);
+    MXD_REQUIRE(head_dim > 0 && head_dim % 2 == 0, MXD_ERR_UNSUPPORTED, "mxd_rope_kv: head_dim=%d must be even",
+                head_dim);
+    MXD_REQUIRE(pos0 + rows <= max_ctx, MXD_ERR_INVALID_ARG, "mxd_rope_kv: positions %d..%d exceed max_ctx %d", pos0,
+                pos0 + rows - 1, max_ctx);
+    const int pairs = (n_heads + n_kv_heads) * (head_dim / 2);
+    hipLaunchKernelGGL(rope_kv_kernel, dim3((pairs + 255) / 256, rows), dim3(256), 0, mxd::as_stream(stream), qkv,
+                       kcache, vcache, inv_freq, n_heads, n_kv_heads, head_dim, max_ctx, pos0);
+    return mxd::check_launch("mxd_rope_kv");
+}

@@ -1,0 +1,257 @@
+"""Operator surface of the decode hot path on torch device tensors.
+
+Names and argument meaning follow the reference's Metal operators (paths
+relative to ios_kernels/kernels/, KL = the Llama-3.2-1B kernel folder,
+KG = the Gemma-4-E2B kernel folder):
+
+    matvec_f16 / matvec_f16_add / matvec_f16_gelu_mul   KG/kernels.metal:159-198
+    matvec_q8b32                                        (new: int8 block-32)
+    matvec_gate_up_gelu / matvec_gate_up_silu           KG/kernels.metal:205-234, KL/kernels.metal:144-173
+    rmsnorm (rmsnorm_f32 / rmsnorm_f16)                 KL/kernels.metal:71-96
+    embed / embed_rows                                  KL/kernels.metal:31-39, KG/kernels.metal:34-42
+    rope_kv                                             KL/kernels.metal:182-224
+    attention                                           KL/kernels.metal:235-305
+    argmax                                              KL/kernels.metal:310-345
+    f32_to_f16                                          KL/kernels.metal:361-365
+
+Every function checks shapes on the host and raises ValueError before any
+launch (the reference's host preconditions, KG/main.swift:306, crash instead).
+All work is enqueued on torch's current stream; tensors must live on the GPU.
+torch is only the allocator/stream plumbing here: the arithmetic is in
+libmxdecode.so.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from ._lib import call, query
+
+_EPI = {"store": _lib.MXD_EPI_STORE, "add": _lib.MXD_EPI_ADD, "gelu_mul": _lib.MXD_EPI_GELU_MUL}
+_ACT = {"gelu_tanh": _lib.MXD_ACT_GELU_TANH, "silu": _lib.MXD_ACT_SILU}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _on_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        _need(t.is_cuda, "tensor must be on the GPU")
+        _need(t.is_contiguous(), "tensor must be contiguous")
+
+
+def _xdtype(x: torch.Tensor) -> int:
+    if x.dtype == torch.float32:
+        return _lib.MXD_F32
+    if x.dtype == torch.float16:
+        return _lib.MXD_F16
+    raise ValueError(f"activation dtype {x.dtype} (float32 or float16)")
+
+
+# ---------------------------------------------------------------- weights
+
+
+def fill_normal(shape, dtype: torch.dtype, seed: int, tensor_id: int, std: float, device="cuda") -> torch.Tensor:
+    """Synthetic N(0, std^2) tensor from the counter-based generator (bit-exact
+    with the oracle's restatement)."""
+    _need(dtype in (torch.float32, torch.float16), "fill_normal: float32 or float16")
+    t = torch.empty(shape, dtype=dtype, device=device)
+    code = _lib.MXD_F32 if dtype == torch.float32 else _lib.MXD_F16
+    call("mxd_fill_normal", _ptr(t), code, t.numel(), seed, tensor_id, float(std), _stream())
+    return t
+
+
+# ---------------------------------------------------------------- matvec
+
+
+def gemv_f32(W: torch.Tensor, x: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
+    _on_gpu(W, x)
+    _need(W.dtype == torch.float32 and x.dtype == torch.float32, "gemv_f32: float32 W and x")
+    M, K = W.shape
+    _need(x.numel() == K, f"gemv_f32: x has {x.numel()} elements, W is {M}x{K}")
+    y = torch.empty(M, dtype=torch.float32, device=W.device) if y is None else y
+    call("mxd_gemv_f32", _ptr(W), _ptr(x), _ptr(y), M, K, _stream())
+    return y
+
+
+def matvec_f16(W, x, y=None, epilogue: str = "store", aux=None) -> torch.Tensor:
+    """y (op)= W.x; W fp16 [M, K], x fp32/fp16 [K], y fp32 [M]."""
+    _on_gpu(W, x)
+    _need(W.dtype == torch.float16 and W.dim() == 2, "matvec_f16: W must be a 2-D float16 tensor")
+    M, K = W.shape
+    _need(x.numel() == K, f"matvec_f16: x has {x.numel()} elements, W is {M}x{K}")
+    _need(epilogue in _EPI, f"matvec_f16: epilogue {epilogue!r}")
+    if y is None:
+        _need(epilogue != "add", "matvec_f16: epilogue 'add' needs y")
+        y = torch.empty(M, dtype=torch.float32, device=W.device)
+    _need(y.dtype == torch.float32 and y.numel() == M, "matvec_f16: y must be float32 [M]")
+    if epilogue == "gelu_mul":
+        _need(aux is not None and aux.numel() == M and aux.dtype == torch.float32, "matvec_f16: aux float32 [M]")
+    call("mxd_matvec_f16", _ptr(W), _ptr(x), _xdtype(x), _ptr(y), M, K, _EPI[epilogue], _ptr(aux), _stream())
+    return y
+
+
+def matvec_f16_add(W, x, y) -> torch.Tensor:
+    return matvec_f16(W, x, y, "add")
+
+
+def matvec_f16_gelu_mul(W, x, aux, y=None) -> torch.Tensor:
+    return matvec_f16(W, x, y, "gelu_mul", aux)
+
+
+def matvec_q8b32(Wq, scales, x, y=None, epilogue: str = "store", aux=None) -> torch.Tensor:
+    """y (op)= dequant(Wq, scales).x; Wq int8 [M, K], scales fp16 [M, K/32]."""
+    _on_gpu(Wq, scales, x)
+    _need(Wq.dtype == torch.int8 and Wq.dim() == 2, "matvec_q8b32: Wq must be a 2-D int8 tensor")
+    M, K = Wq.shape
+    _need(K % 32 == 0, f"matvec_q8b32: K={K} must be a multiple of 32")
+    _need(scales.dtype == torch.float16 and tuple(scales.shape) == (M, K // 32), "matvec_q8b32: scales fp16 [M, K/32]")
+    _need(x.numel() == K, f"matvec_q8b32: x has {x.numel()} elements, W is {M}x{K}")
+    _need(epilogue in _EPI, f"matvec_q8b32: epilogue {epilogue!r}")
+    if y is None:
+        _need(epilogue != "add", "matvec_q8b32: epilogue 'add' needs y")
+        y = torch.empty(M, dtype=torch.float32, device=Wq.device)
+    if epilogue == "gelu_mul":
+        _need(aux is not None and aux.numel() == M, "matvec_q8b32: aux float32 [M]")
+    call(
+        "mxd_matvec_q8b32", _ptr(Wq), _ptr(scales), _ptr(x), _xdtype(x), _ptr(y), M, K, _EPI[epilogue], _ptr(aux),
+        _stream(),
+    )
+    return y
+
+
+def matvec_gate_up(Wg, Wu, x, act: str = "gelu_tanh", h=None, sg=None, su=None) -> torch.Tensor:
+    """h = act(Wg.x) * (Wu.x); fp16 weights, or int8 block-32 with scales sg/su."""
+    _on_gpu(Wg, Wu, x)
+    _need(Wg.shape == Wu.shape and Wg.dim() == 2 and Wg.dtype == Wu.dtype, "matvec_gate_up: Wg/Wu mismatch")
+    F, K = Wg.shape
+    _need(x.numel() == K, f"matvec_gate_up: x has {x.numel()} elements, W is {F}x{K}")
+    _need(act in _ACT, f"matvec_gate_up: act {act!r}")
+    if Wg.dtype == torch.float16:
+        fmt = _lib.MXD_W_F16
+    elif Wg.dtype == torch.int8:
+        fmt = _lib.MXD_W_Q8B32
+        _need(sg is not None and su is not None, "matvec_gate_up: int8 weights need sg and su")
+        _need(tuple(sg.shape) == (F, K // 32) and tuple(su.shape) == (F, K // 32), "matvec_gate_up: scales shape")
+    else:
+        raise ValueError(f"matvec_gate_up: weight dtype {Wg.dtype}")
+    h = torch.empty(F, dtype=torch.float32, device=Wg.device) if h is None else h
+    call(
+        "mxd_matvec_gate_up", fmt, _ptr(Wg), _ptr(sg), _ptr(Wu), _ptr(su), _ptr(x), _xdtype(x), _ptr(h), F, K,
+        _ACT[act], _stream(),
+    )
+    return h
+
+
+def matvec_gate_up_gelu(Wg, Wu, x, h=None) -> torch.Tensor:
+    return matvec_gate_up(Wg, Wu, x, "gelu_tanh", h)
+
+
+def matvec_gate_up_silu(Wg, Wu, x, h=None) -> torch.Tensor:
+    return matvec_gate_up(Wg, Wu, x, "silu", h)
+
+
+# ---------------------------------------------------------------- norms etc.
+
+
+def rmsnorm(x, w, eps: float, plus_one: bool = False, y=None, out_dtype=torch.float32) -> torch.Tensor:
+    """Row-wise RMSNorm of x [rows, D] (or [D])."""
+    _on_gpu(x, w)
+    _need(x.dtype == torch.float32 and w.dtype == torch.float32, "rmsnorm: float32 x and w")
+    D = x.shape[-1]
+    rows = x.numel() // D
+    _need(w.numel() == D, f"rmsnorm: w has {w.numel()} elements, D={D}")
+    y = torch.empty(x.shape, dtype=out_dtype, device=x.device) if y is None else y
+    call("mxd_rmsnorm", _ptr(x), _ptr(w), _ptr(y), _xdtype(y), rows, D, float(eps), int(plus_one), _stream())
+    return y
+
+
+def embed(E, tokens, pos: int, scale: float = 1.0, rows: int = 1, x=None) -> torch.Tensor:
+    """x[r] = float(E[tokens[pos + r]]) * scale (token ids read on the device)."""
+    _on_gpu(E, tokens)
+    _need(E.dtype == torch.float16 and E.dim() == 2, "embed: E must be a 2-D float16 tensor")
+    _need(tokens.dtype == torch.int32, "embed: tokens must be int32")
+    _need(0 <= pos and pos + rows <= tokens.numel(), "embed: pos out of range")
+    V, D = E.shape
+    x = torch.empty((rows, D), dtype=torch.float32, device=E.device) if x is None else x
+    call("mxd_embed", _ptr(E), _ptr(tokens), pos, rows, _ptr(x), D, float(scale), V, _stream())
+    return x
+
+
+def f32_to_f16(src, dst=None) -> torch.Tensor:
+    _on_gpu(src)
+    dst = torch.empty(src.shape, dtype=torch.float16, device=src.device) if dst is None else dst
+    call("mxd_f32_to_f16", _ptr(src), _ptr(dst), src.numel(), _stream())
+    return dst
+
+
+def inv_freq(head_dim: int, theta: float) -> list[float]:
+    """RoPE inverse frequencies in double, stored as float (KL/main.swift:92-94)."""
+    return [1.0 / theta ** (2 * i / head_dim) for i in range(head_dim // 2)]
+
+
+def rope_kv(qkv, kcache, vcache, inv_freq_t, n_heads: int, n_kv_heads: int, pos0: int) -> None:
+    """Rotate q in place and k, append k and v (fp16) to the caches at pos0 + row.
+    kcache [n_kv, max_ctx, hd]; vcache [n_kv, hd, max_ctx] (transposed)."""
+    _on_gpu(qkv, kcache, vcache, inv_freq_t)
+    n_kv, max_ctx, hd = kcache.shape
+    _need(n_kv == n_kv_heads and tuple(vcache.shape) == (n_kv, hd, max_ctx), "rope_kv: cache shapes")
+    _need(kcache.dtype == torch.float16 and vcache.dtype == torch.float16, "rope_kv: fp16 caches")
+    row_len = (n_heads + 2 * n_kv_heads) * hd
+    _need(qkv.dtype == torch.float32 and qkv.numel() % row_len == 0, f"rope_kv: qkv rows of {row_len} floats")
+    rows = qkv.numel() // row_len
+    _need(inv_freq_t.numel() == hd // 2, "rope_kv: inv_freq has head_dim/2 entries")
+    call(
+        "mxd_rope_kv", _ptr(qkv), _ptr(kcache), _ptr(vcache), _ptr(inv_freq_t), n_heads, n_kv_heads, hd, max_ctx,
+        pos0, rows, _stream(),
+    )
+
+
+def attention_workspace(n_heads: int, n_kv_heads: int, head_dim: int, max_ctx: int, device="cuda") -> torch.Tensor:
+    nbytes = query("mxd_attention_workspace_size", n_heads, n_kv_heads, head_dim, max_ctx)
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+def attention(q, kcache, vcache, n_keys: int, n_heads: int, scale: float | None = None, out=None, workspace=None,
+              pos_dev=None) -> torch.Tensor:
+    """Single-query attention of q [n_heads*hd] over keys [0, n_keys) of the
+    caches (kcache [n_kv, max_ctx, hd], vcache [n_kv, hd, max_ctx])."""
+    _on_gpu(q, kcache, vcache)
+    n_kv, max_ctx, hd = kcache.shape
+    _need(tuple(vcache.shape) == (n_kv, hd, max_ctx), "attention: vcache must be [n_kv, hd, max_ctx]")
+    _need(q.numel() == n_heads * hd and q.dtype == torch.float32, "attention: q float32 [n_heads*hd]")
+    scale = 1.0 / math.sqrt(hd) if scale is None else scale
+    out = torch.empty(n_heads * hd, dtype=torch.float32, device=q.device) if out is None else out
+    if workspace is None:
+        workspace = attention_workspace(n_heads, n_kv, hd, max_ctx, q.device)
+    call(
+        "mxd_attention", _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(out), n_heads, n_kv, hd, max_ctx, int(n_keys),
+        _ptr(pos_dev), float(scale), _ptr(workspace), workspace.numel(), _stream(),
+    )
+    return out
+
+
+def argmax_workspace(device="cuda") -> torch.Tensor:
+    """Zeroed once here; the kernel leaves it zeroed after every call."""
+    return torch.zeros(max(query("mxd_argmax_workspace_size", 0), 16), dtype=torch.uint8, device=device)
+
+
+def argmax(logits, tokens, out_idx: int, workspace) -> None:
+    """tokens[out_idx] = argmax(logits), ties to the lowest index."""
+    _on_gpu(logits, tokens)
+    _need(logits.dtype == torch.float32 and tokens.dtype == torch.int32, "argmax: float32 logits, int32 tokens")
+    _need(0 <= out_idx < tokens.numel(), "argmax: out_idx out of range")
+    call("mxd_argmax", _ptr(logits), _ptr(tokens), logits.numel(), out_idx, _ptr(workspace), workspace.numel(), _stream())

@@ -1,0 +1,168 @@
+/*
+ * mxdecode.h — C ABI of libmxdecode, the MI355X (gfx950) LLM decode hot path.
+ *
+ * Every entry point:
+ *   - takes caller-owned DEVICE pointers and plain sizes (no framework types),
+ *   - enqueues work on `stream` (a hipStream_t passed as void*; NULL = the null
+ *     stream) and returns without synchronising,
+ *   - returns MXD_OK (0) or a negative MXD_ERR_* code and never aborts; the text
+ *     of the last failure on the calling thread is mxd_last_error().
+ * Argument checks happen on the host before anything is launched, so a bad
+ * shape never reaches the GPU.
+ *
+ * Each declaration names the reference interface it replaces. The reference is
+ * a Metal/Swift engine whose device operators are Metal kernels bound by
+ * buffer index; paths below are relative to ios_kernels/kernels/:
+ *   KL = unsloth__Llama-3.2-1B-Instruct/kernel_metal_f16_20261024-1620/
+ *   KG = google__gemma-4-E2B-it/kernel_metal_f16_20261025-1225/
+ *
+ * Storage conventions (as in the reference, KL/kernels.metal:7-10):
+ *   weights fp16 row-major [out_features][in_features]; activations and the
+ *   residual stream fp32; KV cache fp16. fp16 values travel as uint16_t bits.
+ * KV cache layout (this library's contract):
+ *   K: [n_kv_heads][max_ctx][head_dim]   (the reference's layout)
+ *   V: [n_kv_heads][head_dim][max_ctx]   (transposed, so the attention
+ *      kernel's P·V matrix-core operand is a contiguous 16-byte load)
+ */
+#ifndef MXDECODE_H
+#define MXDECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* mxd_stream_t;
+
+enum {
+    MXD_OK = 0,
+    MXD_ERR_INVALID_ARG = -1,    /* null pointer, negative size, unknown enum */
+    MXD_ERR_UNSUPPORTED = -2,    /* shape/alignment the kernels do not handle */
+    MXD_ERR_HIP = -3,            /* a HIP runtime call or launch failed       */
+    MXD_ERR_WORKSPACE = -4,      /* workspace missing or too small            */
+    MXD_ERR_ALLOC = -5           /* device allocation failed                  */
+};
+
+enum { MXD_F32 = 0, MXD_F16 = 1 };                               /* activation dtypes */
+enum { MXD_W_F16 = 0, MXD_W_Q8B32 = 1 };                         /* weight formats    */
+enum { MXD_EPI_STORE = 0, MXD_EPI_ADD = 1, MXD_EPI_GELU_MUL = 2 }; /* KG/kernels.metal:152-153 */
+enum { MXD_ACT_GELU_TANH = 0, MXD_ACT_SILU = 1 };
+
+/* ---- library ---------------------------------------------------------- */
+
+/* Text of the last failure on this thread ("" if none). */
+const char* mxd_last_error(void);
+/* ABI version of this header (bumped on any signature change). */
+int mxd_abi_version(void);
+/* Kernel tunables by name, e.g. "MV_NR" (rows per workgroup) or "MV_NW"
+ * (waves splitting K). value <= 0 restores the shape-based default.
+ * Replaces the reference's `--define NAME=VALUE` (KL/main.swift:178-184). */
+int mxd_set_tunable(const char* name, int value);
+
+/* ---- synthetic weights -------------------------------------------------- */
+
+/* dst[i] = N(0, stddev^2)-distributed value for element i of tensor
+ * (seed, tensor_id), from a counter-based hash (splitmix64) summed over
+ * eight 16-bit uniforms and scaled in fp32; dtype MXD_F32 or MXD_F16 (RNE).
+ * Stands in for the converted HF checkpoint (KL/convert_weights.py:71-89),
+ * which needs a network fetch; the oracle computes the same bits on the CPU. */
+int mxd_fill_normal(void* dst, int dtype, uint64_t n, uint64_t seed, uint64_t tensor_id,
+                    float stddev, mxd_stream_t stream);
+
+/* ---- matvec (GEMV) ------------------------------------------------------ */
+
+/* y = W·x, W fp32 [M][K] row-major, x fp32 [K], y fp32 [M]. fp32 variant of
+ * matvec_f16 (KL/kernels.metal:106-137) for the fp32 parity configuration. */
+int mxd_gemv_f32(const float* W, const float* x, float* y, int M, int K, mxd_stream_t stream);
+
+/* y (op)= W·x with W fp16 [M][K]; x fp32 or fp16 (x_dtype); y fp32; fp32
+ * accumulation. epilogue: STORE y=s, ADD y+=s, GELU_MUL y=gelu_tanh(s)*aux.
+ * Replaces matvec_f16 / matvec_f16_add / matvec_f16_gelu_mul
+ * (KG/kernels.metal:159-198, KL/kernels.metal:106-137; host KG/main.swift:303-316).
+ * Needs K % 8 == 0 (16-byte rows); any M. */
+int mxd_matvec_f16(const uint16_t* W, const void* x, int x_dtype, float* y, int M, int K,
+                   int epilogue, const float* aux, mxd_stream_t stream);
+
+/* Same contract with int8 block-32 weights: y[r] = sum_b s[r][b] * sum_{k in b} q[r][k]*x[k].
+ * Wq int8 [M][K]; scales fp16 [M][K/32] (= max|w|/127 of the block).
+ * No reference counterpart (Q8_0 is a roadmap item, ios_kernels/PLAN.md:175);
+ * drops in wherever matvec_f16 is bound. Needs K % 32 == 0. */
+int mxd_matvec_q8b32(const int8_t* Wq, const uint16_t* scales, const void* x, int x_dtype,
+                     float* y, int M, int K, int epilogue, const float* aux, mxd_stream_t stream);
+
+/* Fused gated up-projection h[r] = act(Wg[r]·x) * (Wu[r]·x), F rows, K columns.
+ * w_format MXD_W_F16 (scales ignored) or MXD_W_Q8B32; x fp32 or fp16.
+ * Replaces matvec_gate_up_gelu (KG/kernels.metal:205-234) and
+ * matvec_gate_up_silu (KL/kernels.metal:144-173); host KG/main.swift:318-330. */
+int mxd_matvec_gate_up(int w_format, const void* Wg, const uint16_t* sg, const void* Wu,
+                       const uint16_t* su, const void* x, int x_dtype, float* h, int F, int K,
+                       int act, mxd_stream_t stream);
+
+/* ---- normalisation, embedding, casts ------------------------------------ */
+
+/* y[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * (plus_one ? 1 + w : w), rows x D,
+ * x fp32, w fp32, y fp32 or fp16 (y_dtype). Replaces rmsnorm_f32/rmsnorm_f16
+ * (KL/kernels.metal:71-96; host KL/main.swift:233-244). plus_one selects the
+ * Gemma (1 + w) weight convention. */
+int mxd_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int rows, int D, float eps,
+                int plus_one, mxd_stream_t stream);
+
+/* x[r][i] = float(E[tokens[pos + r]][i]) * scale for r < rows. Replaces embed
+ * (KL/kernels.metal:31-39) and embed_rows (KG/kernels.metal:34-42); the token
+ * index is read on the device, so a sampled token feeds the next step without
+ * a host round trip (KL/main.swift:319-320). */
+int mxd_embed(const uint16_t* E, const int32_t* tokens, int pos, int rows, float* x, int D,
+              float scale, int vocab, mxd_stream_t stream);
+
+/* dst = fp16(src), n elements. Replaces f32_to_f16 (KL/kernels.metal:361-365). */
+int mxd_f32_to_f16(const float* src, uint16_t* dst, size_t n, mxd_stream_t stream);
+
+/* ---- RoPE + KV-cache append --------------------------------------------- */
+
+/* qkv rows are [q n_heads*hd | k n_kv_heads*hd | v n_kv_heads*hd] fp32 (row r at
+ * position pos0 + r). Rotates q in place and k (HF rotate_half pairs (i, i+hd/2),
+ * angle = pos * inv_freq[i] in fp32, accurate sin/cos), then appends fp16 k to
+ * kcache and fp16 v to vcache at that position (layouts in the header comment).
+ * Replaces rope_kv (KL/kernels.metal:182-224; host KL/main.swift:275-287). */
+int mxd_rope_kv(float* qkv, uint16_t* kcache, uint16_t* vcache, const float* inv_freq,
+                int n_heads, int n_kv_heads, int head_dim, int max_ctx, int pos0, int rows,
+                mxd_stream_t stream);
+
+/* ---- single-query attention ---------------------------------------------- */
+
+/* Workspace bytes mxd_attention needs for this shape (0 is possible). */
+size_t mxd_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim, int max_ctx);
+
+/* out[h] = softmax(scale * q[h]·K[kvh][0..n_keys)) · V[kvh][0..n_keys) for
+ * every query head h, kvh = h / (n_heads / n_kv_heads) (GQA/MQA), fp32 scores
+ * and softmax. Split over the key axis with an online softmax and a
+ * log-sum-exp merge, so n_keys is bounded only by max_ctx; the G = n_heads /
+ * n_kv_heads query heads of a group share each K/V tile. head_dim 128 or 256;
+ * max_ctx % 32 == 0. q [n_heads*hd] fp32, out [n_heads*hd] fp32.
+ * If n_keys_dev is not NULL the key count is read on the device from
+ * *n_keys_dev (+1), so a captured step replays at a moving position.
+ * Replaces attention (KL/kernels.metal:235-305, KG/kernels.metal:317-399;
+ * host KL/main.swift:289-303) for the decode case T = 1. */
+int mxd_attention(const float* q, const uint16_t* kcache, const uint16_t* vcache, float* out,
+                  int n_heads, int n_kv_heads, int head_dim, int max_ctx, int n_keys,
+                  const int32_t* n_keys_dev, float scale, void* workspace, size_t ws_bytes,
+                  mxd_stream_t stream);
+
+/* ---- greedy sample -------------------------------------------------------- */
+
+/* Workspace bytes mxd_argmax needs for N logits. */
+size_t mxd_argmax_workspace_size(int N);
+
+/* tokens[out_idx] = argmax(logits[0..N)), ties to the lowest index.
+ * Replaces argmax (KL/kernels.metal:310-345; host KL/main.swift:305-315). The
+ * workspace must be zeroed once before first use; the kernel leaves it zeroed. */
+int mxd_argmax(const float* logits, int32_t* tokens, int N, int out_idx, void* workspace,
+               size_t ws_bytes, mxd_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXDECODE_H */

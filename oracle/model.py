@@ -1,0 +1,144 @@
+"""The decode step composed from oracle.ops (NumPy; small configurations).
+
+Step order follows the reference's Engine.encodeDecode (KL/main.swift:321-347)
+with the Gemma substitutions BASELINE's Gemma-2B shape needs: sqrt(D) embedding
+scale (KG/main.swift:397), GeGLU (KG/kernels.metal:205-234), MQA, tied LM head
+(KG/main.swift:379-380), (1 + w) RMSNorm weights. Values are rounded to fp32
+between ops and K/V to fp16, the storage points of the GPU path.
+
+Weights are synthetic: hashrng with one tensor id per named tensor (names as
+in KL/convert_weights.py:56-69).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import hashrng, ops
+
+F32 = np.float32
+
+
+@dataclass(frozen=True)
+class DecodeConfig:
+    n_layers: int
+    dim: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    ffn_dim: int
+    vocab: int
+    eps: float = 1e-6
+    rope_theta: float = 10000.0
+    act: str = "gelu_tanh"
+    gemma_embed_scale: bool = True   # x = E[tok] * sqrt(D)
+    plus_one: bool = True            # RMSNorm weight (1 + w)
+
+    @property
+    def qkv_dim(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+
+GEMMA_2B = DecodeConfig(n_layers=18, dim=2048, n_heads=8, n_kv_heads=1, head_dim=256, ffn_dim=16384, vocab=256000)
+TINY = DecodeConfig(n_layers=2, dim=256, n_heads=4, n_kv_heads=1, head_dim=128, ffn_dim=512, vocab=1000)
+
+
+def tensor_id(name: str) -> int:
+    """Tensor id of a named weight for the hash generator."""
+    fixed = {"embed": 1, "final_norm": 2}
+    if name in fixed:
+        return fixed[name]
+    layer, kind = name.split(".")
+    kinds = ["attn_norm", "wqkv", "wo", "ffn_norm", "wgate", "wup", "wdown"]
+    return 1000 + 16 * int(layer[1:]) + kinds.index(kind)
+
+
+def weight_shapes(cfg: DecodeConfig) -> dict[str, tuple[tuple[int, ...], type]]:
+    D, F = cfg.dim, cfg.ffn_dim
+    shapes = {"embed": ((cfg.vocab, D), np.float16), "final_norm": ((D,), np.float32)}
+    for l in range(cfg.n_layers):
+        shapes[f"l{l}.attn_norm"] = ((D,), np.float32)
+        shapes[f"l{l}.wqkv"] = ((cfg.qkv_dim, D), np.float16)
+        shapes[f"l{l}.wo"] = ((D, cfg.n_heads * cfg.head_dim), np.float16)
+        shapes[f"l{l}.ffn_norm"] = ((D,), np.float32)
+        shapes[f"l{l}.wgate"] = ((F, D), np.float16)
+        shapes[f"l{l}.wup"] = ((F, D), np.float16)
+        shapes[f"l{l}.wdown"] = ((D, F), np.float16)
+    return shapes
+
+
+def make_weights(cfg: DecodeConfig, seed: int, std: float = 0.02) -> dict[str, np.ndarray]:
+    return {
+        name: hashrng.normal(shape, dt, seed, tensor_id(name), std)
+        for name, (shape, dt) in weight_shapes(cfg).items()
+    }
+
+
+class OracleDecoder:
+    """Greedy decoder over a token buffer, mirroring Engine.decode: step(pos) reads
+    tokens[pos] and writes argmax to tokens[pos + 1] (KL/main.swift:319-320)."""
+
+    def __init__(self, cfg: DecodeConfig, weights: dict[str, np.ndarray], max_ctx: int, fp16_kv: bool = True):
+        self.cfg, self.w, self.max_ctx = cfg, weights, max_ctx
+        kv_dt = np.float16 if fp16_kv else np.float64
+        self.k = np.zeros((cfg.n_layers, cfg.n_kv_heads, max_ctx, cfg.head_dim), kv_dt)
+        self.v = np.zeros((cfg.n_layers, cfg.n_kv_heads, cfg.head_dim, max_ctx), kv_dt)
+        self.invf = ops.inv_freq(cfg.head_dim, cfg.rope_theta)
+        self.tokens = np.zeros(max_ctx + 1, np.int32)
+        self.fp16_kv = fp16_kv
+
+    def _rope_kv(self, l: int, qkv: np.ndarray, pos: int) -> np.ndarray:
+        c = self.cfg
+        if self.fp16_kv:
+            return ops.rope_kv(qkv, self.k[l], self.v[l], self.invf, c.n_heads, c.n_kv_heads, pos)
+        hd = c.head_dim
+        row = qkv.astype(np.float64)
+        q = ops.rope(row[: c.n_heads * hd].reshape(c.n_heads, hd), pos, self.invf)
+        k = ops.rope(row[c.n_heads * hd : (c.n_heads + c.n_kv_heads) * hd].reshape(c.n_kv_heads, hd), pos, self.invf)
+        self.k[l][:, pos, :] = k
+        self.v[l][:, :, pos] = row[(c.n_heads + c.n_kv_heads) * hd :].reshape(c.n_kv_heads, hd)
+        return q.reshape(-1)
+
+    def forward(self, pos: int) -> np.ndarray:
+        """Logits (fp32) for tokens[pos] at position pos; updates the KV caches."""
+        c, w = self.cfg, self.w
+        scale = F32(math.sqrt(c.dim)) if c.gemma_embed_scale else F32(1.0)
+        x = ops.embed(w["embed"], int(self.tokens[pos]), float(scale)).astype(F32)
+        att_scale = float(F32(1.0) / F32(math.sqrt(c.head_dim)))
+        for l in range(c.n_layers):
+            xn = ops.rmsnorm(x, w[f"l{l}.attn_norm"], c.eps, c.plus_one).astype(F32)
+            qkv = ops.matvec(w[f"l{l}.wqkv"], xn).astype(F32)
+            q = self._rope_kv(l, qkv, pos).astype(F32)
+            att = ops.attention(q, self.k[l], self.v[l], pos + 1, c.n_heads, att_scale).astype(F32)
+            x = (x + ops.matvec(w[f"l{l}.wo"], att).astype(F32)).astype(F32)
+            xn = ops.rmsnorm(x, w[f"l{l}.ffn_norm"], c.eps, c.plus_one).astype(F32)
+            h = ops.gate_up(w[f"l{l}.wgate"], w[f"l{l}.wup"], xn, c.act).astype(F32)
+            x = (x + ops.matvec(w[f"l{l}.wdown"], h).astype(F32)).astype(F32)
+        xn = ops.rmsnorm(x, w["final_norm"], c.eps, c.plus_one).astype(F32)
+        return ops.matvec(w["embed"], xn).astype(F32)
+
+    def step(self, pos: int, sample: bool = True) -> tuple[int, float]:
+        """One decode step; with sample, tokens[pos + 1] = argmax. Returns (token,
+        top-1 minus top-2 logit margin)."""
+        logits = self.forward(pos)
+        tok = ops.argmax(logits)
+        if sample:
+            self.tokens[pos + 1] = tok
+        top2 = np.partition(logits, -2)[-2:]
+        return tok, float(top2[1] - top2[0])
+
+    def generate(self, prompt: list[int], n_new: int) -> tuple[list[int], list[float]]:
+        """Prefill token by token through the decode path (the reference's
+        --no-gemm prefill, KL/main.swift:367-368), then n_new - 1 more steps:
+        returns the n_new greedy tokens tokens[P .. P + n_new) and margins."""
+        P = len(prompt)
+        self.tokens[:P] = prompt
+        margins = []
+        for pos in range(P + n_new - 1):
+            _, m = self.step(pos, sample=pos >= P - 1)
+            if pos >= P - 1:
+                margins.append(m)
+        return [int(t) for t in self.tokens[P : P + n_new]], margins

@@ -1,0 +1,321 @@
+"""Pins for the CPU oracle (runs without a GPU).
+
+The reference has no per-operator tests or golden vectors (its only checks are
+end-to-end strings on real checkpoints, ios_kernels/surfaces/tests/
+test_kernel_e2e.py:23-32). Each oracle function is pinned here instead by
+something independent of its own formula: a closed form, a library routine
+(torch / transformers), brute force, a second restatement (the C oracle), or
+HF transformers' Gemma on a tiny config (tests/golden/hf_gemma_tiny.npz).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import hashrng, model as om, native, ops
+
+# ---------------------------------------------------------------- generator
+
+
+def test_hashrng_three_restatements_agree():
+    v = hashrng.normal_f32(64, 1234, 1000 + 16 * 3 + 4, 0.02)
+    ints = [hashrng.normal_int(i, 1234, 1000 + 16 * 3 + 4, 0.02) for i in range(64)]
+    assert np.array_equal(v, np.array(ints, np.float32))
+    c = native.fill_normal((64,), np.float32, 1234, 1000 + 16 * 3 + 4, 0.02)
+    assert np.array_equal(v, c)
+    h_np = hashrng.normal((50000,), np.float16, 9, 1, 0.02)
+    h_c = native.fill_normal((50000,), np.float16, 9, 1, 0.02)
+    assert np.array_equal(h_np.view(np.uint16), h_c.view(np.uint16))
+
+
+def test_hashrng_mix_is_splitmix64():
+    # splitmix64 from state 0: first outputs of the published generator.
+    assert hashrng.mix_int(0) == 0xE220A8397B1DCDAF
+    assert hashrng.mix_int(0x9E3779B97F4A7C15) == 0x6E789E6AA1B965F4
+    z = np.array([0, 0x9E3779B97F4A7C15], np.uint64)
+    assert hashrng.mix(z).tolist() == [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4]
+
+
+def test_hashrng_statistics():
+    v = hashrng.normal_f32(1 << 20, 5, 77, 1.0).astype(np.float64)
+    assert abs(v.mean()) < 5e-3
+    assert abs(v.std() - 1.0) < 5e-3
+    kurt = ((v - v.mean()) ** 4).mean() / v.var() ** 2
+    assert abs(kurt - (3 - 1.2 / 8)) < 0.03  # Irwin-Hall(8): excess kurtosis -6/(5*8)
+    assert np.abs(v).max() <= 4 * 65535 / hashrng.SIGMA_SUM + 1e-6
+    w = hashrng.normal_f32(1 << 16, 5, 78, 0.02)
+    assert abs(w.std() - 0.02) < 5e-4
+    assert not np.array_equal(hashrng.normal_f32(16, 5, 77, 1.0), hashrng.normal_f32(16, 5, 79, 1.0))
+
+
+# ---------------------------------------------------------------- matvec
+
+
+def test_matvec_closed_forms(rng):
+    x = rng.standard_normal(64)
+    assert np.array_equal(ops.matvec(np.eye(64, dtype=np.float16), x), x)
+    W = rng.standard_normal((5, 64)).astype(np.float16)
+    assert np.array_equal(ops.matvec(W, np.eye(64)[7]), W[:, 7].astype(np.float64))
+    assert np.allclose(ops.matvec(np.ones((3, 64), np.float16), x), x.sum())
+
+
+def test_matvec_brute_force(rng):
+    W = rng.standard_normal((7, 40)).astype(np.float16)
+    x = rng.standard_normal(40).astype(np.float32)
+    brute = [math.fsum(float(W[r, k]) * float(x[k]) for k in range(40)) for r in range(7)]
+    assert np.allclose(ops.matvec(W, x), brute, rtol=0, atol=1e-12)
+    assert np.allclose(native.matvec_f16(W, x), brute, rtol=0, atol=1e-12)
+
+
+def test_matvec_linearity(rng):
+    W = rng.standard_normal((9, 32)).astype(np.float16)
+    a, b = rng.standard_normal(32), rng.standard_normal(32)
+    assert np.allclose(ops.matvec(W, 2 * a - 3 * b), 2 * ops.matvec(W, a) - 3 * ops.matvec(W, b))
+
+
+def test_quantize_closed_forms():
+    s = np.float16(0.5)
+    W = np.zeros((3, 64), np.float32)
+    W[0, :32] = np.arange(-16, 16) * float(s)  # exact multiples of s with max 16*s -> s' = 16s/127
+    W[1, :32] = 127 * float(s)                  # a block at +127 s
+    W[1, 32:] = -127 * float(s)
+    q, sc = ops.quantize_q8b32(W)
+    assert sc[2, 0] == 0 and sc[2, 1] == 0 and not q[2].any()  # zero blocks
+    assert sc[1, 0] == s and np.all(q[1, :32] == 127) and np.all(q[1, 32:] == -127)
+    deq = q.astype(np.float32).reshape(3, 2, 32) * sc.astype(np.float32)[..., None]
+    assert np.array_equal(deq[1].reshape(-1), W[1])
+
+
+def test_quantize_roundtrip_and_package_agree(rng):
+    from gemmagemini4hackathon2026_10_2425_amd.quant import quantize_q8b32
+
+    W = rng.standard_normal((33, 320)).astype(np.float32) * 0.02
+    W[4, 32:64] = 0.0
+    q, s = ops.quantize_q8b32(W)
+    q2, s2 = quantize_q8b32(W)
+    assert np.array_equal(q, q2) and np.array_equal(s.view(np.uint16), s2.view(np.uint16))
+    deq = q.reshape(33, 10, 32).astype(np.float64) * s.astype(np.float64)[..., None]
+    err = np.abs(deq.reshape(33, 320) - W)
+    bound = (s.astype(np.float64)[..., None] * np.ones((1, 1, 32))).reshape(33, 320) * 0.5
+    # fp16 rounding of the scale adds up to 127 * s * 2^-11 on top of s/2
+    assert np.all(err <= bound * (1 + 127 * 2**-10) + 1e-12)
+    assert np.abs(q).max() <= 127
+
+
+def test_matvec_q8b32_equals_dequant(rng):
+    W = rng.standard_normal((17, 256)).astype(np.float32)
+    q, s = ops.quantize_q8b32(W)
+    x = rng.standard_normal(256).astype(np.float32)
+    deq = q.reshape(17, 8, 32).astype(np.float64) * s.astype(np.float64)[..., None]
+    assert np.allclose(ops.matvec_q8b32(q, s, x), deq.reshape(17, 256) @ x, rtol=1e-13, atol=1e-13)
+    assert np.allclose(native.matvec_q8b32(q, s, x), ops.matvec_q8b32(q, s, x), rtol=1e-13, atol=1e-13)
+
+
+# ---------------------------------------------------------------- activations
+
+
+def test_activations_match_torch(rng):
+    g = torch.from_numpy(rng.standard_normal(1000) * 6)
+    want_gelu = torch.nn.functional.gelu(g, approximate="tanh").numpy()
+    assert np.allclose(ops.gelu_tanh(g.numpy()), want_gelu, rtol=1e-13, atol=1e-15)
+    assert np.allclose(ops.silu(g.numpy()), torch.nn.functional.silu(g).numpy(), rtol=1e-13, atol=1e-15)
+    assert ops.gelu_tanh(0.0) == 0.0 and ops.silu(0.0) == 0.0
+    assert abs(ops.gelu_tanh(30.0) - 30.0) < 1e-12 and abs(ops.silu(40.0) - 40.0) < 1e-12
+
+
+def test_gate_up_special_cases(rng):
+    Wg = np.zeros((4, 32), np.float16)
+    Wu = rng.standard_normal((4, 32)).astype(np.float16)
+    x = rng.standard_normal(32)
+    assert np.all(ops.gate_up(Wg, Wu, x) == 0)
+
+
+# ---------------------------------------------------------------- rmsnorm
+
+
+def test_rmsnorm_matches_torch(rng):
+    x = rng.standard_normal((3, 2048)) * 5
+    w = rng.standard_normal(2048) * 0.02
+    want = torch.nn.functional.rms_norm(torch.from_numpy(x), (2048,), torch.from_numpy(w), eps=1e-6).numpy()
+    assert np.allclose(ops.rmsnorm(x, w, 1e-6), want, rtol=1e-12, atol=1e-14)
+    want1 = torch.nn.functional.rms_norm(torch.from_numpy(x), (2048,), torch.from_numpy(1 + w), eps=1e-6).numpy()
+    assert np.allclose(ops.rmsnorm(x, w, 1e-6, plus_one=True), want1, rtol=1e-12, atol=1e-14)
+
+
+def test_rmsnorm_closed_forms():
+    c, eps = 3.0, 1e-6
+    y = ops.rmsnorm(np.full(16, c), np.full(16, 2.0), eps)
+    assert np.allclose(y, c / math.sqrt(c * c + eps) * 2.0)
+    x = np.arange(1, 9, dtype=np.float64)
+    assert np.allclose(ops.rmsnorm(x * 1000, np.ones(8), 0.0), ops.rmsnorm(x, np.ones(8), 0.0))
+
+
+# ---------------------------------------------------------------- rope
+
+
+def test_rope_identity_and_norm(rng):
+    invf = ops.inv_freq(128, 10000.0)
+    v = rng.standard_normal(128)
+    assert np.allclose(ops.rope(v, 0, invf), v)
+    r = ops.rope(v, 777, invf)
+    pn = lambda a: a[:64] ** 2 + a[64:] ** 2  # noqa: E731
+    assert np.allclose(pn(r), pn(v))
+
+
+def test_rope_composition():
+    # inv_freq of powers of two keeps fp32 angles exact, so R(a) R(b) = R(a + b).
+    invf = np.array([2.0 ** -k for k in range(64)], np.float32)
+    v = np.random.default_rng(1).standard_normal(128)
+    assert np.allclose(ops.rope(ops.rope(v, 5, invf), 9, invf), ops.rope(v, 14, invf), atol=1e-12)
+
+
+def test_rope_matches_hf_apply_rotary():
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+
+    rng = np.random.default_rng(3)
+    hd, pos = 256, 300
+    invf = ops.inv_freq(hd, 10000.0)
+    q = rng.standard_normal((1, 2, 1, hd))
+    k = rng.standard_normal((1, 1, 1, hd))
+    ang = (np.float32(pos) * invf).astype(np.float64)
+    emb = np.concatenate([ang, ang])
+    cos, sin = torch.from_numpy(np.cos(emb))[None, None], torch.from_numpy(np.sin(emb))[None, None]
+    qh, kh = apply_rotary_pos_emb(torch.from_numpy(q), torch.from_numpy(k), cos, sin, unsqueeze_dim=1)
+    assert np.allclose(ops.rope(q[0, :, 0], pos, invf), qh.numpy()[0, :, 0], atol=1e-12)
+    assert np.allclose(ops.rope(k[0, :, 0], pos, invf), kh.numpy()[0, :, 0], atol=1e-12)
+
+
+def test_inv_freq_definition():
+    f = ops.inv_freq(128, 500000.0)
+    assert f[0] == 1.0 and f.dtype == np.float32
+    assert f[63] == np.float32(1.0 / 500000.0 ** (126 / 128))
+
+
+def test_rope_kv_appends_fp16(rng):
+    nh, nkv, hd, ctx = 4, 2, 128, 16
+    kc = np.zeros((nkv, ctx, hd), np.float16)
+    vc = np.zeros((nkv, hd, ctx), np.float16)
+    row = rng.standard_normal((nh + 2 * nkv) * hd).astype(np.float32)
+    invf = ops.inv_freq(hd, 10000.0)
+    q = ops.rope_kv(row, kc, vc, invf, nh, nkv, 5)
+    assert np.allclose(q.reshape(nh, hd), ops.rope(row[: nh * hd].reshape(nh, hd), 5, invf))
+    k_want = ops.rope(row[nh * hd : (nh + nkv) * hd].reshape(nkv, hd), 5, invf).astype(np.float16)
+    assert np.array_equal(kc[:, 5, :], k_want)
+    assert np.array_equal(vc[:, :, 5], row[(nh + nkv) * hd :].reshape(nkv, hd).astype(np.float16))
+    assert np.count_nonzero(kc[:, :5]) == 0 and np.count_nonzero(vc[:, :, 6:]) == 0
+
+
+# ---------------------------------------------------------------- attention
+
+
+def _cache(rng, nkv, L, hd):
+    K = rng.standard_normal((nkv, L, hd)).astype(np.float16)
+    V = rng.standard_normal((nkv, L, hd)).astype(np.float16)
+    return K, np.ascontiguousarray(V.transpose(0, 2, 1)), V
+
+
+def test_attention_matches_torch_sdpa(rng):
+    nh, nkv, hd, L = 8, 2, 128, 50
+    K, Vt, V = _cache(rng, nkv, L, hd)
+    q = rng.standard_normal(nh * hd)
+    got = ops.attention(q, K, Vt, L, nh, 1 / math.sqrt(hd))
+    G = nh // nkv
+    Kr = torch.from_numpy(K.astype(np.float64)).repeat_interleave(G, 0)[None]
+    Vr = torch.from_numpy(V.astype(np.float64)).repeat_interleave(G, 0)[None]
+    qt = torch.from_numpy(q.reshape(1, nh, 1, hd))
+    want = torch.nn.functional.scaled_dot_product_attention(qt, Kr, Vr, scale=1 / math.sqrt(hd)).numpy()
+    assert np.allclose(got, want.reshape(-1), rtol=1e-12, atol=1e-13)
+
+
+def test_attention_closed_forms(rng):
+    nh, nkv, hd = 4, 1, 128
+    K, Vt, V = _cache(rng, nkv, 10, hd)
+    q = rng.standard_normal(nh * hd)
+    one = ops.attention(q, K, Vt, 1, nh, 0.1).reshape(nh, hd)
+    assert np.allclose(one, np.broadcast_to(V[0, 0].astype(np.float64), (nh, hd)))
+    Ks = np.broadcast_to(K[:, :1], K.shape).copy()
+    same = ops.attention(q, Ks, Vt, 10, nh, 0.1).reshape(nh, hd)
+    assert np.allclose(same, V[0].astype(np.float64).mean(axis=0))
+    # a constant shift of all scores (q orthogonal part) does not change the output
+    K2 = K.astype(np.float64) + 0.0
+    a = ops.attention(q, K2, Vt, 10, nh, 0.1)
+    assert np.allclose(a, ops.attention(q, K, Vt, 10, nh, 0.1))
+
+
+def test_attention_split_merge_identity(rng):
+    """The log-sum-exp merge the GPU uses equals one pass (the rule itself, in fp64)."""
+    nh, nkv, hd, L = 2, 1, 128, 96
+    K, Vt, _ = _cache(rng, nkv, L, hd)
+    q = rng.standard_normal(nh * hd)
+    s = (K[0].astype(np.float64) @ q.reshape(nh, hd).T).T * 0.2  # [nh, L]
+    V = Vt[0].astype(np.float64).T
+    parts = []
+    for a, b in [(0, 30), (30, 64), (64, 96)]:
+        m = s[:, a:b].max(axis=1, keepdims=True)
+        p = np.exp(s[:, a:b] - m)
+        parts.append((m, p.sum(axis=1, keepdims=True), p @ V[a:b]))
+    M = np.max([m for m, _, _ in parts], axis=0)
+    num = sum(np.exp(m - M) * o for m, _, o in parts)
+    den = sum(np.exp(m - M) * l for m, l, _ in parts)
+    assert np.allclose(num / den, ops.attention(q, K, Vt, L, nh, 0.2).reshape(nh, hd))
+
+
+def test_argmax_first_max():
+    x = np.array([1.0, 5.0, 2.0, 5.0, -1.0], np.float32)
+    assert ops.argmax(x) == 1
+    assert ops.argmax(np.zeros(10, np.float32)) == 0
+
+
+def test_embed_closed_form(rng):
+    E = rng.standard_normal((10, 8)).astype(np.float16)
+    assert np.array_equal(ops.embed(E, 3, 2.0), E[3].astype(np.float64) * 2.0)
+
+
+# ---------------------------------------------------------------- decode step
+
+
+def test_decode_matches_hf_gemma():
+    """Logits of every prompt position and the greedy continuation equal HF
+    transformers' GemmaForCausalLM (fp64) on the same weights."""
+    z = np.load(__file__.rsplit("/", 1)[0] + "/golden/hf_gemma_tiny.npz")
+    cfg = om.TINY
+    d = om.OracleDecoder(cfg, om.make_weights(cfg, int(z["seed"])), 64, fp16_kv=False)
+    prompt = [int(t) for t in z["prompt"]]
+    d.tokens[: len(prompt)] = prompt
+    for pos in range(len(prompt)):
+        lg = d.forward(pos)
+        ref = z["logits"][pos]
+        assert np.abs(lg - ref).max() / np.abs(ref).max() < 1e-6
+    toks, _ = d.generate(prompt, len(z["greedy"]))
+    assert toks == [int(t) for t in z["greedy"]]
+
+
+def test_decode_numpy_and_c_restatements_agree():
+    cfg = om.DecodeConfig(n_layers=2, dim=256, n_heads=8, n_kv_heads=1, head_dim=256, ffn_dim=512, vocab=2000)
+    seed = 21
+    d = om.OracleDecoder(cfg, om.make_weights(cfg, seed), 64)
+    n = native.NativeDecoder(cfg, 64, seed)
+    prompt = [7, 1999, 0, 1234, 55]
+    t1, m1 = d.generate(prompt, 10)
+    t2, m2 = n.generate(prompt, 10)
+    assert t1 == t2
+    assert np.allclose(m1, m2, rtol=1e-4, atol=1e-5)
+    d2 = om.OracleDecoder(cfg, om.make_weights(cfg, seed), 64)
+    d2.tokens[: len(prompt)] = prompt
+    n2 = native.NativeDecoder(cfg, 64, seed)
+    n2.tokens[: len(prompt)] = prompt
+    for pos in range(len(prompt)):
+        a = d2.forward(pos)
+        _, _, b = n2.step(pos, want_logits=True, sample=False)
+        assert np.abs(a - b).max() / np.abs(a).max() < 1e-5
+
+
+@pytest.mark.parametrize("name", ["embed", "final_norm", "l0.attn_norm", "l17.wdown"])
+def test_tensor_ids_are_distinct(name):
+    ids = {om.tensor_id(n) for n in om.weight_shapes(om.GEMMA_2B)}
+    assert len(ids) == len(om.weight_shapes(om.GEMMA_2B))
+    assert om.tensor_id(name) in ids
