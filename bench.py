@@ -118,7 +118,7 @@ def attention_leg(steps: int, warmup: int, dev, L: int = 32768) -> dict:
     kv_bytes = 2 * nkv * max_ctx * hd * 2
     R = _copies(kv_bytes)
     ks = [ops.fill_normal((nkv, max_ctx, hd), torch.float16, 8, 10 + i, 1.0, dev) for i in range(R)]
-    vs = [ops.fill_normal((nkv, hd, max_ctx), torch.float16, 8, 50 + i, 1.0, dev) for i in range(R)]
+    vs = [ops.fill_normal((nkv, max_ctx, hd), torch.float16, 8, 50 + i, 1.0, dev) for i in range(R)]
     q = ops.fill_normal((nh * hd,), torch.float32, 8, 1, 1.0, dev)
     out = torch.empty(nh * hd, dtype=torch.float32, device=dev)
     ws = ops.attention_workspace(nh, nkv, hd, max_ctx, dev)

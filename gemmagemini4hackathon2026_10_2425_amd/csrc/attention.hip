@@ -20,11 +20,17 @@
 //  * the S^T accumulator layout (lane = column, 4 rows per lane group) is
 //    already the A-operand layout of the P.V MFMA once the key rows are
 //    permuted at load time, so P never leaves registers.
-//  * K loads are 16-byte rows of [kvh][ctx][hd]; V is cached transposed,
-//    [kvh][hd][ctx], so the P.V B operand (8 consecutive keys of one dim) is one
-//    16-byte load too.
-//  * splits write unnormalised (O, max, sum) partials, merged by a second
-//    kernel with the log-sum-exp rule; one split writes the output directly.
+//  * K and V are cached in tiles of 32 positions stored in MFMA operand order,
+//    so each operand is one fully coalesced 1 KiB wave load (every 16-lane
+//    quarter-wave reads 256 contiguous bytes) and a block is one contiguous
+//    8 KiB (hd 128) run per cache.
+//  * 32-key blocks are dealt round-robin to the splits of a kv head (split s
+//    takes blocks s, s+S, ...), so the grid streams the cache front to back;
+//    for head_dim 128 each wave prefetches its next block while it computes.
+//  * splits write unnormalised (O, max, sum) partials, merged by a second small
+//    kernel with the log-sum-exp rule; a single split writes the output
+//    directly. (A merge by the last-arriving split needs device-scope fences
+//    in every workgroup, which on a multi-XCD part costs more than a launch.)
 #include "common.hpp"
 
 namespace {
@@ -32,6 +38,7 @@ namespace {
 constexpr int ATT_WAVES = 4;
 constexpr int ATT_THREADS = ATT_WAVES * 64;
 constexpr int BLK = 32;  // keys per wave step
+constexpr int MAX_SPLITS = 512;
 constexpr float LOG2E = 1.4426950408889634f;
 
 struct AttnArgs {
@@ -42,7 +49,7 @@ struct AttnArgs {
     float* ws_o;   // [n_splits][n_heads][HD]
     float* ws_ml;  // [n_splits][n_heads][2]
     const int32_t* pos_dev;
-    int n_heads, n_kv, G, max_ctx, n_keys, split;
+    int n_heads, n_kv, G, max_ctx, n_keys, n_splits;
     float qscale;  // scale * log2(e): scores live in the log2 domain
 };
 
@@ -54,19 +61,47 @@ __device__ __forceinline__ int n_keys_of(const AttnArgs& a) {
 }
 
 template <int HD>
+struct KVBlock {
+    h8_t k[2][HD / 32];
+    h8_t v[HD / 16];
+};
+
+// Loads of one 32-key block starting at key0 (a multiple of 32). The caches
+// are stored in MFMA operand order (the tile layouts in include/mxdecode.h),
+// so every operand is one 1 KiB contiguous wave load: lane l reads the 16
+// bytes at l * 16 of its chunk. K chunk (t, c) holds, for lane (col, g), key
+// 8(col>>2) + 4t + (col&3) of the block and dims 32c + 8g .. +7 (row 4g'+i of
+// S^T tile t is then key 8g' + 4t + i); V chunk d holds keys 8g .. +7 of dim
+// 16d + col.
+template <int HD>
+__device__ __forceinline__ void load_block(KVBlock<HD>& kv, const uint16_t* kbase, const uint16_t* vbase, int key0,
+                                           int lane) {
+    const uint16_t* kt = kbase + (size_t)key0 * HD + 8 * lane;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int c = 0; c < HD / 32; ++c)
+            kv.k[t][c] = *reinterpret_cast<const h8_t*>(kt + (t * (HD / 32) + c) * 512);
+    const uint16_t* vt = vbase + (size_t)key0 * HD + 8 * lane;
+#pragma unroll
+    for (int d = 0; d < HD / 16; ++d) kv.v[d] = *reinterpret_cast<const h8_t*>(vt + d * 512);
+}
+
+template <int HD>
 __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
     constexpr int NC = HD / 32;  // MFMA k-chunks over head_dim for Q.K
     constexpr int ND = HD / 16;  // 16-wide dim tiles for P.V
+    // Prefetching the next block doubles the K/V registers; it fits the
+    // register budget (2 waves per SIMD either way) for head_dim 128 only.
+    constexpr bool PREFETCH = HD == 128;
     __shared__ float sm_o[ATT_WAVES][8][HD];
     __shared__ float sm_m[ATT_WAVES][8];
     __shared__ float sm_l[ATT_WAVES][8];
 
     const int n = n_keys_of(a);
-    const int split = blockIdx.x, kvh = blockIdx.y;
-    const int k_begin = split * a.split;
-    if (k_begin >= n) return;
-    const int k_end = min(k_begin + a.split, n);
-    const int nblk = (k_end - k_begin + BLK - 1) / BLK;
+    const int nblocks = (n + BLK - 1) / BLK;
+    const int S = a.n_splits, split = blockIdx.x, kvh = blockIdx.y;
+    if (split >= nblocks) return;  // an empty split
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, g = lane >> 4;
@@ -95,29 +130,25 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
     }
 
     const uint16_t* kbase = a.k + (size_t)kvh * a.max_ctx * HD;
-    const uint16_t* vbase = a.v + (size_t)kvh * HD * a.max_ctx;
+    const uint16_t* vbase = a.v + (size_t)kvh * a.max_ctx * HD;
 
     float m_run = -INFINITY, l_run = 0.0f;
     f4_t o[ND];
 #pragma unroll
     for (int d = 0; d < ND; ++d) o[d] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (int b = wave; b < nblk; b += ATT_WAVES) {
-        const int key0 = k_begin + b * BLK;
-        // ---- loads: K rows permuted so that S^T row 4g'+i of tile t is key
-        // key0 + 8g' + 4t + i; V^T rows give keys key0 + 8g .. +7 of one dim.
-        h8_t kop[2][NC];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            const int key = key0 + 8 * (col >> 2) + 4 * t + (col & 3);
-            const uint16_t* kr = kbase + (size_t)key * HD + 8 * g;
-#pragma unroll
-            for (int c = 0; c < NC; ++c) kop[t][c] = *reinterpret_cast<const h8_t*>(kr + 32 * c);
+    // Blocks are dealt round-robin: split s owns global blocks s, s+S, s+2S, ...
+    // and wave w takes every 4th of those, so at any moment the splits of a kv
+    // head stream one contiguous run of the cache.
+    const int step = S * ATT_WAVES;
+    int b = split + S * wave;
+    KVBlock<HD> cur, nxt;
+    if (b < nblocks) load_block<HD>(cur, kbase, vbase, b * BLK, lane);
+    for (; b < nblocks; b += step) {
+        const int key0 = b * BLK;
+        if constexpr (PREFETCH) {
+            if (b + step < nblocks) load_block<HD>(nxt, kbase, vbase, (b + step) * BLK, lane);
         }
-        h8_t vop[ND];
-#pragma unroll
-        for (int d = 0; d < ND; ++d)
-            vop[d] = *reinterpret_cast<const h8_t*>(vbase + (size_t)(16 * d + col) * a.max_ctx + key0 + 8 * g);
 
         // ---- scores (log2 domain)
         float s[8];
@@ -125,7 +156,7 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
         for (int t = 0; t < 2; ++t) {
             f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int c = 0; c < NC; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[t][c], qop[c], acc, 0, 0, 0);
+            for (int c = 0; c < NC; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.k[t][c], qop[c], acc, 0, 0, 0);
 #pragma unroll
             for (int i = 0; i < 4; ++i) s[4 * t + i] = acc[i];
         }
@@ -164,13 +195,19 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
             for (int d = 0; d < ND; ++d)
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    if (key0 + 8 * g + j >= n) vop[d][j] = (_Float16)0.0f;
+                    if (key0 + 8 * g + j >= n) cur.v[d][j] = (_Float16)0.0f;
         }
 #pragma unroll
         for (int d = 0; d < ND; ++d) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[d][i] *= ar[i];
-            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vop[d], o[d], 0, 0, 0);
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, cur.v[d], o[d], 0, 0, 0);
+        }
+
+        if constexpr (PREFETCH) {
+            cur = nxt;
+        } else if (b + step < nblocks) {
+            load_block<HD>(cur, kbase, vbase, (b + step) * BLK, lane);
         }
     }
 
@@ -205,7 +242,7 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
     __syncthreads();
 
     // ---- merge the 4 waves (and write the split's partial or the output)
-    const int n_active = (n + a.split - 1) / a.split;
+    const int n_active = min(S, nblocks);
     for (int idx = threadIdx.x; idx < G * HD; idx += ATT_THREADS) {
         const int h = idx / HD, dim = idx - h * HD;
         float M = sm_m[0][h];
@@ -231,32 +268,66 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
     }
 }
 
-// out[h] = sum_s 2^(M_s - M) O_s / sum_s 2^(M_s - M) L_s over the active splits.
+// out[h] = sum_s 2^(M_s - M) O_s / sum_s 2^(M_s - M) L_s over the active
+// splits (log-sum-exp rule). One workgroup per query head: the (M_s, L_s) pairs
+// go through LDS first, then every thread sums its dim over the splits with
+// eight independent loads in flight.
 template <int HD>
 __global__ void __launch_bounds__(HD) attn_merge_kernel(AttnArgs a) {
+    __shared__ float sw[MAX_SPLITS];
+    __shared__ float sl[MAX_SPLITS];
+    __shared__ float red[HD / 64][2];
     const int n = n_keys_of(a);
-    const int n_active = (n + a.split - 1) / a.split;
+    const int n_active = min(a.n_splits, (n + BLK - 1) / BLK);
     if (n_active <= 1) return;
-    const int head = blockIdx.x, dim = threadIdx.x;
-    float M = -INFINITY;
-    for (int s = 0; s < n_active; ++s) M = fmaxf(M, a.ws_ml[((size_t)s * a.n_heads + head) * 2]);
-    float so = 0.0f, sl = 0.0f;
-    for (int s = 0; s < n_active; ++s) {
-        const size_t base = (size_t)s * a.n_heads + head;
-        const float f = exp2f(a.ws_ml[base * 2] - M);
-        so += f * a.ws_o[base * HD + dim];
-        sl += f * a.ws_ml[base * 2 + 1];
+    const int head = blockIdx.x, tid = threadIdx.x;
+    float mloc = -INFINITY;
+    for (int sp = tid; sp < n_active; sp += HD) {
+        const float m = a.ws_ml[((size_t)sp * a.n_heads + head) * 2];
+        sw[sp] = m;
+        sl[sp] = a.ws_ml[((size_t)sp * a.n_heads + head) * 2 + 1];
+        mloc = fmaxf(mloc, m);
     }
-    a.out[(size_t)head * HD + dim] = so / sl;
+    mloc = mxd::wave_max(mloc);
+    if ((tid & 63) == 0) red[tid >> 6][0] = mloc;
+    __syncthreads();
+    float M = red[0][0];
+#pragma unroll
+    for (int w = 1; w < HD / 64; ++w) M = fmaxf(M, red[w][0]);
+    float lloc = 0.0f;
+    for (int sp = tid; sp < n_active; sp += HD) {
+        const float f = exp2f(sw[sp] - M);
+        sw[sp] = f;
+        lloc += f * sl[sp];
+    }
+    lloc = mxd::wave_sum(lloc);
+    if ((tid & 63) == 0) red[tid >> 6][1] = lloc;
+    __syncthreads();
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < HD / 64; ++w) L += red[w][1];
+
+    const float* po = a.ws_o + (size_t)head * HD + tid;
+    const size_t stride = (size_t)a.n_heads * HD;
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int sp = 0;
+    for (; sp + 8 <= n_active; sp += 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc[u] += sw[sp + u] * po[(size_t)(sp + u) * stride];
+    }
+    for (; sp < n_active; ++sp) acc[0] += sw[sp] * po[(size_t)sp * stride];
+    const float tot = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+    a.out[(size_t)head * HD + tid] = tot / L;
 }
 
-int target_splits(int n_kv) { return (2 * 256 + n_kv - 1) / n_kv; }
+// Splits per kv head: about two workgroups per CU over the whole grid, and
+// never more splits than 32-key blocks.
+int target_splits(int n_kv) { return min(MAX_SPLITS, (2 * 256 + n_kv - 1) / n_kv); }
 
-int split_keys(int max_keys, int n_kv) {
+int splits_for(int max_keys, int n_kv) {
+    const int nblocks = (max_keys + BLK - 1) / BLK;
     const int t = target_splits(n_kv);
-    int split = (max_keys + t - 1) / t;
-    split = (split + 127) / 128 * 128;
-    return split < 128 ? 128 : split;
+    return nblocks < t ? nblocks : t;
 }
 
 }  // namespace
@@ -287,8 +358,7 @@ extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint1
                          reinterpret_cast<uintptr_t>(vcache);
     MXD_REQUIRE((al & 15) == 0, MXD_ERR_UNSUPPORTED, "mxd_attention: q, kcache, vcache must be 16-byte aligned");
 
-    const int split = split_keys(pos_dev ? max_ctx : n_keys, n_kv_heads);
-    const int n_splits = ((pos_dev ? max_ctx : n_keys) + split - 1) / split;
+    const int n_splits = splits_for(pos_dev ? max_ctx : n_keys, n_kv_heads);
     const size_t need = (size_t)n_splits * n_heads * (head_dim + 2) * sizeof(float);
     MXD_REQUIRE(n_splits == 1 || (workspace && ws_bytes >= need), MXD_ERR_WORKSPACE,
                 "mxd_attention: workspace of %zu bytes needed (got %zu)", need, ws_bytes);
@@ -300,15 +370,16 @@ extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint1
     a.k = kcache;
     a.v = vcache;
     a.out = out;
+    // Workspace: [O partials | (max, sum) partials]
     a.ws_o = static_cast<float*>(workspace);
-    a.ws_ml = workspace ? static_cast<float*>(workspace) + (size_t)n_splits * n_heads * head_dim : nullptr;
+    a.ws_ml = workspace ? a.ws_o + (size_t)n_splits * n_heads * head_dim : nullptr;
     a.pos_dev = pos_dev;
     a.n_heads = n_heads;
     a.n_kv = n_kv_heads;
     a.G = G;
     a.max_ctx = max_ctx;
     a.n_keys = n_keys;
-    a.split = split;
+    a.n_splits = n_splits;
     a.qscale = scale * LOG2E;
 
     hipStream_t s = mxd::as_stream(stream);

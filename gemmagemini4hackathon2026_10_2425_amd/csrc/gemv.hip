@@ -121,6 +121,13 @@ __device__ __forceinline__ size_t welem_bytes() {
     return WF == MXD_W_F16 ? 2 : WF == MXD_W_Q8B32 ? 1 : 4;
 }
 
+// Weights are read exactly once per call: nontemporal loads keep them from
+// displacing the activations and partial sums that are reused from cache.
+template <int WF>
+__device__ __forceinline__ u4_t ld_stream(const unsigned char* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p));
+}
+
 // NMAT == 1: OP is an MXD_EPI_*; NMAT == 2: OP is an MXD_ACT_* (gate, up).
 template <int WF, typename XT, int NMAT, int OP, int NR, int NW>
 __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
@@ -166,7 +173,7 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
                 for (int m = 0; m < NMAT; ++m)
 #pragma unroll
                     for (int r = 0; r < NR; ++r) {
-                        wv[u][m][r] = *reinterpret_cast<const u4_t*>(wrow[m][r] + (size_t)col * welem_bytes<WF>());
+                        wv[u][m][r] = ld_stream<WF>(wrow[m][r] + (size_t)col * welem_bytes<WF>());
                         if (WF == MXD_W_Q8B32) sv[u][m][r] = srow[m][r][col / 32];
                     }
             }
@@ -231,6 +238,133 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Row-streaming variant. A persistent grid walks the rows front to back
+// (workgroup b takes rows b, b + grid, ...); the NW waves of a workgroup split
+// one row's chunks (wave w always owns chunks w, w + NW, ... of every row), so
+// at any moment the whole GPU reads one compact, sequential window of W, which
+// is what keeps the HBM pages open. Each wave keeps its x fragments in
+// registers for the whole kernel, streams W with nontemporal loads (W is read
+// once), and issues the next row's loads before reducing the current row.
+// The NW partial sums of a row are added in a fixed order (deterministic).
+// ---------------------------------------------------------------------------
+constexpr int RS_MAX_CHUNKS = 64;  // 16 waves x 4 chunks
+
+template <int WF, typename XT, int NMAT, int OP, int NW, int RS_CPW>
+__global__ void __launch_bounds__(NW * 64) gemv_rows_kernel(GemvArgs a) {
+    constexpr int EPL = WT<WF>::EPL;
+    constexpr int CH = 64 * EPL;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int M = a.M, K = a.K;
+    const int nch = (K + CH - 1) / CH;
+    const size_t row_bytes = (size_t)K * welem_bytes<WF>();
+
+    // This wave's columns: chunk wave + j * NW for j < RS_CPW (the host picks
+    // RS_CPW = ceil(nch / NW)).
+    int col[RS_CPW];
+    bool ok[RS_CPW];
+    XFrag<XT, EPL> xf[RS_CPW];
+#pragma unroll
+    for (int j = 0; j < RS_CPW; ++j) {
+        col[j] = (wave + j * NW) * CH + lane * EPL;
+        ok[j] = (wave + j * NW) < nch && col[j] < K;
+        if (ok[j]) xf[j].load(a.x, col[j]);
+    }
+
+    __shared__ float red[2][NW][NMAT];
+    u4_t wv[RS_CPW][NMAT];
+    uint16_t sv[RS_CPW][NMAT];
+    auto issue = [&](int row) {
+#pragma unroll
+        for (int j = 0; j < RS_CPW; ++j)
+            if (ok[j]) {
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) {
+                    const unsigned char* base = static_cast<const unsigned char*>(a.W[m]) + (size_t)row * row_bytes;
+                    wv[j][m] = ld_stream<WF>(base + (size_t)col[j] * welem_bytes<WF>());
+                    if (WF == MXD_W_Q8B32) sv[j][m] = a.S[m][(size_t)row * (K / 32) + col[j] / 32];
+                }
+            }
+    };
+
+    int row = blockIdx.x;
+    if (row < M) issue(row);
+    int buf = 0;
+    for (; row < M; row += gridDim.x) {
+        float acc[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) acc[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < RS_CPW; ++j)
+            if (ok[j]) {
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) {
+                    if constexpr (WF == MXD_W_Q8B32)
+                        acc[m] = fmaf(dot16q(wv[j][m], xf[j]), mxd::h2f(sv[j][m]), acc[m]);
+                    else
+                        acc[m] = dot16(wv[j][m], xf[j], acc[m]);
+                }
+            }
+        const int next = row + gridDim.x;
+        if (next < M) issue(next);  // the next row streams in while this one reduces
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) acc[m] = mxd::wave_sum(acc[m]);
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) red[buf][wave][m] = acc[m];
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float s[NMAT];
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) {
+                s[m] = red[buf][0][m];
+#pragma unroll
+                for (int w = 1; w < NW; ++w) s[m] += red[buf][w][m];
+            }
+            if constexpr (NMAT == 2) {
+                a.y[row] = (OP == MXD_ACT_SILU ? mxd::silu(s[0]) : mxd::gelu_tanh(s[0])) * s[1];
+            } else if constexpr (OP == MXD_EPI_ADD) {
+                a.y[row] += s[0];
+            } else if constexpr (OP == MXD_EPI_GELU_MUL) {
+                a.y[row] = mxd::gelu_tanh(s[0]) * a.aux[row];
+            } else {
+                a.y[row] = s[0];
+            }
+        }
+        buf ^= 1;
+    }
+}
+
+template <int WF, typename XT, int NMAT, int OP, int NW, int CPW>
+int launch_rows_k(const GemvArgs& a, int wg_per_cu, hipStream_t s) {
+    auto kern = gemv_rows_kernel<WF, XT, NMAT, OP, NW, CPW>;
+    // A persistent grid must fit on the GPU at once: cap by the occupancy the
+    // kernel's registers and LDS allow.
+    int fit = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&fit, kern, NW * 64, 0) != hipSuccess || fit < 1) fit = 1;
+    if (wg_per_cu > fit) wg_per_cu = fit;
+    int grid = 256 * wg_per_cu;
+    if (grid > a.M) grid = a.M;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), 0, s, a);
+    return mxd::check_launch("matvec");
+}
+
+template <int WF, typename XT, int NMAT, int OP>
+int launch_rows(const GemvArgs& a, int nw, int cpw, int wg_per_cu, hipStream_t s) {
+    if (nw == 4 && cpw == 1) return launch_rows_k<WF, XT, NMAT, OP, 4, 1>(a, wg_per_cu, s);
+    if (nw == 4 && cpw == 2) return launch_rows_k<WF, XT, NMAT, OP, 4, 2>(a, wg_per_cu, s);
+    if (nw == 4 && cpw == 4) return launch_rows_k<WF, XT, NMAT, OP, 4, 4>(a, wg_per_cu, s);
+    if (nw == 8 && cpw == 1) return launch_rows_k<WF, XT, NMAT, OP, 8, 1>(a, wg_per_cu, s);
+    if (nw == 8 && cpw == 2) return launch_rows_k<WF, XT, NMAT, OP, 8, 2>(a, wg_per_cu, s);
+    if (nw == 8 && cpw == 4) return launch_rows_k<WF, XT, NMAT, OP, 8, 4>(a, wg_per_cu, s);
+    if (nw == 16 && cpw == 1) return launch_rows_k<WF, XT, NMAT, OP, 16, 1>(a, wg_per_cu, s);
+    if (nw == 16 && cpw == 2) return launch_rows_k<WF, XT, NMAT, OP, 16, 2>(a, wg_per_cu, s);
+    if (nw == 16 && cpw == 4) return launch_rows_k<WF, XT, NMAT, OP, 16, 4>(a, wg_per_cu, s);
+    return mxd::fail(MXD_ERR_INVALID_ARG, "matvec: row streaming has no (waves %d, chunks/wave %d) variant", nw, cpw);
+}
+
 // Rows per workgroup and waves per workgroup for a shape, overridable through
 // the MV_NR / MV_NW tunables.
 void pick_tiling(int M, int nch, int& nr, int& nw) {
@@ -257,8 +391,22 @@ int launch_nw(const GemvArgs& a, int nw, hipStream_t s) {
 template <int WF, typename XT, int NMAT, int OP>
 int launch(const GemvArgs& a, hipStream_t s) {
     constexpr int CH = 64 * WT<WF>::EPL;
+    const int nch = (a.K + CH - 1) / CH;
+    // MV_ALGO: 0 = row-tiled workgroups (default), 1 = row streaming (while a
+    // row fits 16 waves x 4 chunks). Both sustain about the same HBM rate on
+    // the FFN shapes; the tiled kernel needs no persistent-grid sizing.
+    const int algo = mxd::tunable("MV_ALGO", 0);
+    if (algo == 1) {
+        MXD_REQUIRE(nch <= RS_MAX_CHUNKS, MXD_ERR_UNSUPPORTED, "matvec: row streaming needs K <= %d",
+                    RS_MAX_CHUNKS * CH);
+        const int nw = mxd::tunable("MV_RS_NW", nch <= 4 ? 4 : nch <= 8 ? 8 : 16);
+        int cpw = (nch + nw - 1) / nw;
+        cpw = cpw <= 1 ? 1 : cpw <= 2 ? 2 : 4;
+        const int wg_per_cu = mxd::tunable("MV_RS_WGCU", 32 / nw > 0 ? 32 / nw : 1);
+        return launch_rows<WF, XT, NMAT, OP>(a, nw, cpw, wg_per_cu, s);
+    }
     int nr, nw;
-    pick_tiling(a.M, (a.K + CH - 1) / CH, nr, nw);
+    pick_tiling(a.M, nch, nr, nw);
     switch (nr) {
         case 1: return launch_nw<WF, XT, NMAT, OP, 1>(a, nw, s);
         case 2: return launch_nw<WF, XT, NMAT, OP, 2>(a, nw, s);

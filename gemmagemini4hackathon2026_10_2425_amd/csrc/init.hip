@@ -33,7 +33,11 @@ __global__ void __launch_bounds__(256) fill_normal_kernel(void* dst, uint64_t n,
         const uint64_t h0 = mix64(key + 2 * i);
         const uint64_t h1 = mix64(key + 2 * i + 1);
         const int32_t c = sum16x4(h0) + sum16x4(h1) - 4 * 65535;
-        const float v = (float)c * k;
+        float v = (float)c * k;
+        // Keep the fp32 product: without this the compiler folds the multiply
+        // and the fp16 conversion into one mixed-precision FMA that rounds once,
+        // straight to fp16, which is not the value this generator defines.
+        asm volatile("" : "+v"(v));
         if (DT == MXD_F32)
             static_cast<float*>(dst)[i] = v;
         else

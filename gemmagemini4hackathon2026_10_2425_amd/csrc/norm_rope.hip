@@ -55,9 +55,23 @@ __global__ void __launch_bounds__(256) f32_to_f16_kernel(const float* __restrict
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = mxd::f2h_bits(src[i]);
 }
 
+// Offsets (in halfs) of position k (0..31) and dim d inside a 32-position cache
+// tile, in the MFMA operand order the attention kernel loads (the layouts are
+// spelled out in include/mxdecode.h).
+__device__ __forceinline__ int k_tile_offset(int k, int d, int hd) {
+    const int t = (k >> 2) & 1, col = ((k >> 3) << 2) | (k & 3);
+    const int c = d >> 5, g = (d >> 3) & 3, e = d & 7;
+    return ((t * (hd >> 5) + c) * 64 + g * 16 + col) * 8 + e;
+}
+
+__device__ __forceinline__ int v_tile_offset(int k, int d) {
+    const int dt = d >> 4, col = d & 15, g = k >> 3, j = k & 7;
+    return (dt * 64 + g * 16 + col) * 8 + j;
+}
+
 // One thread per rotation pair (i, i + hd/2) per head per row; heads run over
-// the q heads, then the kv heads (KL/kernels.metal:182-224). V goes to the
-// transposed cache [kvh][hd][max_ctx].
+// the q heads, then the kv heads (KL/kernels.metal:182-224). K and V go to
+// the tiled caches.
 __global__ void __launch_bounds__(256)
 rope_kv_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kcache, uint16_t* __restrict__ vcache,
                const float* __restrict__ inv_freq, int n_heads, int n_kv, int hd, int max_ctx, int pos0) {
@@ -81,13 +95,13 @@ rope_kv_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kcache, uint16_t*
         v[p + half_d] = rb;
     } else {
         const int kvh = h - n_heads;
-        const size_t kbase = ((size_t)kvh * max_ctx + pos) * hd;
-        kcache[kbase + p] = mxd::f2h_bits(ra);
-        kcache[kbase + p + half_d] = mxd::f2h_bits(rb);
+        const size_t tile = ((size_t)kvh * max_ctx + (pos & ~31)) * hd;
+        const int k = pos & 31;
+        kcache[tile + k_tile_offset(k, p, hd)] = mxd::f2h_bits(ra);
+        kcache[tile + k_tile_offset(k, p + half_d, hd)] = mxd::f2h_bits(rb);
         const float* vv = row + (n_heads + n_kv + kvh) * hd;
-        const size_t vbase = (size_t)kvh * hd * max_ctx + pos;
-        vcache[vbase + (size_t)p * max_ctx] = mxd::f2h_bits(vv[p]);
-        vcache[vbase + (size_t)(p + half_d) * max_ctx] = mxd::f2h_bits(vv[p + half_d]);
+        vcache[tile + v_tile_offset(k, p)] = mxd::f2h_bits(vv[p]);
+        vcache[tile + v_tile_offset(k, p + half_d)] = mxd::f2h_bits(vv[p + half_d]);
     }
 }
 
@@ -139,8 +153,10 @@ extern "C" int mxd_rope_kv(float* qkv, uint16_t* kcache, uint16_t* vcache, const
     MXD_REQUIRE(qkv && kcache && vcache && inv_freq, MXD_ERR_INVALID_ARG, "mxd_rope_kv: null pointer");
     MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && rows > 0 && pos0 >= 0, MXD_ERR_INVALID_ARG,
                 "mxd_rope_kv: n_heads=%d n_kv_heads=%d rows=%d pos0=%d", n_heads, n_kv_heads, rows, pos0);
-    MXD_REQUIRE(head_dim > 0 && head_dim % 2 == 0, MXD_ERR_UNSUPPORTED, "mxd_rope_kv: head_dim=%d must be even",
-                head_dim);
+    MXD_REQUIRE(head_dim > 0 && head_dim % 32 == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_rope_kv: head_dim=%d must be a multiple of 32 (cache tile layout)", head_dim);
+    MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_rope_kv: max_ctx=%d must be a positive multiple of 32", max_ctx);
     MXD_REQUIRE(pos0 + rows <= max_ctx, MXD_ERR_INVALID_ARG, "mxd_rope_kv: positions %d..%d exceed max_ctx %d", pos0,
                 pos0 + rows - 1, max_ctx);
     const int pairs = (n_heads + n_kv_heads) * (head_dim / 2);

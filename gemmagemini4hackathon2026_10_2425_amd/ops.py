@@ -25,6 +25,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -203,13 +204,59 @@ def inv_freq(head_dim: int, theta: float) -> list[float]:
     return [1.0 / theta ** (2 * i / head_dim) for i in range(head_dim // 2)]
 
 
+def tile_offsets(max_ctx: int, head_dim: int, which: str) -> np.ndarray:
+    """Element offset, within one kv head's cache, of (position p, dim d) for
+    the library's tiled K or V layout, as a [max_ctx, head_dim] int64 array."""
+    p = np.arange(max_ctx)[:, None]
+    d = np.arange(head_dim)[None, :]
+    k = p & 31
+    base = (p & ~31) * head_dim
+    if which == "k":
+        t, col = (k >> 2) & 1, ((k >> 3) << 2) | (k & 3)
+        c, g, e = d >> 5, (d >> 3) & 3, d & 7
+        return base + ((t * (head_dim >> 5) + c) * 64 + g * 16 + col) * 8 + e
+    if which == "v":
+        return base + ((d >> 4) * 64 + (k >> 3) * 16 + (d & 15)) * 8 + (k & 7)
+    raise ValueError(which)
+
+
+def to_tiles(rows, which: str):
+    """Cache rows [n_kv, max_ctx, hd] (the reference's layout) -> the library's
+    tiled K ("k") or V ("v") storage, same shape; numpy arrays or torch tensors."""
+    n_kv, ctx, hd = rows.shape
+    off = tile_offsets(ctx, hd, which).reshape(-1)
+    if isinstance(rows, torch.Tensor):
+        out = torch.empty_like(rows).reshape(n_kv, -1)
+        out[:, torch.from_numpy(off).to(rows.device)] = rows.reshape(n_kv, -1)
+        return out.reshape(n_kv, ctx, hd)
+    out = np.empty_like(rows).reshape(n_kv, -1)
+    out[:, off] = rows.reshape(n_kv, -1)
+    return out.reshape(n_kv, ctx, hd)
+
+
+def from_tiles(tiles, which: str):
+    """Inverse of to_tiles."""
+    n_kv, ctx, hd = tiles.shape
+    off = tile_offsets(ctx, hd, which).reshape(-1)
+    if isinstance(tiles, torch.Tensor):
+        return tiles.reshape(n_kv, -1)[:, torch.from_numpy(off).to(tiles.device)].reshape(n_kv, ctx, hd)
+    return tiles.reshape(n_kv, -1)[:, off].reshape(n_kv, ctx, hd)
+
+
+def _check_caches(kcache, vcache, fn: str):
+    n_kv, max_ctx, hd = kcache.shape
+    _need(max_ctx % 32 == 0, f"{fn}: max_ctx={max_ctx} must be a multiple of 32")
+    _need(tuple(vcache.shape) == (n_kv, max_ctx, hd), f"{fn}: kcache and vcache must both be [n_kv, max_ctx, hd]")
+    _need(kcache.dtype == torch.float16 and vcache.dtype == torch.float16, f"{fn}: fp16 caches")
+    return n_kv, max_ctx, hd
+
+
 def rope_kv(qkv, kcache, vcache, inv_freq_t, n_heads: int, n_kv_heads: int, pos0: int) -> None:
     """Rotate q in place and k, append k and v (fp16) to the caches at pos0 + row.
-    kcache [n_kv, max_ctx, hd]; vcache [n_kv, hd, max_ctx] (transposed)."""
+    kcache, vcache: [n_kv, max_ctx, hd] fp16 in the tiled layout (to_tiles)."""
     _on_gpu(qkv, kcache, vcache, inv_freq_t)
-    n_kv, max_ctx, hd = kcache.shape
-    _need(n_kv == n_kv_heads and tuple(vcache.shape) == (n_kv, hd, max_ctx), "rope_kv: cache shapes")
-    _need(kcache.dtype == torch.float16 and vcache.dtype == torch.float16, "rope_kv: fp16 caches")
+    n_kv, max_ctx, hd = _check_caches(kcache, vcache, "rope_kv")
+    _need(n_kv == n_kv_heads, "rope_kv: cache has a different number of kv heads")
     row_len = (n_heads + 2 * n_kv_heads) * hd
     _need(qkv.dtype == torch.float32 and qkv.numel() % row_len == 0, f"rope_kv: qkv rows of {row_len} floats")
     rows = qkv.numel() // row_len
@@ -221,17 +268,17 @@ def rope_kv(qkv, kcache, vcache, inv_freq_t, n_heads: int, n_kv_heads: int, pos0
 
 
 def attention_workspace(n_heads: int, n_kv_heads: int, head_dim: int, max_ctx: int, device="cuda") -> torch.Tensor:
+    """Zeroed once here; the kernel leaves its counters at zero after every call."""
     nbytes = query("mxd_attention_workspace_size", n_heads, n_kv_heads, head_dim, max_ctx)
-    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+    return torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=device)
 
 
 def attention(q, kcache, vcache, n_keys: int, n_heads: int, scale: float | None = None, out=None, workspace=None,
               pos_dev=None) -> torch.Tensor:
     """Single-query attention of q [n_heads*hd] over keys [0, n_keys) of the
-    caches (kcache [n_kv, max_ctx, hd], vcache [n_kv, hd, max_ctx])."""
+    tiled caches (kcache, vcache [n_kv, max_ctx, hd], see to_tiles)."""
     _on_gpu(q, kcache, vcache)
-    n_kv, max_ctx, hd = kcache.shape
-    _need(tuple(vcache.shape) == (n_kv, hd, max_ctx), "attention: vcache must be [n_kv, hd, max_ctx]")
+    n_kv, max_ctx, hd = _check_caches(kcache, vcache, "attention")
     _need(q.numel() == n_heads * hd and q.dtype == torch.float32, "attention: q float32 [n_heads*hd]")
     scale = 1.0 / math.sqrt(hd) if scale is None else scale
     out = torch.empty(n_heads * hd, dtype=torch.float32, device=q.device) if out is None else out

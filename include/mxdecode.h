@@ -19,10 +19,18 @@
  * Storage conventions (as in the reference, KL/kernels.metal:7-10):
  *   weights fp16 row-major [out_features][in_features]; activations and the
  *   residual stream fp32; KV cache fp16. fp16 values travel as uint16_t bits.
- * KV cache layout (this library's contract):
- *   K: [n_kv_heads][max_ctx][head_dim]   (the reference's layout)
- *   V: [n_kv_heads][head_dim][max_ctx]   (transposed, so the attention
- *      kernel's P·V matrix-core operand is a contiguous 16-byte load)
+ * KV cache layout (this library's contract). Each cache holds n_kv_heads *
+ * max_ctx * head_dim fp16 values (the size of the reference's
+ * [kv_head][max_ctx][head_dim], KL/kernels.metal:10), max_ctx % 32 == 0,
+ * cut into tiles of 32 positions; the tile of position p of kv head h starts
+ * at element (h * max_ctx + (p & ~31)) * head_dim. Inside a tile, with
+ * k = p & 31 and d the dim, values sit in the order the attention kernel's
+ * matrix-core operands are loaded, so every operand is one contiguous 1 KiB
+ * wave load:
+ *   K: ((t * head_dim/32 + c) * 64 + g * 16 + col) * 8 + e
+ *      t = (k >> 2) & 1, col = ((k >> 3) << 2) | (k & 3),
+ *      c = d >> 5, g = (d >> 3) & 3, e = d & 7
+ *   V: ((d >> 4) * 64 + (k >> 3) * 16 + (d & 15)) * 8 + (k & 7)
  */
 #ifndef MXDECODE_H
 #define MXDECODE_H
@@ -124,7 +132,8 @@ int mxd_f32_to_f16(const float* src, uint16_t* dst, size_t n, mxd_stream_t strea
 /* qkv rows are [q n_heads*hd | k n_kv_heads*hd | v n_kv_heads*hd] fp32 (row r at
  * position pos0 + r). Rotates q in place and k (HF rotate_half pairs (i, i+hd/2),
  * angle = pos * inv_freq[i] in fp32, accurate sin/cos), then appends fp16 k to
- * kcache and fp16 v to vcache at that position (layouts in the header comment).
+ * kcache and fp16 v to vcache at that position (tile layouts above).
+ * head_dim % 32 == 0.
  * Replaces rope_kv (KL/kernels.metal:182-224; host KL/main.swift:275-287). */
 int mxd_rope_kv(float* qkv, uint16_t* kcache, uint16_t* vcache, const float* inv_freq,
                 int n_heads, int n_kv_heads, int head_dim, int max_ctx, int pos0, int rows,
@@ -132,7 +141,7 @@ int mxd_rope_kv(float* qkv, uint16_t* kcache, uint16_t* vcache, const float* inv
 
 /* ---- single-query attention ---------------------------------------------- */
 
-/* Workspace bytes mxd_attention needs for this shape (0 is possible). */
+/* Workspace bytes mxd_attention needs for this shape (any max_ctx). */
 size_t mxd_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim, int max_ctx);
 
 /* out[h] = softmax(scale * q[h]·K[kvh][0..n_keys)) · V[kvh][0..n_keys) for

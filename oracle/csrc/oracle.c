@@ -146,7 +146,7 @@ typedef struct {
     uint16_t* embed;
     float* final_norm;
     oracle_layer* L;
-    uint16_t *k, *v; /* [layer][kvh][ctx][hd], [layer][kvh][hd][ctx] */
+    uint16_t *k, *v; /* both [layer][kvh][ctx][hd] */
     float *x, *xn, *qkv, *att, *h, *logits, *invf;
     double *tmp, *scores;
 } oracle_model;
@@ -254,7 +254,7 @@ int oracle_model_step(oracle_model* m, int32_t* tokens, int pos, int sample, flo
     for (int l = 0; l < c->n_layers; ++l) {
         const oracle_layer* L = &m->L[l];
         uint16_t* K = m->k + (size_t)l * NKV * C * HD;
-        uint16_t* V = m->v + (size_t)l * NKV * HD * C;
+        uint16_t* V = m->v + (size_t)l * NKV * C * HD;
         rmsnorm(m->x, L->attn_norm, m->xn, D, c->eps, c->plus_one);
         oracle_matvec_f16(L->wqkv, m->xn, t, qkvd, D);
         for (int i = 0; i < qkvd; ++i) m->qkv[i] = (float)t[i];
@@ -268,7 +268,7 @@ int oracle_model_step(oracle_model* m, int32_t* tokens, int pos, int sample, flo
                 const float* vv = m->qkv + (NH + NKV + kvh) * HD;
                 for (int i = 0; i < HD; ++i) {
                     K[((size_t)kvh * C + pos) * HD + i] = f2h((float)rot[i]);
-                    V[((size_t)kvh * HD + i) * C + pos] = f2h(vv[i]);
+                    V[((size_t)kvh * C + pos) * HD + i] = f2h(vv[i]);
                 }
             }
         }
@@ -287,12 +287,13 @@ int oracle_model_step(oracle_model* m, int32_t* tokens, int pos, int sample, flo
             }
             double sum = 0.0;
             for (int j = 0; j < n; ++j) { s[j] = exp(s[j] - mx); sum += s[j]; }
-            for (int i = 0; i < HD; ++i) {
-                double o = 0.0;
-                const uint16_t* vr = V + ((size_t)kvh * HD + i) * C;
-                for (int j = 0; j < n; ++j) o += s[j] * (double)h2f(vr[j]);
-                m->att[h * HD + i] = (float)(o / sum);
+            double o[512];
+            for (int i = 0; i < HD; ++i) o[i] = 0.0;
+            for (int j = 0; j < n; ++j) {
+                const uint16_t* vr = V + ((size_t)kvh * C + j) * HD;
+                for (int i = 0; i < HD; ++i) o[i] += s[j] * (double)h2f(vr[i]);
             }
+            for (int i = 0; i < HD; ++i) m->att[h * HD + i] = (float)(o[i] / sum);
         }
         oracle_matvec_f16(L->wo, m->att, t, D, qd);
         for (int i = 0; i < D; ++i) m->x[i] = m->x[i] + (float)t[i];

@@ -85,7 +85,7 @@ class OracleDecoder:
         self.cfg, self.w, self.max_ctx = cfg, weights, max_ctx
         kv_dt = np.float16 if fp16_kv else np.float64
         self.k = np.zeros((cfg.n_layers, cfg.n_kv_heads, max_ctx, cfg.head_dim), kv_dt)
-        self.v = np.zeros((cfg.n_layers, cfg.n_kv_heads, cfg.head_dim, max_ctx), kv_dt)
+        self.v = np.zeros((cfg.n_layers, cfg.n_kv_heads, max_ctx, cfg.head_dim), kv_dt)
         self.invf = ops.inv_freq(cfg.head_dim, cfg.rope_theta)
         self.tokens = np.zeros(max_ctx + 1, np.int32)
         self.fp16_kv = fp16_kv
@@ -99,7 +99,7 @@ class OracleDecoder:
         q = ops.rope(row[: c.n_heads * hd].reshape(c.n_heads, hd), pos, self.invf)
         k = ops.rope(row[c.n_heads * hd : (c.n_heads + c.n_kv_heads) * hd].reshape(c.n_kv_heads, hd), pos, self.invf)
         self.k[l][:, pos, :] = k
-        self.v[l][:, :, pos] = row[(c.n_heads + c.n_kv_heads) * hd :].reshape(c.n_kv_heads, hd)
+        self.v[l][:, pos, :] = row[(c.n_heads + c.n_kv_heads) * hd :].reshape(c.n_kv_heads, hd)
         return q.reshape(-1)
 
     def forward(self, pos: int) -> np.ndarray:

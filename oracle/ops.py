@@ -8,8 +8,9 @@ Every op computes in float64 from its (fp16 / fp32) inputs and returns float64;
 the caller decides where values are rounded (model.py rounds at the same points
 as the GPU: fp32 activations between ops, fp16 KV cache).
 
-KV cache layout (the library's contract): K [n_kv, max_ctx, hd],
-V [n_kv, hd, max_ctx] (transposed).
+KV caches are in the reference's layout, K and V both [n_kv, max_ctx, hd]
+(KL/kernels.metal:10); the GPU library's tiled V layout is a storage detail
+the tests convert.
 """
 
 from __future__ import annotations
@@ -103,7 +104,7 @@ def rope_kv(qkv_row: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, invf: n
             n_kv: int, pos: int) -> np.ndarray:
     """One qkv row [q NH*hd | k NKV*hd | v NKV*hd] at position pos: returns the
     rotated q (fp64) and appends fp16(rotated k) / fp16(v) to the caches
-    (KL/kernels.metal:189-224). kcache [n_kv, ctx, hd], vcache [n_kv, hd, ctx]."""
+    (KL/kernels.metal:189-224). kcache, vcache [n_kv, ctx, hd]."""
     hd = kcache.shape[2]
     row = np.asarray(qkv_row, dtype=F64)
     q = row[: n_heads * hd].reshape(n_heads, hd)
@@ -112,7 +113,7 @@ def rope_kv(qkv_row: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, invf: n
     qr = rope(q, pos, invf)
     kr = rope(k, pos, invf)
     kcache[:, pos, :] = kr.astype(np.float16)
-    vcache[:, :, pos] = v.astype(np.float16)
+    vcache[:, pos, :] = v.astype(np.float16)
     return qr.reshape(-1)
 
 
@@ -127,7 +128,7 @@ def attention(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, n_keys: int
     for h in range(n_heads):
         kvh = h // G
         K = kcache[kvh, :n_keys, :].astype(F64)
-        V = vcache[kvh, :, :n_keys].astype(F64).T
+        V = vcache[kvh, :n_keys, :].astype(F64)
         s = (K @ qh[h]) * scale
         p = np.exp(s - s.max())
         out[h] = (p @ V) / p.sum()

@@ -109,14 +109,21 @@ def test_matvec_f16_tunables(dev, rng):
     want = ref.matvec(W16, x)
     Wd, xd = torch.from_numpy(W16).to(dev), torch.from_numpy(x).to(dev)
     try:
+        _lib.set_tunable("MV_ALGO", 0)  # row-tiled workgroups
         for nr in (1, 2, 4, 8):
             for nw in (1, 2, 4, 8):
                 _lib.set_tunable("MV_NR", nr)
                 _lib.set_tunable("MV_NW", nw)
                 _close(ops.matvec_f16(Wd, xd).cpu().numpy(), want)
+        _lib.set_tunable("MV_ALGO", 1)  # row streaming
+        for nw in (4, 8, 16):
+            for wgcu in (1, 2, 3):
+                _lib.set_tunable("MV_RS_NW", nw)
+                _lib.set_tunable("MV_RS_WGCU", wgcu)
+                _close(ops.matvec_f16(Wd, xd).cpu().numpy(), want)
     finally:
-        _lib.set_tunable("MV_NR", 0)
-        _lib.set_tunable("MV_NW", 0)
+        for name in ("MV_NR", "MV_NW", "MV_ALGO", "MV_RS_NW", "MV_RS_WGCU"):
+            _lib.set_tunable(name, 0)
 
 
 def _quant(W):
@@ -218,33 +225,51 @@ def test_rope_kv(dev, rng, nh, nkv, hd, theta, pos):
     qkv = rng.standard_normal((nh + 2 * nkv) * hd, dtype=np.float32)
     invf = ref.inv_freq(hd, theta)
     kc = np.zeros((nkv, max_ctx, hd), np.float16)
-    vc = np.zeros((nkv, hd, max_ctx), np.float16)
+    vc = np.zeros((nkv, max_ctx, hd), np.float16)
     q_want = ref.rope_kv(qkv, kc, vc, invf, nh, nkv, pos)
     qkv_d = torch.from_numpy(qkv.copy()).to(dev)
     kd = torch.zeros((nkv, max_ctx, hd), dtype=torch.float16, device=dev)
-    vd = torch.zeros((nkv, hd, max_ctx), dtype=torch.float16, device=dev)
+    vd = torch.zeros((nkv, max_ctx, hd), dtype=torch.float16, device=dev)
     ops.rope_kv(qkv_d, kd, vd, torch.from_numpy(invf).to(dev), nh, nkv, pos)
     got = qkv_d.cpu().numpy()
     _close(got[: nh * hd], q_want, 1e-5)
-    # k: fp16 of the rotated value; allow a 1-ulp difference from sin/cos rounding
-    kg = kd.cpu().numpy()[:, pos, :].astype(np.float64)
+    # k: fp16 of the rotated value at the tiled address; allow 1 ulp from sin/cos rounding
+    tk = pos & 31
+    t, colk = (tk >> 2) & 1, ((tk >> 3) << 2) | (tk & 3)
+    d = np.arange(hd)
+    k_off = (pos & ~31) * hd + ((t * (hd // 32) + (d >> 5)) * 64 + ((d >> 3) & 3) * 16 + colk) * 8 + (d & 7)
+    kflat = kd.cpu().numpy().reshape(nkv, -1)
+    kg = kflat[:, k_off].astype(np.float64)
     kw = kc[:, pos, :].astype(np.float64)
     assert np.max(np.abs(kg - kw) / np.maximum(np.abs(kw), 6e-5)) <= 2 ** -10
-    # v: plain fp16 copy, bit exact
-    assert np.array_equal(vd.cpu().numpy()[:, :, pos].view(np.uint16), vc[:, :, pos].view(np.uint16))
-    assert np.count_nonzero(kd.cpu().numpy()) == np.count_nonzero(kc)
+    assert np.count_nonzero(kflat) == np.count_nonzero(kc)
+    # v: plain fp16 copy, bit exact, at the tiled address
+    v_off = (pos & ~31) * hd + ((d >> 4) * 64 + (tk >> 3) * 16 + (d & 15)) * 8 + (tk & 7)
+    flat = vd.cpu().numpy().reshape(nkv, -1)
+    assert np.array_equal(flat[:, v_off].view(np.uint16), vc[:, pos].view(np.uint16))
+    # the helper layout functions agree with the formula
+    assert np.array_equal(ops.tile_offsets(max_ctx, hd, "k")[pos], k_off)
+    assert np.array_equal(ops.tile_offsets(max_ctx, hd, "v")[pos], v_off)
+    assert np.count_nonzero(flat) == np.count_nonzero(vc)
 
 
 # ---------------------------------------------------------------- attention
 
 
 def _attn_case(rng, nh, nkv, hd, L, max_ctx):
+    """q, K and V (the reference's [n_kv, ctx, hd] layout) with L filled rows."""
     q = rng.standard_normal(nh * hd, dtype=np.float32)
     kc = np.zeros((nkv, max_ctx, hd), np.float16)
-    vc = np.zeros((nkv, hd, max_ctx), np.float16)
+    vc = np.zeros((nkv, max_ctx, hd), np.float16)
     kc[:, :L, :] = rng.standard_normal((nkv, L, hd), dtype=np.float32).astype(np.float16)
-    vc[:, :, :L] = rng.standard_normal((nkv, hd, L), dtype=np.float32).astype(np.float16)
+    vc[:, :L, :] = rng.standard_normal((nkv, L, hd), dtype=np.float32).astype(np.float16)
     return q, kc, vc
+
+
+def _gpu_attention(dev, q, kc, vc, L, nh, **kw):
+    ops = _ops()
+    return ops.attention(torch.from_numpy(q).to(dev), torch.from_numpy(ops.to_tiles(kc, "k")).to(dev),
+                         torch.from_numpy(ops.to_tiles(vc, "v")).to(dev), L, nh, **kw)
 
 
 @pytest.mark.parametrize("L", [1, 31, 32, 33, 127, 129, 512, 4096, 32768])
@@ -254,7 +279,7 @@ def test_attention_gqa_config(dev, rng, L):
     nh, nkv, hd = 32, 8, 128
     max_ctx = max(32, (L + 31) // 32 * 32)
     q, kc, vc = _attn_case(rng, nh, nkv, hd, L, max_ctx)
-    out = ops.attention(torch.from_numpy(q).to(dev), torch.from_numpy(kc).to(dev), torch.from_numpy(vc).to(dev), L, nh)
+    out = _gpu_attention(dev, q, kc, vc, L, nh)
     _close(out.cpu().numpy(), ref.attention(q, kc, vc, L, nh, 1 / math.sqrt(hd)), 1e-3)
 
 
@@ -264,7 +289,7 @@ def test_attention_shapes(dev, rng, nh, nkv, hd, L):
     ops = _ops()
     max_ctx = 1024
     q, kc, vc = _attn_case(rng, nh, nkv, hd, L, max_ctx)
-    out = ops.attention(torch.from_numpy(q).to(dev), torch.from_numpy(kc).to(dev), torch.from_numpy(vc).to(dev), L, nh)
+    out = _gpu_attention(dev, q, kc, vc, L, nh)
     _close(out.cpu().numpy(), ref.attention(q, kc, vc, L, nh, 1 / math.sqrt(hd)), 1e-3)
 
 
@@ -275,8 +300,8 @@ def test_attention_stale_cache_ignored(dev, rng):
     q, kc, vc = _attn_case(rng, nh, nkv, hd, L, max_ctx)
     kc_g, vc_g = kc.copy(), vc.copy()
     kc_g[:, L:, :] = np.float16(np.nan)
-    vc_g[:, :, L:] = np.float16(np.inf)
-    out = ops.attention(torch.from_numpy(q).to(dev), torch.from_numpy(kc_g).to(dev), torch.from_numpy(vc_g).to(dev), L, nh)
+    vc_g[:, L:, :] = np.float16(np.inf)
+    out = _gpu_attention(dev, q, kc_g, vc_g, L, nh)
     _close(out.cpu().numpy(), ref.attention(q, kc, vc, L, nh, 1 / math.sqrt(hd)), 1e-3)
 
 
@@ -285,7 +310,7 @@ def test_attention_device_position(dev, rng):
     ops = _ops()
     nh, nkv, hd, max_ctx = 32, 8, 128, 4096
     q, kc, vc = _attn_case(rng, nh, nkv, hd, 3000, max_ctx)
-    qd, kd, vd = (torch.from_numpy(a).to(dev) for a in (q, kc, vc))
+    qd, kd, vd = (torch.from_numpy(a).to(dev) for a in (q, ops.to_tiles(kc, "k"), ops.to_tiles(vc, "v")))
     for L in (1, 200, 2999):
         pos = torch.tensor([L - 1], dtype=torch.int32, device=dev)
         out = ops.attention(qd, kd, vd, 0, nh, pos_dev=pos)

@@ -198,15 +198,15 @@ def test_inv_freq_definition():
 def test_rope_kv_appends_fp16(rng):
     nh, nkv, hd, ctx = 4, 2, 128, 16
     kc = np.zeros((nkv, ctx, hd), np.float16)
-    vc = np.zeros((nkv, hd, ctx), np.float16)
+    vc = np.zeros((nkv, ctx, hd), np.float16)
     row = rng.standard_normal((nh + 2 * nkv) * hd).astype(np.float32)
     invf = ops.inv_freq(hd, 10000.0)
     q = ops.rope_kv(row, kc, vc, invf, nh, nkv, 5)
     assert np.allclose(q.reshape(nh, hd), ops.rope(row[: nh * hd].reshape(nh, hd), 5, invf))
     k_want = ops.rope(row[nh * hd : (nh + nkv) * hd].reshape(nkv, hd), 5, invf).astype(np.float16)
     assert np.array_equal(kc[:, 5, :], k_want)
-    assert np.array_equal(vc[:, :, 5], row[(nh + nkv) * hd :].reshape(nkv, hd).astype(np.float16))
-    assert np.count_nonzero(kc[:, :5]) == 0 and np.count_nonzero(vc[:, :, 6:]) == 0
+    assert np.array_equal(vc[:, 5, :], row[(nh + nkv) * hd :].reshape(nkv, hd).astype(np.float16))
+    assert np.count_nonzero(kc[:, :5]) == 0 and np.count_nonzero(vc[:, 6:]) == 0
 
 
 # ---------------------------------------------------------------- attention
@@ -215,7 +215,7 @@ def test_rope_kv_appends_fp16(rng):
 def _cache(rng, nkv, L, hd):
     K = rng.standard_normal((nkv, L, hd)).astype(np.float16)
     V = rng.standard_normal((nkv, L, hd)).astype(np.float16)
-    return K, np.ascontiguousarray(V.transpose(0, 2, 1)), V
+    return K, V, V
 
 
 def test_attention_matches_torch_sdpa(rng):
@@ -252,7 +252,7 @@ def test_attention_split_merge_identity(rng):
     K, Vt, _ = _cache(rng, nkv, L, hd)
     q = rng.standard_normal(nh * hd)
     s = (K[0].astype(np.float64) @ q.reshape(nh, hd).T).T * 0.2  # [nh, L]
-    V = Vt[0].astype(np.float64).T
+    V = Vt[0].astype(np.float64)
     parts = []
     for a, b in [(0, 30), (30, 64), (64, 96)]:
         m = s[:, a:b].max(axis=1, keepdims=True)
