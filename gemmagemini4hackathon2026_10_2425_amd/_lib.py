@@ -51,9 +51,37 @@ class MxdRuntimeError(MxdError, RuntimeError):
     pass
 
 
+class ModelConfig(ctypes.Structure):
+    """mxd_model_config (include/mxdecode.h)."""
+
+    _fields_ = [
+        ("n_layers", c_int), ("dim", c_int), ("n_heads", c_int), ("n_kv_heads", c_int), ("head_dim", c_int),
+        ("ffn_dim", c_int), ("vocab", c_int), ("rms_eps", c_float), ("rope_theta", c_float), ("act", c_int),
+        ("norm_plus_one", c_int), ("embed_scale_sqrt_dim", c_int),
+    ]
+
+
 P = c_void_p
+E = c_void_p  # mxd_engine*
 # name -> (restype, argtypes); must match include/mxdecode.h one for one.
 SIGNATURES: dict[str, tuple] = {
+    "mxd_engine_create": (c_int, [ctypes.POINTER(ModelConfig), c_int, ctypes.POINTER(c_void_p)]),
+    "mxd_engine_destroy": (c_int, [E]),
+    "mxd_engine_num_tensors": (c_int, [E]),
+    "mxd_engine_tensor": (c_int, [E, c_int, ctypes.POINTER(c_char_p), ctypes.POINTER(c_void_p),
+                                  ctypes.POINTER(c_size_t), ctypes.POINTER(c_int)]),
+    "mxd_engine_find_tensor": (c_int, [E, c_char_p]),
+    "mxd_engine_upload": (c_int, [E, c_int, P, c_size_t]),
+    "mxd_engine_download": (c_int, [E, c_int, P, c_size_t]),
+    "mxd_engine_init_random": (c_int, [E, c_uint64, c_float]),
+    "mxd_engine_weight_bytes": (c_size_t, [E]),
+    "mxd_engine_set_tokens": (c_int, [E, P, c_int, c_int]),
+    "mxd_engine_get_tokens": (c_int, [E, P, c_int, c_int]),
+    "mxd_engine_get_logits": (c_int, [E, P]),
+    "mxd_engine_step": (c_int, [E, c_int, c_int]),
+    "mxd_engine_prefill": (c_int, [E, c_int]),
+    "mxd_engine_decode": (c_int, [E, c_int, c_int]),
+    "mxd_engine_sync": (c_int, [E]),
     "mxd_last_error": (c_char_p, []),
     "mxd_abi_version": (c_int, []),
     "mxd_set_tunable": (c_int, [c_char_p, c_int]),

@@ -7,7 +7,7 @@
 // combines them, and the last workgroup to finish (ticket counter) writes the
 // token and clears both words, leaving the workspace zeroed for the next call
 // without a memset (safe inside a captured graph).
-#include "common.hpp"
+#include "internal.hpp"
 
 namespace {
 
@@ -34,7 +34,8 @@ __device__ __forceinline__ unsigned long long shfl_xor64(unsigned long long v, i
 }
 
 __global__ void __launch_bounds__(AM_THREADS)
-argmax_kernel(const float* __restrict__ logits, int32_t* __restrict__ tokens, int N, int out_idx, ArgmaxWs* ws) {
+argmax_kernel(const float* __restrict__ logits, int32_t* __restrict__ tokens, int N, int out_idx, int32_t* pos_dev,
+              int advance, ArgmaxWs* ws) {
     __shared__ unsigned long long wbest[AM_THREADS / 64];
     __shared__ bool last;
     unsigned long long best = 0;  // below every real key
@@ -55,7 +56,11 @@ argmax_kernel(const float* __restrict__ logits, int32_t* __restrict__ tokens, in
     if (last && threadIdx.x == 0) {
         __threadfence();
         const unsigned long long b = atomicMax(&ws->best, 0ull);
+        // With pos_dev (a replayed decode step) the token goes to tokens[pos + 1]
+        // and, with advance, the step position moves on by one.
+        if (pos_dev) out_idx = pos_dev[0] + 1;
         tokens[out_idx] = (int32_t)(~(uint32_t)(b & 0xFFFFFFFFull));
+        if (pos_dev && advance) pos_dev[0] = out_idx;
         atomicExch(&ws->best, 0ull);
         atomicExch(&ws->ticket, 0u);
     }
@@ -76,9 +81,18 @@ extern "C" int mxd_argmax(const float* logits, int32_t* tokens, int N, int out_i
                 "mxd_argmax: workspace of %zu bytes needed", sizeof(ArgmaxWs));
     MXD_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 7) == 0, MXD_ERR_UNSUPPORTED,
                 "mxd_argmax: workspace must be 8-byte aligned");
+    return mxd::argmax_dev(logits, tokens, N, out_idx, nullptr, false, workspace, mxd::as_stream(stream));
+}
+
+namespace mxd {
+
+int argmax_dev(const float* logits, int32_t* tokens, int N, int out_idx, int32_t* pos_dev, bool advance,
+               void* workspace, hipStream_t s) {
     int blocks = (N + AM_THREADS * AM_PER_THREAD - 1) / (AM_THREADS * AM_PER_THREAD);
     if (blocks > 1024) blocks = 1024;
-    hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(AM_THREADS), 0, mxd::as_stream(stream), logits, tokens, N,
-                       out_idx, static_cast<ArgmaxWs*>(workspace));
-    return mxd::check_launch("mxd_argmax");
+    hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(AM_THREADS), 0, s, logits, tokens, N, out_idx, pos_dev,
+                       advance ? 1 : 0, static_cast<ArgmaxWs*>(workspace));
+    return check_launch("argmax");
 }
+
+}  // namespace mxd

@@ -1,0 +1,396 @@
+// The decode engine: device-resident weights, activations, KV caches and token
+// buffer, and the one-token decode step composed from the library's kernels.
+//
+// Reference: Engine (KL/main.swift:152-347, KG/main.swift:394-457). Step order
+// follows encodeDecode (KL/main.swift:321-347) with the Gemma substitutions
+// (sqrt(D) embedding scale KG/main.swift:397, GeGLU, tied LM head
+// KG/main.swift:379-380, (1 + w) RMSNorm weights). The token of step t is
+// written by the GPU into tokens[t + 1] and read from there by step t + 1
+// (KL/kernels.metal:343 / :38), so a run of steps needs no host round trip.
+//
+// MI355X specifics: the engine owns one non-blocking HIP stream (default
+// priority). A decode run replays one captured hipGraph per token; inside it
+// every kernel reads the step position from a device counter that the final
+// argmax advances, so the same graph serves every position.
+#include "internal.hpp"
+
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace {
+
+struct TensorInfo {
+    std::string name;
+    size_t offset, bytes;
+    int dtype;  // MXD_F16 / MXD_F32
+    uint64_t id;
+};
+
+struct LayerPtrs {
+    float *attn_norm, *ffn_norm;
+    uint16_t *wqkv, *wo, *wgate, *wup, *wdown;
+    uint16_t *kc, *vc;
+};
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+#define HIP_OK(expr, what)                                                                         \
+    do {                                                                                           \
+        hipError_t e_ = (expr);                                                                    \
+        if (e_ != hipSuccess) return mxd::fail(MXD_ERR_HIP, "%s: %s", what, hipGetErrorString(e_)); \
+    } while (0)
+
+__global__ void set_int_kernel(int32_t* p, int v) { *p = v; }
+
+}  // namespace
+
+struct mxd_engine {
+    mxd_model_config c{};
+    int max_ctx = 0;
+    hipStream_t stream = nullptr;
+    std::vector<TensorInfo> tensors;
+    std::unordered_map<std::string, int> index;
+    char* wbase = nullptr;
+    size_t wbytes = 0;
+    char* abase = nullptr;
+    size_t abytes = 0;
+    std::vector<LayerPtrs> L;
+    uint16_t* embed = nullptr;
+    float* final_norm = nullptr;
+    float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
+    float* invf = nullptr;
+    int32_t *tokens = nullptr, *pos = nullptr;
+    void* attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+    void* am_ws = nullptr;
+    hipGraphExec_t graph = nullptr;
+
+    int qkv_dim() const { return (c.n_heads + 2 * c.n_kv_heads) * c.head_dim; }
+    int q_dim() const { return c.n_heads * c.head_dim; }
+};
+
+namespace {
+
+void add_tensor(mxd_engine* e, const std::string& name, size_t elems, int dtype, uint64_t id, size_t& off) {
+    const size_t bytes = elems * (dtype == MXD_F32 ? 4 : 2);
+    e->index[name] = (int)e->tensors.size();
+    e->tensors.push_back({name, off, bytes, dtype, id});
+    off += align256(bytes);
+}
+
+// Tensor ids of the synthetic-weight generator: embed 1, final_norm 2, and
+// 1000 + 16 * layer + {attn_norm 0, wqkv 1, wo 2, ffn_norm 3, wgate 4, wup 5,
+// wdown 6}; names follow the reference's weight file (KL/convert_weights.py:56-69).
+void plan_weights(mxd_engine* e) {
+    const mxd_model_config& c = e->c;
+    const size_t D = c.dim, F = c.ffn_dim;
+    size_t off = 0;
+    add_tensor(e, "embed", (size_t)c.vocab * D, MXD_F16, 1, off);
+    add_tensor(e, "final_norm", D, MXD_F32, 2, off);
+    for (int l = 0; l < c.n_layers; ++l) {
+        const std::string p = "l" + std::to_string(l) + ".";
+        const uint64_t base = 1000 + 16 * (uint64_t)l;
+        add_tensor(e, p + "attn_norm", D, MXD_F32, base + 0, off);
+        add_tensor(e, p + "wqkv", (size_t)e->qkv_dim() * D, MXD_F16, base + 1, off);
+        add_tensor(e, p + "wo", D * (size_t)e->q_dim(), MXD_F16, base + 2, off);
+        add_tensor(e, p + "ffn_norm", D, MXD_F32, base + 3, off);
+        add_tensor(e, p + "wgate", F * D, MXD_F16, base + 4, off);
+        add_tensor(e, p + "wup", F * D, MXD_F16, base + 5, off);
+        add_tensor(e, p + "wdown", D * F, MXD_F16, base + 6, off);
+    }
+    e->wbytes = off;
+}
+
+template <typename T>
+T* wptr(mxd_engine* e, const std::string& name) {
+    return reinterpret_cast<T*>(e->wbase + e->tensors[e->index.at(name)].offset);
+}
+
+void destroy(mxd_engine* e) {
+    if (!e) return;
+    if (e->graph) hipGraphExecDestroy(e->graph);
+    if (e->wbase) hipFree(e->wbase);
+    if (e->abase) hipFree(e->abase);
+    if (e->stream) hipStreamDestroy(e->stream);
+    delete e;
+}
+
+// One decode step: reads tokens[pos], appends K/V at pos, and with `sample`
+// writes argmax(logits) to tokens[pos + 1]. With pos_dev the position is read
+// on the device and advanced by the argmax (the captured form).
+int encode_step(mxd_engine* e, int pos, int32_t* pos_dev, bool sample) {
+    const mxd_model_config& c = e->c;
+    hipStream_t s = e->stream;
+    mxd_stream_t ms = reinterpret_cast<mxd_stream_t>(s);
+    const int D = c.dim, NH = c.n_heads, NKV = c.n_kv_heads, HD = c.head_dim, F = c.ffn_dim, V = c.vocab;
+    const float escale = c.embed_scale_sqrt_dim ? sqrtf((float)D) : 1.0f;
+    const float ascale = 1.0f / sqrtf((float)HD);
+    int rc;
+    if ((rc = mxd::embed_dev(e->embed, e->tokens, pos, pos_dev, 1, e->x, D, escale, V, s))) return rc;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const LayerPtrs& Lp = e->L[l];
+        if ((rc = mxd_rmsnorm(e->x, Lp.attn_norm, e->xn, MXD_F32, 1, D, c.rms_eps, c.norm_plus_one, ms))) return rc;
+        if ((rc = mxd_matvec_f16(Lp.wqkv, e->xn, MXD_F32, e->qkv, e->qkv_dim(), D, MXD_EPI_STORE, nullptr, ms))) return rc;
+        if ((rc = mxd::rope_kv_dev(e->qkv, Lp.kc, Lp.vc, e->invf, NH, NKV, HD, e->max_ctx, pos, 1, pos_dev, s))) return rc;
+        if ((rc = mxd_attention(e->qkv, Lp.kc, Lp.vc, e->att, NH, NKV, HD, e->max_ctx, pos + 1, pos_dev, ascale,
+                                e->attn_ws, e->attn_ws_bytes, ms)))
+            return rc;
+        if ((rc = mxd_matvec_f16(Lp.wo, e->att, MXD_F32, e->x, D, e->q_dim(), MXD_EPI_ADD, nullptr, ms))) return rc;
+        if ((rc = mxd_rmsnorm(e->x, Lp.ffn_norm, e->xn, MXD_F32, 1, D, c.rms_eps, c.norm_plus_one, ms))) return rc;
+        if ((rc = mxd_matvec_gate_up(MXD_W_F16, Lp.wgate, nullptr, Lp.wup, nullptr, e->xn, MXD_F32, e->h, F, D, c.act,
+                                     ms)))
+            return rc;
+        if ((rc = mxd_matvec_f16(Lp.wdown, e->h, MXD_F32, e->x, D, F, MXD_EPI_ADD, nullptr, ms))) return rc;
+    }
+    if (!sample) return MXD_OK;
+    if ((rc = mxd_rmsnorm(e->x, e->final_norm, e->xn, MXD_F32, 1, D, c.rms_eps, c.norm_plus_one, ms))) return rc;
+    if ((rc = mxd_matvec_f16(e->embed, e->xn, MXD_F32, e->logits, V, D, MXD_EPI_STORE, nullptr, ms))) return rc;
+    return mxd::argmax_dev(e->logits, e->tokens, V, pos + 1, pos_dev, pos_dev != nullptr, e->am_ws, s);
+}
+
+int check_config(const mxd_model_config* c, int max_ctx) {
+    MXD_REQUIRE(c, MXD_ERR_INVALID_ARG, "mxd_engine_create: null config");
+    MXD_REQUIRE(c->n_layers > 0 && c->dim > 0 && c->n_heads > 0 && c->n_kv_heads > 0 && c->head_dim > 0 &&
+                    c->ffn_dim > 0 && c->vocab > 0,
+                MXD_ERR_INVALID_ARG, "mxd_engine_create: sizes must be positive");
+    MXD_REQUIRE(c->n_heads % c->n_kv_heads == 0, MXD_ERR_INVALID_ARG, "mxd_engine_create: n_heads %% n_kv_heads != 0");
+    MXD_REQUIRE(c->head_dim == 128 || c->head_dim == 256, MXD_ERR_UNSUPPORTED, "mxd_engine_create: head_dim %d",
+                c->head_dim);
+    MXD_REQUIRE(c->dim % 8 == 0 && c->ffn_dim % 8 == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_engine_create: dim and ffn_dim must be multiples of 8");
+    MXD_REQUIRE(c->act == MXD_ACT_GELU_TANH || c->act == MXD_ACT_SILU, MXD_ERR_INVALID_ARG,
+                "mxd_engine_create: act %d", c->act);
+    MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_engine_create: max_ctx=%d must be a positive multiple of 32", max_ctx);
+    return MXD_OK;
+}
+
+}  // namespace
+
+extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_engine** out) {
+    MXD_REQUIRE(out, MXD_ERR_INVALID_ARG, "mxd_engine_create: null out");
+    *out = nullptr;
+    if (int rc = check_config(cfg, max_ctx)) return rc;
+    mxd_engine* e = new mxd_engine();
+    e->c = *cfg;
+    e->max_ctx = max_ctx;
+    const mxd_model_config& c = e->c;
+    plan_weights(e);
+
+    // Activations, caches and small buffers share one allocation.
+    const size_t D = c.dim, F = c.ffn_dim;
+    const size_t kv_bytes = (size_t)c.n_kv_heads * max_ctx * c.head_dim * 2;
+    e->attn_ws_bytes = mxd_attention_workspace_size(c.n_heads, c.n_kv_heads, c.head_dim, max_ctx);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += align256(bytes);
+        return o;
+    };
+    const size_t o_x = take(D * 4), o_xn = take(D * 4), o_qkv = take((size_t)e->qkv_dim() * 4);
+    const size_t o_att = take((size_t)e->q_dim() * 4), o_h = take(F * 4), o_logits = take((size_t)c.vocab * 4);
+    const size_t o_invf = take((size_t)c.head_dim / 2 * 4), o_tok = take(((size_t)max_ctx + 1) * 4), o_pos = take(4);
+    const size_t o_aws = take(e->attn_ws_bytes), o_am = take(mxd_argmax_workspace_size(c.vocab));
+    std::vector<size_t> o_kc(c.n_layers), o_vc(c.n_layers);
+    for (int l = 0; l < c.n_layers; ++l) {
+        o_kc[l] = take(kv_bytes);
+        o_vc[l] = take(kv_bytes);
+    }
+    e->abytes = off;
+
+    hipError_t he;
+    if ((he = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking)) != hipSuccess ||
+        (he = hipMalloc(&e->wbase, e->wbytes)) != hipSuccess || (he = hipMalloc(&e->abase, e->abytes)) != hipSuccess) {
+        destroy(e);
+        return mxd::fail(MXD_ERR_ALLOC, "mxd_engine_create: %s (weights %zu B, buffers %zu B)", hipGetErrorString(he),
+                         e->wbytes, off);
+    }
+    char* a = e->abase;
+    e->x = reinterpret_cast<float*>(a + o_x);
+    e->xn = reinterpret_cast<float*>(a + o_xn);
+    e->qkv = reinterpret_cast<float*>(a + o_qkv);
+    e->att = reinterpret_cast<float*>(a + o_att);
+    e->h = reinterpret_cast<float*>(a + o_h);
+    e->logits = reinterpret_cast<float*>(a + o_logits);
+    e->invf = reinterpret_cast<float*>(a + o_invf);
+    e->tokens = reinterpret_cast<int32_t*>(a + o_tok);
+    e->pos = reinterpret_cast<int32_t*>(a + o_pos);
+    e->attn_ws = a + o_aws;
+    e->am_ws = a + o_am;
+    e->embed = wptr<uint16_t>(e, "embed");
+    e->final_norm = wptr<float>(e, "final_norm");
+    e->L.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers; ++l) {
+        const std::string p = "l" + std::to_string(l) + ".";
+        LayerPtrs& Lp = e->L[l];
+        Lp.attn_norm = wptr<float>(e, p + "attn_norm");
+        Lp.ffn_norm = wptr<float>(e, p + "ffn_norm");
+        Lp.wqkv = wptr<uint16_t>(e, p + "wqkv");
+        Lp.wo = wptr<uint16_t>(e, p + "wo");
+        Lp.wgate = wptr<uint16_t>(e, p + "wgate");
+        Lp.wup = wptr<uint16_t>(e, p + "wup");
+        Lp.wdown = wptr<uint16_t>(e, p + "wdown");
+        Lp.kc = reinterpret_cast<uint16_t*>(a + o_kc[l]);
+        Lp.vc = reinterpret_cast<uint16_t*>(a + o_vc[l]);
+    }
+    // Zero everything once (caches, token buffer, argmax workspace), off any graph.
+    if ((he = hipMemsetAsync(e->abase, 0, e->abytes, e->stream)) != hipSuccess) {
+        destroy(e);
+        return mxd::fail(MXD_ERR_HIP, "mxd_engine_create: %s", hipGetErrorString(he));
+    }
+    // RoPE inverse frequencies in double, stored as float (KL/main.swift:92-94).
+    std::vector<float> invf(c.head_dim / 2);
+    for (int i = 0; i < c.head_dim / 2; ++i)
+        invf[i] = (float)(1.0 / pow((double)c.rope_theta, (double)(2 * i) / (double)c.head_dim));
+    he = hipMemcpyAsync(e->invf, invf.data(), invf.size() * 4, hipMemcpyHostToDevice, e->stream);
+    if (he == hipSuccess) he = hipStreamSynchronize(e->stream);
+    if (he != hipSuccess) {
+        destroy(e);
+        return mxd::fail(MXD_ERR_HIP, "mxd_engine_create: %s", hipGetErrorString(he));
+    }
+    *out = e;
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_destroy(mxd_engine* e) {
+    if (e) {
+        hipStreamSynchronize(e->stream);
+        destroy(e);
+    }
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_num_tensors(const mxd_engine* e) { return e ? (int)e->tensors.size() : 0; }
+
+extern "C" int mxd_engine_tensor(const mxd_engine* e, int i, const char** name, void** dev_ptr, size_t* bytes,
+                                 int* dtype) {
+    MXD_REQUIRE(e && i >= 0 && i < (int)e->tensors.size(), MXD_ERR_INVALID_ARG, "mxd_engine_tensor: index %d", i);
+    const TensorInfo& t = e->tensors[i];
+    if (name) *name = t.name.c_str();
+    if (dev_ptr) *dev_ptr = e->wbase + t.offset;
+    if (bytes) *bytes = t.bytes;
+    if (dtype) *dtype = t.dtype;
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_find_tensor(const mxd_engine* e, const char* name) {
+    if (!e || !name) return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_engine_find_tensor: null argument");
+    auto it = e->index.find(name);
+    if (it == e->index.end()) return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_engine_find_tensor: no tensor %s", name);
+    return it->second;
+}
+
+extern "C" int mxd_engine_init_random(mxd_engine* e, uint64_t seed, float stddev) {
+    MXD_REQUIRE(e, MXD_ERR_INVALID_ARG, "mxd_engine_init_random: null engine");
+    for (const TensorInfo& t : e->tensors) {
+        const uint64_t n = t.bytes / (t.dtype == MXD_F32 ? 4 : 2);
+        if (int rc = mxd_fill_normal(e->wbase + t.offset, t.dtype, n, seed, t.id, stddev,
+                                     reinterpret_cast<mxd_stream_t>(e->stream)))
+            return rc;
+    }
+    HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_init_random");
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_upload(mxd_engine* e, int i, const void* host, size_t bytes) {
+    MXD_REQUIRE(e && host && i >= 0 && i < (int)e->tensors.size(), MXD_ERR_INVALID_ARG,
+                "mxd_engine_upload: bad arguments");
+    MXD_REQUIRE(bytes == e->tensors[i].bytes, MXD_ERR_INVALID_ARG, "mxd_engine_upload: %s has %zu bytes, got %zu",
+                e->tensors[i].name.c_str(), e->tensors[i].bytes, bytes);
+    HIP_OK(hipMemcpyAsync(e->wbase + e->tensors[i].offset, host, bytes, hipMemcpyHostToDevice, e->stream),
+           "mxd_engine_upload");
+    HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_upload");
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_download(mxd_engine* e, int i, void* host, size_t bytes) {
+    MXD_REQUIRE(e && host && i >= 0 && i < (int)e->tensors.size(), MXD_ERR_INVALID_ARG,
+                "mxd_engine_download: bad arguments");
+    MXD_REQUIRE(bytes == e->tensors[i].bytes, MXD_ERR_INVALID_ARG, "mxd_engine_download: %s has %zu bytes, got %zu",
+                e->tensors[i].name.c_str(), e->tensors[i].bytes, bytes);
+    HIP_OK(hipMemcpyAsync(host, e->wbase + e->tensors[i].offset, bytes, hipMemcpyDeviceToHost, e->stream),
+           "mxd_engine_download");
+    HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_download");
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_set_tokens(mxd_engine* e, const int32_t* ids, int start, int n) {
+    MXD_REQUIRE(e && ids && start >= 0 && n >= 0 && start + n <= e->max_ctx + 1, MXD_ERR_INVALID_ARG,
+                "mxd_engine_set_tokens: range [%d, %d) outside [0, %d]", start, start + n, e ? e->max_ctx + 1 : 0);
+    for (int i = 0; i < n; ++i)
+        MXD_REQUIRE(ids[i] >= 0 && ids[i] < e->c.vocab, MXD_ERR_INVALID_ARG,
+                    "mxd_engine_set_tokens: token id %d out of range", ids[i]);
+    HIP_OK(hipMemcpyAsync(e->tokens + start, ids, (size_t)n * 4, hipMemcpyHostToDevice, e->stream),
+           "mxd_engine_set_tokens");
+    HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_set_tokens");
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_get_tokens(mxd_engine* e, int32_t* ids, int start, int n) {
+    MXD_REQUIRE(e && ids && start >= 0 && n >= 0 && start + n <= e->max_ctx + 1, MXD_ERR_INVALID_ARG,
+                "mxd_engine_get_tokens: bad range");
+    HIP_OK(hipMemcpyAsync(ids, e->tokens + start, (size_t)n * 4, hipMemcpyDeviceToHost, e->stream),
+           "mxd_engine_get_tokens");
+    HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_get_tokens");
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_get_logits(mxd_engine* e, float* host) {
+    MXD_REQUIRE(e && host, MXD_ERR_INVALID_ARG, "mxd_engine_get_logits: null argument");
+    HIP_OK(hipMemcpyAsync(host, e->logits, (size_t)e->c.vocab * 4, hipMemcpyDeviceToHost, e->stream),
+           "mxd_engine_get_logits");
+    HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_get_logits");
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_step(mxd_engine* e, int pos, int sample) {
+    MXD_REQUIRE(e, MXD_ERR_INVALID_ARG, "mxd_engine_step: null engine");
+    MXD_REQUIRE(pos >= 0 && pos < e->max_ctx, MXD_ERR_INVALID_ARG, "mxd_engine_step: pos %d outside [0, %d)", pos,
+                e->max_ctx);
+    return encode_step(e, pos, nullptr, sample != 0);
+}
+
+extern "C" int mxd_engine_prefill(mxd_engine* e, int n) {
+    MXD_REQUIRE(e && n >= 1 && n <= e->max_ctx, MXD_ERR_INVALID_ARG, "mxd_engine_prefill: n=%d", n);
+    for (int p = 0; p < n; ++p)
+        if (int rc = encode_step(e, p, nullptr, p == n - 1)) return rc;
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_decode(mxd_engine* e, int pos, int count) {
+    MXD_REQUIRE(e, MXD_ERR_INVALID_ARG, "mxd_engine_decode: null engine");
+    MXD_REQUIRE(pos >= 0 && count >= 0 && pos + count <= e->max_ctx, MXD_ERR_INVALID_ARG,
+                "mxd_engine_decode: steps %d..%d exceed max_ctx %d", pos, pos + count - 1, e->max_ctx);
+    if (count == 0) return MXD_OK;
+    if (!e->graph) {
+        hipGraph_t g = nullptr;
+        HIP_OK(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "mxd_engine_decode: begin capture");
+        const int rc = encode_step(e, 0, e->pos, true);
+        const hipError_t ce = hipStreamEndCapture(e->stream, &g);
+        if (rc) {
+            if (g) hipGraphDestroy(g);
+            return rc;
+        }
+        HIP_OK(ce, "mxd_engine_decode: end capture");
+        const hipError_t ie = hipGraphInstantiate(&e->graph, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        HIP_OK(ie, "mxd_engine_decode: instantiate");
+    }
+    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, e->stream, e->pos, pos);
+    if (int rc = mxd::check_launch("mxd_engine_decode")) return rc;
+    for (int i = 0; i < count; ++i) HIP_OK(hipGraphLaunch(e->graph, e->stream), "mxd_engine_decode: graph launch");
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_sync(mxd_engine* e) {
+    MXD_REQUIRE(e, MXD_ERR_INVALID_ARG, "mxd_engine_sync: null engine");
+    HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_sync");
+    return MXD_OK;
+}
+
+extern "C" size_t mxd_engine_weight_bytes(const mxd_engine* e) { return e ? e->wbytes : 0; }

@@ -1,0 +1,22 @@
+// Library-internal launchers shared between translation units (not part of
+// the C ABI). The *_dev variants read the step position from device memory
+// when pos_dev is not null, so a captured decode step replays at a moving
+// position without host involvement.
+#pragma once
+
+#include "common.hpp"
+
+namespace mxd {
+
+int embed_dev(const uint16_t* E, const int32_t* tokens, int pos, const int32_t* pos_dev, int rows, float* x, int D,
+              float scale, int vocab, hipStream_t s);
+
+int rope_kv_dev(float* qkv, uint16_t* kcache, uint16_t* vcache, const float* inv_freq, int n_heads, int n_kv, int hd,
+                int max_ctx, int pos0, int rows, const int32_t* pos_dev, hipStream_t s);
+
+// tokens[pos + 1] (or tokens[out_idx] without pos_dev) = argmax; with advance,
+// *pos_dev += 1 afterwards.
+int argmax_dev(const float* logits, int32_t* tokens, int N, int out_idx, int32_t* pos_dev, bool advance,
+               void* workspace, hipStream_t s);
+
+}  // namespace mxd

@@ -1,7 +1,7 @@
 // RMSNorm, embedding lookup, fp32->fp16 cast, and RoPE with KV-cache append.
 // These move kilobytes per decode step; they are latency-bound, so each is a
 // single small launch with no host synchronisation.
-#include "common.hpp"
+#include "internal.hpp"
 
 namespace {
 
@@ -40,11 +40,14 @@ rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w, YT* __r
 
 // x[r][i] = float(E[tokens[pos + r]][i]) * scale; ids outside [0, vocab) give
 // a zero row instead of an out-of-bounds read.
+// With pos_dev set, the position is read on the device (a replayed step).
 __global__ void __launch_bounds__(256) embed_kernel(const uint16_t* __restrict__ E, const int32_t* __restrict__ tokens,
-                                                    int pos, float* __restrict__ x, int D, float scale, int vocab) {
+                                                    int pos, const int32_t* __restrict__ pos_dev, float* __restrict__ x,
+                                                    int D, float scale, int vocab) {
     const int r = blockIdx.y;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= D) return;
+    if (pos_dev) pos = pos_dev[0];
     const int tok = tokens[pos + r];
     x[(size_t)r * D + i] = (tok >= 0 && tok < vocab) ? mxd::h2f(E[(size_t)tok * D + i]) * scale : 0.0f;
 }
@@ -74,12 +77,15 @@ __device__ __forceinline__ int v_tile_offset(int k, int d) {
 // the tiled caches.
 __global__ void __launch_bounds__(256)
 rope_kv_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kcache, uint16_t* __restrict__ vcache,
-               const float* __restrict__ inv_freq, int n_heads, int n_kv, int hd, int max_ctx, int pos0) {
+               const float* __restrict__ inv_freq, int n_heads, int n_kv, int hd, int max_ctx, int pos0,
+               const int32_t* __restrict__ pos_dev) {
     const int half_d = hd >> 1;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;  // pair index over heads
     const int t = blockIdx.y;                              // row
     const int h = i / half_d, p = i - h * half_d;
     if (h >= n_heads + n_kv) return;
+    if (pos_dev) pos0 = pos_dev[0];
+    if (pos0 < 0 || pos0 + t >= max_ctx) return;  // a device position past the cache writes nothing
     const int row_len = (n_heads + 2 * n_kv) * hd;
     const int pos = pos0 + t;
     float* row = qkv + (size_t)t * row_len;
@@ -106,6 +112,25 @@ rope_kv_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kcache, uint16_t*
 }
 
 }  // namespace
+
+namespace mxd {
+
+int embed_dev(const uint16_t* E, const int32_t* tokens, int pos, const int32_t* pos_dev, int rows, float* x, int D,
+              float scale, int vocab, hipStream_t s) {
+    hipLaunchKernelGGL(embed_kernel, dim3((D + 255) / 256, rows), dim3(256), 0, s, E, tokens, pos, pos_dev, x, D, scale,
+                       vocab);
+    return check_launch("embed");
+}
+
+int rope_kv_dev(float* qkv, uint16_t* kcache, uint16_t* vcache, const float* inv_freq, int n_heads, int n_kv, int hd,
+                int max_ctx, int pos0, int rows, const int32_t* pos_dev, hipStream_t s) {
+    const int pairs = (n_heads + n_kv) * (hd / 2);
+    hipLaunchKernelGGL(rope_kv_kernel, dim3((pairs + 255) / 256, rows), dim3(256), 0, s, qkv, kcache, vcache, inv_freq,
+                       n_heads, n_kv, hd, max_ctx, pos0, pos_dev);
+    return check_launch("rope_kv");
+}
+
+}  // namespace mxd
 
 extern "C" int mxd_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int rows, int D, float eps,
                            int plus_one, mxd_stream_t stream) {
@@ -134,9 +159,7 @@ extern "C" int mxd_embed(const uint16_t* E, const int32_t* tokens, int pos, int 
     MXD_REQUIRE(E && tokens && x, MXD_ERR_INVALID_ARG, "mxd_embed: null pointer");
     MXD_REQUIRE(pos >= 0 && rows > 0 && D > 0 && vocab > 0, MXD_ERR_INVALID_ARG,
                 "mxd_embed: pos=%d rows=%d D=%d vocab=%d", pos, rows, D, vocab);
-    hipLaunchKernelGGL(embed_kernel, dim3((D + 255) / 256, rows), dim3(256), 0, mxd::as_stream(stream), E, tokens, pos,
-                       x, D, scale, vocab);
-    return mxd::check_launch("mxd_embed");
+    return mxd::embed_dev(E, tokens, pos, nullptr, rows, x, D, scale, vocab, mxd::as_stream(stream));
 }
 
 extern "C" int mxd_f32_to_f16(const float* src, uint16_t* dst, size_t n, mxd_stream_t stream) {
@@ -160,7 +183,7 @@ extern "C" int mxd_rope_kv(float* qkv, uint16_t* kcache, uint16_t* vcache, const
     MXD_REQUIRE(pos0 + rows <= max_ctx, MXD_ERR_INVALID_ARG, "mxd_rope_kv: positions %d..%d exceed max_ctx %d", pos0,
                 pos0 + rows - 1, max_ctx);
     const int pairs = (n_heads + n_kv_heads) * (head_dim / 2);
-    hipLaunchKernelGGL(rope_kv_kernel, dim3((pairs + 255) / 256, rows), dim3(256), 0, mxd::as_stream(stream), qkv,
-                       kcache, vcache, inv_freq, n_heads, n_kv_heads, head_dim, max_ctx, pos0);
-    return mxd::check_launch("mxd_rope_kv");
+    (void)pairs;
+    return mxd::rope_kv_dev(qkv, kcache, vcache, inv_freq, n_heads, n_kv_heads, head_dim, max_ctx, pos0, rows, nullptr,
+                            mxd::as_stream(stream));
 }

@@ -170,6 +170,65 @@ size_t mxd_argmax_workspace_size(int N);
 int mxd_argmax(const float* logits, int32_t* tokens, int N, int out_idx, void* workspace,
                size_t ws_bytes, mxd_stream_t stream);
 
+/* ---- decode engine ---------------------------------------------------------- */
+
+/* Model shape. Replaces the reference's Config read from the weight file's JSON
+ * header (KL/main.swift:75-110). Weights fp16, norm weights fp32, tied LM head. */
+typedef struct mxd_model_config {
+    int n_layers, dim, n_heads, n_kv_heads, head_dim, ffn_dim, vocab;
+    float rms_eps, rope_theta;
+    int act;                  /* MXD_ACT_GELU_TANH (Gemma GeGLU) or MXD_ACT_SILU */
+    int norm_plus_one;        /* RMSNorm weight (1 + w) (Gemma) instead of w     */
+    int embed_scale_sqrt_dim; /* x = E[tok] * sqrt(dim) (KG/main.swift:397)      */
+} mxd_model_config;
+
+typedef struct mxd_engine mxd_engine;
+
+/* Allocates weights (one arena, tensors 256-byte aligned as in the reference's
+ * flat weight file, KL/convert_weights.py:71-89), activations, a token buffer of
+ * max_ctx + 1 ids and fp16 KV caches; owns one HIP stream. Replaces Engine.init
+ * (KL/main.swift:168-215). Weights start uninitialised. */
+int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_engine** out);
+int mxd_engine_destroy(mxd_engine* e);
+/* Weight tensors by index / name: "embed", "final_norm", "l<i>.attn_norm",
+ * "l<i>.wqkv" (rows q|k|v), "l<i>.wo", "l<i>.ffn_norm", "l<i>.wgate",
+ * "l<i>.wup", "l<i>.wdown" (names of KL/convert_weights.py:56-69). */
+int mxd_engine_num_tensors(const mxd_engine* e);
+int mxd_engine_tensor(const mxd_engine* e, int index, const char** name, void** dev_ptr, size_t* bytes,
+                      int* dtype);
+/* Index of a named tensor, or a negative error code. */
+int mxd_engine_find_tensor(const mxd_engine* e, const char* name);
+/* Copies one tensor's bytes from host memory (the weight-file loader's path),
+ * or back to host memory. Both synchronise the engine stream. */
+int mxd_engine_upload(mxd_engine* e, int index, const void* host, size_t bytes);
+int mxd_engine_download(mxd_engine* e, int index, void* host, size_t bytes);
+/* Fills every weight with mxd_fill_normal(seed, tensor id), ids: embed 1,
+ * final_norm 2, layer l: 1000 + 16 l + {attn_norm 0, wqkv 1, wo 2, ffn_norm 3,
+ * wgate 4, wup 5, wdown 6}. Synchronises. */
+int mxd_engine_init_random(mxd_engine* e, uint64_t seed, float stddev);
+size_t mxd_engine_weight_bytes(const mxd_engine* e);
+
+/* tokens[start .. start+n) from / to host memory (Engine.setTokens / token(at:),
+ * KL/main.swift:383-390). Both synchronise the engine stream. */
+int mxd_engine_set_tokens(mxd_engine* e, const int32_t* ids, int start, int n);
+int mxd_engine_get_tokens(mxd_engine* e, int32_t* ids, int start, int n);
+/* The fp32 logits of the last sampled step (--dump-logits, KL/main.swift:572-575). */
+int mxd_engine_get_logits(mxd_engine* e, float* host);
+
+/* One decode step at pos: reads tokens[pos], appends K/V at pos and, with
+ * sample, writes argmax to tokens[pos + 1]. Asynchronous. Replaces
+ * encodeDecode (KL/main.swift:321-347). */
+int mxd_engine_step(mxd_engine* e, int pos, int sample);
+/* Steps 0..n-1 through the decode path, sampling tokens[n] (the reference's
+ * token-by-token prefill, KL/main.swift:367-368). Asynchronous. */
+int mxd_engine_prefill(mxd_engine* e, int n);
+/* count greedy steps from pos (tokens[pos] must be set) with no host round trip:
+ * one captured graph replayed per step, the position kept on the device.
+ * Replaces Engine.decode(from:count:) (KL/main.swift:376-381). Asynchronous. */
+int mxd_engine_decode(mxd_engine* e, int pos, int count);
+/* Waits for the engine stream (waitUntilCompleted, KL/main.swift:379). */
+int mxd_engine_sync(mxd_engine* e);
+
 #ifdef __cplusplus
 }
 #endif
