@@ -14,8 +14,9 @@
 //    of one 16x16x32 fp16 MFMA, so each K and V element is loaded once for all
 //    of them: S^T[key][col] = K[key][:] . Q^T[:][col].
 //  * fp32 accuracy from fp16 matrix cores: q is split into hi = fp16(q) and
-//    lo = fp16(q - hi) in columns c and c + G (2G <= 16); the score of head c is
-//    the sum of the two columns (products of fp16 values are exact in fp32).
+//    lo = fp16(q - hi) in columns h and h + 8 (G <= 8); the score of head h is
+//    the sum of the two columns (products of fp16 values are exact in fp32),
+//    one DPP row rotation away.
 //    P is split the same way for the P.V product, so out keeps ~22 bits.
 //  * the S^T accumulator layout (lane = column, 4 rows per lane group) is
 //    already the A-operand layout of the P.V MFMA once the key rows are
@@ -107,13 +108,26 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
     const int col = lane & 15, g = lane >> 4;
     const int G = a.G;
 
-    // Q^T operand: column col holds hi (col < G) or lo (G <= col < 2G) parts of
-    // head (kvh*G + col % G); k-slot (g, j) of chunk c is dim 32c + 8g + j.
+    const uint16_t* kbase = a.k + (size_t)kvh * a.max_ctx * HD;
+    const uint16_t* vbase = a.v + (size_t)kvh * a.max_ctx * HD;
+
+    // Blocks are dealt round-robin: split s owns global blocks s, s+S, s+2S, ...
+    // and wave w takes every 4th of those, so at any moment the splits of a kv
+    // head stream one contiguous run of the cache. The first block's loads go
+    // out before the q operand is built so the two latencies overlap.
+    const int step = S * ATT_WAVES;
+    int b = split + S * wave;
+    KVBlock<HD> cur, nxt;
+    if (b < nblocks) load_block<HD>(cur, kbase, vbase, b * BLK, lane);
+
+    // Q^T operand: column h holds fp16(q) of head kvh*G + h and column h + 8
+    // the remainder fp16(q - hi) (h < G <= 8); the rest are zero. k-slot (g, j)
+    // of chunk c is dim 32c + 8g + j.
     h8_t qop[NC];
     {
-        const bool live = col < 2 * G;
-        const int head = kvh * G + (live ? col % G : 0);
-        const float* qh = a.q + (size_t)head * HD;
+        const int h = col & 7;
+        const bool live = h < G;
+        const float* qh = a.q + (size_t)(kvh * G + (live ? h : 0)) * HD;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const f4_t q0 = *reinterpret_cast<const f4_t*>(qh + 32 * c + 8 * g);
@@ -124,33 +138,27 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
                 const float v = qv[j] * a.qscale;
                 const _Float16 hi = (_Float16)v;
                 const _Float16 lo = (_Float16)(v - (float)hi);
-                qop[c][j] = !live ? (_Float16)0.0f : (col < G ? hi : lo);
+                qop[c][j] = !live ? (_Float16)0.0f : (col < 8 ? hi : lo);
             }
         }
     }
 
-    const uint16_t* kbase = a.k + (size_t)kvh * a.max_ctx * HD;
-    const uint16_t* vbase = a.v + (size_t)kvh * a.max_ctx * HD;
-
-    float m_run = -INFINITY, l_run = 0.0f;
+    // Running softmax state in the log2 domain. m_ref only moves when a block's
+    // maximum exceeds it by more than LAZY (p stays <= 2^LAZY), so the O rows
+    // are rescaled rarely instead of on every block.
+    constexpr float LAZY = 8.0f;
+    float m_ref = -INFINITY, l_run = 0.0f;
     f4_t o[ND];
 #pragma unroll
     for (int d = 0; d < ND; ++d) o[d] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Blocks are dealt round-robin: split s owns global blocks s, s+S, s+2S, ...
-    // and wave w takes every 4th of those, so at any moment the splits of a kv
-    // head stream one contiguous run of the cache.
-    const int step = S * ATT_WAVES;
-    int b = split + S * wave;
-    KVBlock<HD> cur, nxt;
-    if (b < nblocks) load_block<HD>(cur, kbase, vbase, b * BLK, lane);
     for (; b < nblocks; b += step) {
         const int key0 = b * BLK;
         if constexpr (PREFETCH) {
             if (b + step < nblocks) load_block<HD>(nxt, kbase, vbase, (b + step) * BLK, lane);
         }
 
-        // ---- scores (log2 domain)
+        // ---- scores (log2 domain): S^T tile t, row 4g+i = key key0 + 8g + 4t + i
         float s[8];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -161,48 +169,58 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
             for (int i = 0; i < 4; ++i) s[4 * t + i] = acc[i];
         }
         const bool tail = key0 + BLK > n;
+        const int nvalid = n - key0 - 8 * g;  // keys of this lane group still inside [0, n)
         float mb = -INFINITY;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            s[j] += __shfl_xor(s[j], G);  // hi + lo columns
-            if (tail && key0 + 8 * g + j >= n) s[j] = -INFINITY;
+            s[j] += mxd::dpp_f32<0x128>(s[j]);  // row_ror:8 = column h + 8: hi + lo
+            if (tail) s[j] = j < nvalid ? s[j] : -INFINITY;
             mb = fmaxf(mb, s[j]);
         }
         mb = fmaxf(mb, __shfl_xor(mb, 16));
         mb = fmaxf(mb, __shfl_xor(mb, 32));
-        const float m_new = fmaxf(m_run, mb);
-        const float alpha = exp2f(m_run - m_new);
-        m_run = m_new;
+        if (__any(mb > m_ref + LAZY)) {
+            const float m_new = fmaxf(m_ref, mb);
+            const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
+            m_ref = m_new;
+            l_run *= alpha;
+            float ar[4];  // O row 4g+i is head slot (4g+i) mod 8 (hi or lo part)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * g + i);
+#pragma unroll
+            for (int d = 0; d < ND; ++d)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[d][i] *= ar[i];
+        }
 
         h8_t pa;
         float psum = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float p = exp2f(s[j] - m_new);
+            const float p = __builtin_amdgcn_exp2f(s[j] - m_ref);
             psum += p;
             const _Float16 hi = (_Float16)p;
             const _Float16 lo = (_Float16)(p - (float)hi);
-            pa[j] = col < G ? hi : (col < 2 * G ? lo : (_Float16)0.0f);
+            pa[j] = (col & 7) >= G ? (_Float16)0.0f : (col < 8 ? hi : lo);
         }
-        l_run = l_run * alpha + psum;
+        l_run += psum;
 
-        // ---- rescale O rows (row 4g+i belongs to head slot 4g+i) and add P.V
-        float ar[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * g + i);
+        // ---- O += P.V; keys past n may hold stale bits (NaN/Inf): zero them.
         if (tail) {
+            u4_t keep;
 #pragma unroll
-            for (int d = 0; d < ND; ++d)
+            for (int w = 0; w < 4; ++w)
+                keep[w] = (2 * w < nvalid ? 0x0000FFFFu : 0u) | (2 * w + 1 < nvalid ? 0xFFFF0000u : 0u);
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (key0 + 8 * g + j >= n) cur.v[d][j] = (_Float16)0.0f;
+            for (int d = 0; d < ND; ++d) {
+                u4_t v;
+                __builtin_memcpy(&v, &cur.v[d], 16);
+                v &= keep;
+                __builtin_memcpy(&cur.v[d], &v, 16);
+            }
         }
 #pragma unroll
-        for (int d = 0; d < ND; ++d) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[d][i] *= ar[i];
-            o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, cur.v[d], o[d], 0, 0, 0);
-        }
+        for (int d = 0; d < ND; ++d) o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, cur.v[d], o[d], 0, 0, 0);
 
         if constexpr (PREFETCH) {
             cur = nxt;
@@ -215,28 +233,18 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
     if (lane < G) {
-        sm_m[wave][lane] = m_run;
+        sm_m[wave][lane] = m_ref;
         sm_l[wave][lane] = l_run;
     }
-    // Row h (hi) and row h + G (lo) of O -> head h.
+    // Row h (hi, lane group h/4) + row h + 8 (lo, lane group h/4 + 2) -> head h.
 #pragma unroll
     for (int d = 0; d < ND; ++d) {
         const int dim = 16 * d + col;
-        if (G >= 4) {
-            const int mask = G == 4 ? 16 : 32;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float other = __shfl_xor(o[d][i], mask);
-                const int h = 4 * g + i;
-                if (h < G) sm_o[wave][h][dim] = o[d][i] + other;
-            }
-        } else if (g == 0) {
-            if (G == 2) {
-                sm_o[wave][0][dim] = o[d][0] + o[d][2];
-                sm_o[wave][1][dim] = o[d][1] + o[d][3];
-            } else {
-                sm_o[wave][0][dim] = o[d][0] + o[d][1];
-            }
+        for (int i = 0; i < 4; ++i) {
+            const float other = __shfl_xor(o[d][i], 32);
+            const int h = 4 * g + i;
+            if (h < G) sm_o[wave][h][dim] = o[d][i] + other;
         }
     }
     __syncthreads();
@@ -324,8 +332,11 @@ __global__ void __launch_bounds__(HD) attn_merge_kernel(AttnArgs a) {
 // never more splits than 32-key blocks.
 int target_splits(int n_kv) { return min(MAX_SPLITS, (2 * 256 + n_kv - 1) / n_kv); }
 
+// Short contexts (up to 4 blocks per wave) take one split: the waves of one
+// workgroup cover every key and write the output without a merge launch.
 int splits_for(int max_keys, int n_kv) {
     const int nblocks = (max_keys + BLK - 1) / BLK;
+    if (nblocks <= 4 * ATT_WAVES) return 1;
     const int t = target_splits(n_kv);
     return nblocks < t ? nblocks : t;
 }
