@@ -90,6 +90,10 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_matvec_f16": (c_int, [P, P, c_int, P, c_int, c_int, c_int, P, P]),
     "mxd_matvec_q8b32": (c_int, [P, P, P, c_int, P, c_int, c_int, c_int, P, P]),
     "mxd_matvec_gate_up": (c_int, [c_int, P, P, P, P, P, c_int, P, c_int, c_int, c_int, P]),
+    "mxd_matvec_f16_rmsnorm": (c_int, [P, P, P, c_float, c_int, P, c_int, c_int, c_int, P, P]),
+    "mxd_gate_up_rmsnorm": (c_int, [P, P, P, P, c_float, c_int, P, c_int, c_int, c_int, P]),
+    "mxd_qkv_rope_kv": (c_int, [P, P, P, c_float, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P,
+                                P]),
     "mxd_rmsnorm": (c_int, [P, P, P, c_int, c_int, c_int, c_float, c_int, P]),
     "mxd_embed": (c_int, [P, P, c_int, c_int, P, c_int, c_float, c_int, P]),
     "mxd_f32_to_f16": (c_int, [P, P, c_size_t, P]),

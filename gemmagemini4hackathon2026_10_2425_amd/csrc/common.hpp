@@ -110,4 +110,19 @@ __device__ __forceinline__ float gelu_tanh(float x) {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
+// Offsets (in halfs) of position k (0..31) and dim d inside a 32-position KV
+// cache tile, in the MFMA operand order the attention kernel loads (layouts
+// spelled out in include/mxdecode.h). The tile of position p of kv head h
+// starts at (h * max_ctx + (p & ~31)) * hd.
+__device__ __forceinline__ int k_tile_offset(int k, int d, int hd) {
+    const int t = (k >> 2) & 1, col = ((k >> 3) << 2) | (k & 3);
+    const int c = d >> 5, g = (d >> 3) & 3, e = d & 7;
+    return ((t * (hd >> 5) + c) * 64 + g * 16 + col) * 8 + e;
+}
+
+__device__ __forceinline__ int v_tile_offset(int k, int d) {
+    const int dt = d >> 4, col = d & 15, g = k >> 3, j = k & 7;
+    return (dt * 64 + g * 16 + col) * 8 + j;
+}
+
 }  // namespace mxd

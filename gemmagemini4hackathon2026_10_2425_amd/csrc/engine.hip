@@ -132,24 +132,26 @@ int encode_step(mxd_engine* e, int pos, int32_t* pos_dev, bool sample) {
     const float ascale = 1.0f / sqrtf((float)HD);
     int rc;
     if ((rc = mxd::embed_dev(e->embed, e->tokens, pos, pos_dev, 1, e->x, D, escale, V, s))) return rc;
+    // Per layer, five launches: [rmsnorm + qkv + rope + append], attention,
+    // [wo + residual], [rmsnorm + gate_up], [down + residual].
     for (int l = 0; l < c.n_layers; ++l) {
         const LayerPtrs& Lp = e->L[l];
-        if ((rc = mxd_rmsnorm(e->x, Lp.attn_norm, e->xn, MXD_F32, 1, D, c.rms_eps, c.norm_plus_one, ms))) return rc;
-        if ((rc = mxd_matvec_f16(Lp.wqkv, e->xn, MXD_F32, e->qkv, e->qkv_dim(), D, MXD_EPI_STORE, nullptr, ms))) return rc;
-        if ((rc = mxd::rope_kv_dev(e->qkv, Lp.kc, Lp.vc, e->invf, NH, NKV, HD, e->max_ctx, pos, 1, pos_dev, s))) return rc;
+        if ((rc = mxd_qkv_rope_kv(Lp.wqkv, e->x, Lp.attn_norm, c.rms_eps, c.norm_plus_one, e->qkv, Lp.kc, Lp.vc,
+                                  e->invf, NH, NKV, HD, D, e->max_ctx, pos, pos_dev, ms)))
+            return rc;
         if ((rc = mxd_attention(e->qkv, Lp.kc, Lp.vc, e->att, NH, NKV, HD, e->max_ctx, pos + 1, pos_dev, ascale,
                                 e->attn_ws, e->attn_ws_bytes, ms)))
             return rc;
         if ((rc = mxd_matvec_f16(Lp.wo, e->att, MXD_F32, e->x, D, e->q_dim(), MXD_EPI_ADD, nullptr, ms))) return rc;
-        if ((rc = mxd_rmsnorm(e->x, Lp.ffn_norm, e->xn, MXD_F32, 1, D, c.rms_eps, c.norm_plus_one, ms))) return rc;
-        if ((rc = mxd_matvec_gate_up(MXD_W_F16, Lp.wgate, nullptr, Lp.wup, nullptr, e->xn, MXD_F32, e->h, F, D, c.act,
-                                     ms)))
+        if ((rc = mxd_gate_up_rmsnorm(Lp.wgate, Lp.wup, e->x, Lp.ffn_norm, c.rms_eps, c.norm_plus_one, e->h, F, D,
+                                      c.act, ms)))
             return rc;
         if ((rc = mxd_matvec_f16(Lp.wdown, e->h, MXD_F32, e->x, D, F, MXD_EPI_ADD, nullptr, ms))) return rc;
     }
     if (!sample) return MXD_OK;
-    if ((rc = mxd_rmsnorm(e->x, e->final_norm, e->xn, MXD_F32, 1, D, c.rms_eps, c.norm_plus_one, ms))) return rc;
-    if ((rc = mxd_matvec_f16(e->embed, e->xn, MXD_F32, e->logits, V, D, MXD_EPI_STORE, nullptr, ms))) return rc;
+    if ((rc = mxd_matvec_f16_rmsnorm(e->embed, e->x, e->final_norm, c.rms_eps, c.norm_plus_one, e->logits, V, D,
+                                     MXD_EPI_STORE, nullptr, ms)))
+        return rc;
     return mxd::argmax_dev(e->logits, e->tokens, V, pos + 1, pos_dev, pos_dev != nullptr, e->am_ws, s);
 }
 

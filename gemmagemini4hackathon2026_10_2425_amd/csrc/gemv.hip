@@ -30,7 +30,22 @@ struct GemvArgs {
     float* y;
     const float* aux;
     int M, K;
+    // Optional fused RMSNorm of x (fp32 x): x_k * rsqrt(mean(x^2) + eps) * w_k
+    // (or * (1 + w_k)), computed by every workgroup in a prologue.
+    const float* nw = nullptr;
+    float eps = 0.0f;
+    int plus_one = 0;
+    // RoPE + KV-append epilogue of the fused q|k|v projection (EPI_ROPE_KV).
+    const float* inv_freq = nullptr;
+    uint16_t* kcache = nullptr;
+    uint16_t* vcache = nullptr;
+    const int32_t* pos_dev = nullptr;
+    int pos = 0, n_heads = 0, n_kv = 0, hd = 0, max_ctx = 0;
 };
+
+// Internal epilogue: rows are rotated in (i, i + hd/2) pairs and q goes back
+// to y while k and v are appended to the tiled caches.
+constexpr int EPI_ROPE_KV = 16;
 
 // EPL activation values starting at column c.
 template <typename XT, int EPL> struct XFrag;
@@ -48,10 +63,23 @@ template <int EPL> struct XFrag<float, EPL> {
             v[4 * i + 3] = t.w;
         }
     }
+    // x_k * scale * w_k (or * (1 + w_k)): the fused RMSNorm, same operation
+    // order as the standalone kernel.
+    __device__ __forceinline__ void load_norm(const void* x, const float* w, int c, float scale, int plus_one) {
+        load(x, c);
+#pragma unroll
+        for (int i = 0; i < EPL / 4; ++i) {
+            const f4_t t = *reinterpret_cast<const f4_t*>(w + c + 4 * i);
+            const float wv[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[4 * i + j] = v[4 * i + j] * scale * (plus_one ? 1.0f + wv[j] : wv[j]);
+        }
+    }
 };
 
 template <int EPL> struct XFrag<_Float16, EPL> {
     h2_t v[EPL / 2];
+    __device__ __forceinline__ void load_norm(const void*, const float*, int, float, int) {}  // host rejects
     __device__ __forceinline__ void load(const void* x, int c) {
         const _Float16* p = static_cast<const _Float16*>(x) + c;
 #pragma unroll
@@ -128,7 +156,37 @@ __device__ __forceinline__ u4_t ld_stream(const unsigned char* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(p));
 }
 
-// NMAT == 1: OP is an MXD_EPI_*; NMAT == 2: OP is an MXD_ACT_* (gate, up).
+// For EPI_ROPE_KV the workgroup rows are "virtual": consecutive pairs map to
+// the rotation partners (i, i + hd/2) of one q or k head, so the epilogue holds
+// both; the v rows (after all q and k rows) map to themselves.
+__device__ __forceinline__ int rope_row(int v, const GemvArgs& a) {
+    const int half = a.hd >> 1;
+    if (v >= (a.n_heads + a.n_kv) * a.hd) return v;
+    const int p = v >> 1, head = p / half, i = p - head * half;
+    return head * a.hd + i + (v & 1) * half;
+}
+
+// rsqrt(mean(x^2) + eps) of the fp32 vector x[0..K), reduced by the whole
+// workgroup (K % 4 == 0).
+template <int NW>
+__device__ __forceinline__ float block_rms_scale(const float* x, int K, float eps) {
+    __shared__ float nred[NW];
+    float ss = 0.0f;
+    for (int k = threadIdx.x * 4; k < K; k += NW * 64 * 4) {
+        const f4_t t = *reinterpret_cast<const f4_t*>(x + k);
+        ss = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, ss))));
+    }
+    ss = mxd::wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) nred[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = nred[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) tot += nred[w];
+    return rsqrtf(tot / (float)K + eps);
+}
+
+// NMAT == 1: OP is an MXD_EPI_* or EPI_ROPE_KV; NMAT == 2: OP is an MXD_ACT_*
+// (gate, up).
 template <int WF, typename XT, int NMAT, int OP, int NR, int NW>
 __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
     constexpr int EPL = WT<WF>::EPL;
@@ -146,7 +204,8 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
-            const int row = min(r0 + r, M - 1);
+            int row = min(r0 + r, M - 1);
+            if constexpr (OP == EPI_ROPE_KV) row = rope_row(row, a);
             wrow[m][r] = static_cast<const unsigned char*>(a.W[m]) + (size_t)row * K * welem_bytes<WF>();
             srow[m][r] = WF == MXD_W_Q8B32 ? a.S[m] + (size_t)row * (K / 32) : nullptr;
         }
@@ -156,6 +215,8 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
         for (int r = 0; r < NR; ++r) acc[m][r] = 0.0f;
+
+    const float nscale = a.nw ? block_rms_scale<NW>(static_cast<const float*>(a.x), K, a.eps) : 1.0f;
 
     for (int c0 = wave; c0 < nch; c0 += NW * U) {
         u4_t wv[U][NMAT][NR];
@@ -168,7 +229,10 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
             const int col = c * CH + lane * EPL;
             ok[u] = (c < nch) && (col < K);
             if (ok[u]) {
-                xf[u].load(a.x, col);
+                if (a.nw)
+                    xf[u].load_norm(a.x, a.nw, col, nscale, a.plus_one);
+                else
+                    xf[u].load(a.x, col);
 #pragma unroll
                 for (int m = 0; m < NMAT; ++m)
 #pragma unroll
@@ -219,6 +283,49 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
             }
     }
 
+    if constexpr (OP == EPI_ROPE_KV) {
+        // Rotate each (i, i + hd/2) pair at pos (angle pos * inv_freq[i] in fp32,
+        // accurate sin/cos) and write q to y, k and v (fp16) to the tiled caches
+        // (KL/kernels.metal:199-222).
+        if (lane == 0) {
+            const int pos = a.pos_dev ? a.pos_dev[0] : a.pos;
+            const int half = a.hd >> 1, qk_rows = (a.n_heads + a.n_kv) * a.hd;
+            const bool in_cache = pos >= 0 && pos < a.max_ctx;
+            const int kpos = pos & 31;
+#pragma unroll
+            for (int r = 0; r < NR; r += 2) {
+                const int v = r0 + r;
+                if (v >= M) break;
+                if (v < qk_rows) {
+                    const int p = v >> 1, head = p / half, i = p - head * half;
+                    const float ang = (float)pos * a.inv_freq[i];
+                    float sn, cs;
+                    sincosf(ang, &sn, &cs);
+                    const float x0 = acc[0][r], x1 = acc[0][r + 1];
+                    const float ra = x0 * cs - x1 * sn;
+                    const float rb = x1 * cs + x0 * sn;
+                    if (head < a.n_heads) {
+                        a.y[head * a.hd + i] = ra;
+                        a.y[head * a.hd + i + half] = rb;
+                    } else if (in_cache) {
+                        const size_t tile = ((size_t)(head - a.n_heads) * a.max_ctx + (pos & ~31)) * a.hd;
+                        a.kcache[tile + mxd::k_tile_offset(kpos, i, a.hd)] = mxd::f2h_bits(ra);
+                        a.kcache[tile + mxd::k_tile_offset(kpos, i + half, a.hd)] = mxd::f2h_bits(rb);
+                    }
+                } else if (in_cache) {
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        if (v + e >= M) break;
+                        const int vr = v + e - qk_rows, kvh = vr / a.hd, d = vr - kvh * a.hd;
+                        const size_t tile = ((size_t)kvh * a.max_ctx + (pos & ~31)) * a.hd;
+                        a.vcache[tile + mxd::v_tile_offset(kpos, d)] = mxd::f2h_bits(acc[0][r + e]);
+                    }
+                }
+            }
+        }
+        return;
+    }
+
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < NR; ++r) {
@@ -265,11 +372,17 @@ __global__ void __launch_bounds__(NW * 64) gemv_rows_kernel(GemvArgs a) {
     int col[RS_CPW];
     bool ok[RS_CPW];
     XFrag<XT, EPL> xf[RS_CPW];
+    const float nscale = a.nw ? block_rms_scale<NW>(static_cast<const float*>(a.x), K, a.eps) : 1.0f;
 #pragma unroll
     for (int j = 0; j < RS_CPW; ++j) {
         col[j] = (wave + j * NW) * CH + lane * EPL;
         ok[j] = (wave + j * NW) < nch && col[j] < K;
-        if (ok[j]) xf[j].load(a.x, col[j]);
+        if (ok[j]) {
+            if (a.nw)
+                xf[j].load_norm(a.x, a.nw, col[j], nscale, a.plus_one);
+            else
+                xf[j].load(a.x, col[j]);
+        }
     }
 
     __shared__ float red[2][NW][NMAT];
@@ -501,4 +614,84 @@ extern "C" int mxd_matvec_gate_up(int w_format, const void* Wg, const uint16_t* 
         return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_matvec_gate_up: weight format %d", w_format);
     }
     return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_matvec_gate_up: x_dtype %d", x_dtype);
+}
+
+// ---------------------------------------------------------------------------
+// Fused decode-step operators: RMSNorm folded into the matvec's x loads, and
+// the q|k|v projection with RoPE + KV append in its epilogue. Each removes a
+// launch (and an activation round trip) per layer from the decode step.
+// ---------------------------------------------------------------------------
+
+namespace {
+
+int check_norm(const char* fn, const void* W, const float* x, const float* nw, const float* y, int M, int K) {
+    if (int rc = check_common(fn, W, x, y, M, K)) return rc;
+    MXD_REQUIRE(nw && aligned16(nw), MXD_ERR_INVALID_ARG, "%s: norm weight null or not 16-byte aligned", fn);
+    MXD_REQUIRE(K % 8 == 0, MXD_ERR_UNSUPPORTED, "%s: K=%d must be a multiple of 8", fn, K);
+    return MXD_OK;
+}
+
+}  // namespace
+
+extern "C" int mxd_matvec_f16_rmsnorm(const uint16_t* W, const float* x, const float* norm_w, float eps, int plus_one,
+                                      float* y, int M, int K, int epilogue, const float* aux, mxd_stream_t stream) {
+    if (int rc = check_norm("mxd_matvec_f16_rmsnorm", W, x, norm_w, y, M, K)) return rc;
+    MXD_REQUIRE(epilogue != MXD_EPI_GELU_MUL || aux, MXD_ERR_INVALID_ARG, "mxd_matvec_f16_rmsnorm: GELU_MUL needs aux");
+    GemvArgs a{{W, nullptr}, {nullptr, nullptr}, x, y, aux, M, K};
+    a.nw = norm_w;
+    a.eps = eps;
+    a.plus_one = plus_one;
+    return launch_epi<MXD_W_F16, float>(a, epilogue, mxd::as_stream(stream));
+}
+
+extern "C" int mxd_gate_up_rmsnorm(const uint16_t* Wg, const uint16_t* Wu, const float* x, const float* norm_w,
+                                   float eps, int plus_one, float* h, int F, int K, int act, mxd_stream_t stream) {
+    if (int rc = check_norm("mxd_gate_up_rmsnorm", Wg, x, norm_w, h, F, K)) return rc;
+    MXD_REQUIRE(Wu && aligned16(Wu), MXD_ERR_INVALID_ARG, "mxd_gate_up_rmsnorm: Wu null or not 16-byte aligned");
+    GemvArgs a{{Wg, Wu}, {nullptr, nullptr}, x, h, nullptr, F, K};
+    a.nw = norm_w;
+    a.eps = eps;
+    a.plus_one = plus_one;
+    return launch_act<MXD_W_F16, float>(a, act, mxd::as_stream(stream));
+}
+
+extern "C" int mxd_qkv_rope_kv(const uint16_t* Wqkv, const float* x, const float* norm_w, float eps, int plus_one,
+                               float* q, uint16_t* kcache, uint16_t* vcache, const float* inv_freq, int n_heads,
+                               int n_kv_heads, int head_dim, int K, int max_ctx, int pos, const int32_t* pos_dev,
+                               mxd_stream_t stream) {
+    const int M = (n_heads + 2 * n_kv_heads) * head_dim;
+    MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0, MXD_ERR_INVALID_ARG, "mxd_qkv_rope_kv: head counts");
+    MXD_REQUIRE(head_dim > 0 && head_dim % 32 == 0, MXD_ERR_UNSUPPORTED, "mxd_qkv_rope_kv: head_dim=%d", head_dim);
+    MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED, "mxd_qkv_rope_kv: max_ctx=%d", max_ctx);
+    MXD_REQUIRE(pos_dev || (pos >= 0 && pos < max_ctx), MXD_ERR_INVALID_ARG, "mxd_qkv_rope_kv: pos %d outside [0, %d)",
+                pos, max_ctx);
+    MXD_REQUIRE(kcache && vcache && inv_freq, MXD_ERR_INVALID_ARG, "mxd_qkv_rope_kv: null cache or inv_freq");
+    if (norm_w) {
+        if (int rc = check_norm("mxd_qkv_rope_kv", Wqkv, x, norm_w, q, M, K)) return rc;
+    } else {
+        if (int rc = check_common("mxd_qkv_rope_kv", Wqkv, x, q, M, K)) return rc;
+        MXD_REQUIRE(K % 8 == 0, MXD_ERR_UNSUPPORTED, "mxd_qkv_rope_kv: K=%d must be a multiple of 8", K);
+    }
+    GemvArgs a{{Wqkv, nullptr}, {nullptr, nullptr}, x, q, nullptr, M, K};
+    a.nw = norm_w;
+    a.eps = eps;
+    a.plus_one = plus_one;
+    a.inv_freq = inv_freq;
+    a.kcache = kcache;
+    a.vcache = vcache;
+    a.pos_dev = pos_dev;
+    a.pos = pos;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv_heads;
+    a.hd = head_dim;
+    a.max_ctx = max_ctx;
+    int nr, nw;
+    pick_tiling(M, (K + 511) / 512, nr, nw);
+    nr = nr < 2 ? 2 : (nr & ~1);  // rotation pairs stay inside one workgroup
+    hipStream_t s = mxd::as_stream(stream);
+    switch (nr) {
+        case 2: return launch_nw<MXD_W_F16, float, 1, EPI_ROPE_KV, 2>(a, nw, s);
+        case 4: return launch_nw<MXD_W_F16, float, 1, EPI_ROPE_KV, 4>(a, nw, s);
+        default: return launch_nw<MXD_W_F16, float, 1, EPI_ROPE_KV, 8>(a, nw, s);
+    }
 }

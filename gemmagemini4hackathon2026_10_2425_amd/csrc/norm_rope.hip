@@ -58,20 +58,6 @@ __global__ void __launch_bounds__(256) f32_to_f16_kernel(const float* __restrict
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = mxd::f2h_bits(src[i]);
 }
 
-// Offsets (in halfs) of position k (0..31) and dim d inside a 32-position cache
-// tile, in the MFMA operand order the attention kernel loads (the layouts are
-// spelled out in include/mxdecode.h).
-__device__ __forceinline__ int k_tile_offset(int k, int d, int hd) {
-    const int t = (k >> 2) & 1, col = ((k >> 3) << 2) | (k & 3);
-    const int c = d >> 5, g = (d >> 3) & 3, e = d & 7;
-    return ((t * (hd >> 5) + c) * 64 + g * 16 + col) * 8 + e;
-}
-
-__device__ __forceinline__ int v_tile_offset(int k, int d) {
-    const int dt = d >> 4, col = d & 15, g = k >> 3, j = k & 7;
-    return (dt * 64 + g * 16 + col) * 8 + j;
-}
-
 // One thread per rotation pair (i, i + hd/2) per head per row; heads run over
 // the q heads, then the kv heads (KL/kernels.metal:182-224). K and V go to
 // the tiled caches.
@@ -103,11 +89,11 @@ rope_kv_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kcache, uint16_t*
         const int kvh = h - n_heads;
         const size_t tile = ((size_t)kvh * max_ctx + (pos & ~31)) * hd;
         const int k = pos & 31;
-        kcache[tile + k_tile_offset(k, p, hd)] = mxd::f2h_bits(ra);
-        kcache[tile + k_tile_offset(k, p + half_d, hd)] = mxd::f2h_bits(rb);
+        kcache[tile + mxd::k_tile_offset(k, p, hd)] = mxd::f2h_bits(ra);
+        kcache[tile + mxd::k_tile_offset(k, p + half_d, hd)] = mxd::f2h_bits(rb);
         const float* vv = row + (n_heads + n_kv + kvh) * hd;
-        vcache[tile + v_tile_offset(k, p)] = mxd::f2h_bits(vv[p]);
-        vcache[tile + v_tile_offset(k, p + half_d)] = mxd::f2h_bits(vv[p + half_d]);
+        vcache[tile + mxd::v_tile_offset(k, p)] = mxd::f2h_bits(vv[p]);
+        vcache[tile + mxd::v_tile_offset(k, p + half_d)] = mxd::f2h_bits(vv[p + half_d]);
     }
 }
 

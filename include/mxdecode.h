@@ -108,6 +108,28 @@ int mxd_matvec_gate_up(int w_format, const void* Wg, const uint16_t* sg, const v
                        const uint16_t* su, const void* x, int x_dtype, float* h, int F, int K,
                        int act, mxd_stream_t stream);
 
+/* ---- fused decode-step operators ------------------------------------------- */
+
+/* y (op)= W · rmsnorm(x): the RMSNorm (KL/kernels.metal:71-96, weight w or
+ * 1 + w) folded into the matvec's activation loads; W fp16 [M][K], x and y fp32.
+ * Fuses the reference's rmsnorm_f32 + matvec_f16 pair (KL/main.swift:333-334). */
+int mxd_matvec_f16_rmsnorm(const uint16_t* W, const float* x, const float* norm_w, float eps, int plus_one,
+                           float* y, int M, int K, int epilogue, const float* aux, mxd_stream_t stream);
+
+/* h = act(Wg · rmsnorm(x)) * (Wu · rmsnorm(x)); fuses rmsnorm_f32 +
+ * matvec_gate_up_* (KL/main.swift:338-339, KG/kernels.metal:205-234). */
+int mxd_gate_up_rmsnorm(const uint16_t* Wg, const uint16_t* Wu, const float* x, const float* norm_w, float eps,
+                        int plus_one, float* h, int F, int K, int act, mxd_stream_t stream);
+
+/* [q | k | v] = Wqkv · rmsnorm(x) (norm_w NULL: no norm), then RoPE on q and k
+ * at pos and the K/V append, in the projection's epilogue: q (rotated, fp32,
+ * n_heads*head_dim) goes to `q`, k and v (fp16) to the tiled caches. Fuses
+ * rmsnorm_f32 + matvec_f16(wqkv) + rope_kv (KL/main.swift:333-335). With pos_dev
+ * the position is read on the device. head_dim % 32 == 0, max_ctx % 32 == 0. */
+int mxd_qkv_rope_kv(const uint16_t* Wqkv, const float* x, const float* norm_w, float eps, int plus_one, float* q,
+                    uint16_t* kcache, uint16_t* vcache, const float* inv_freq, int n_heads, int n_kv_heads,
+                    int head_dim, int K, int max_ctx, int pos, const int32_t* pos_dev, mxd_stream_t stream);
+
 /* ---- normalisation, embedding, casts ------------------------------------ */
 
 /* y[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * (plus_one ? 1 + w : w), rows x D,
