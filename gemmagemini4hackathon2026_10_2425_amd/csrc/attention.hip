@@ -277,68 +277,104 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
 }
 
 // out[h] = sum_s 2^(M_s - M) O_s / sum_s 2^(M_s - M) L_s over the active
-// splits (log-sum-exp rule). One workgroup per query head: the (M_s, L_s) pairs
-// go through LDS first, then every thread sums its dim over the splits with
-// eight independent loads in flight.
+// splits (log-sum-exp rule). One workgroup of MG * HD threads per query head:
+// thread (grp, dim) sums dim over splits grp, grp + MG, ...; its first PRE
+// partials are loaded before the (M_s, L_s) pass so the two latencies overlap,
+// which makes the common case (up to MG * PRE = 64 splits) one round trip.
+// The groups are combined in LDS in a fixed order (deterministic).
+constexpr int MG = 4;
+constexpr int PRE = 16;
+
 template <int HD>
-__global__ void __launch_bounds__(HD) attn_merge_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(MG * HD) attn_merge_kernel(AttnArgs a) {
+    constexpr int NT = MG * HD;
     __shared__ float sw[MAX_SPLITS];
     __shared__ float sl[MAX_SPLITS];
-    __shared__ float red[HD / 64][2];
+    __shared__ float red[2][NT / 64];
+    __shared__ float part[MG - 1][HD];
     const int n = n_keys_of(a);
     const int n_active = min(a.n_splits, (n + BLK - 1) / BLK);
     if (n_active <= 1) return;
     const int head = blockIdx.x, tid = threadIdx.x;
+    const int grp = tid / HD, dim = tid - grp * HD;
+    const float* po = a.ws_o + (size_t)head * HD + dim;
+    const size_t stride = (size_t)a.n_heads * HD;
+
+    float pre[PRE];
+#pragma unroll
+    for (int u = 0; u < PRE; ++u) {
+        const int sp = grp + MG * u;
+        pre[u] = sp < n_active ? po[(size_t)sp * stride] : 0.0f;
+    }
     float mloc = -INFINITY;
-    for (int sp = tid; sp < n_active; sp += HD) {
+    for (int sp = tid; sp < n_active; sp += NT) {
         const float m = a.ws_ml[((size_t)sp * a.n_heads + head) * 2];
         sw[sp] = m;
         sl[sp] = a.ws_ml[((size_t)sp * a.n_heads + head) * 2 + 1];
         mloc = fmaxf(mloc, m);
     }
     mloc = mxd::wave_max(mloc);
-    if ((tid & 63) == 0) red[tid >> 6][0] = mloc;
+    if ((tid & 63) == 0) red[0][tid >> 6] = mloc;
     __syncthreads();
     float M = red[0][0];
 #pragma unroll
-    for (int w = 1; w < HD / 64; ++w) M = fmaxf(M, red[w][0]);
+    for (int w = 1; w < NT / 64; ++w) M = fmaxf(M, red[0][w]);
     float lloc = 0.0f;
-    for (int sp = tid; sp < n_active; sp += HD) {
+    for (int sp = tid; sp < n_active; sp += NT) {
         const float f = exp2f(sw[sp] - M);
         sw[sp] = f;
         lloc += f * sl[sp];
     }
     lloc = mxd::wave_sum(lloc);
-    if ((tid & 63) == 0) red[tid >> 6][1] = lloc;
+    if ((tid & 63) == 0) red[1][tid >> 6] = lloc;
     __syncthreads();
     float L = 0.0f;
 #pragma unroll
-    for (int w = 0; w < HD / 64; ++w) L += red[w][1];
+    for (int w = 0; w < NT / 64; ++w) L += red[1][w];
 
-    const float* po = a.ws_o + (size_t)head * HD + tid;
-    const size_t stride = (size_t)a.n_heads * HD;
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    int sp = 0;
-    for (; sp + 8 <= n_active; sp += 8) {
+    float acc = 0.0f;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) acc[u] += sw[sp + u] * po[(size_t)(sp + u) * stride];
+    for (int u = 0; u < PRE; ++u) {
+        const int sp = grp + MG * u;
+        if (sp < n_active) acc += sw[sp] * pre[u];
     }
-    for (; sp < n_active; ++sp) acc[0] += sw[sp] * po[(size_t)sp * stride];
-    const float tot = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
-    a.out[(size_t)head * HD + tid] = tot / L;
+    // More than MG * PRE splits (long contexts over few kv heads): the rest,
+    // four loads in flight at a time.
+    int sp = grp + MG * PRE;
+    for (; sp + 3 * MG < n_active; sp += 4 * MG) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = po[(size_t)(sp + MG * u) * stride];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc += sw[sp + MG * u] * v[u];
+    }
+    for (; sp < n_active; sp += MG) acc += sw[sp] * po[(size_t)sp * stride];
+    if (grp > 0) part[grp - 1][dim] = acc;
+    __syncthreads();
+    if (grp == 0) {
+        float tot = acc;
+#pragma unroll
+        for (int g2 = 0; g2 < MG - 1; ++g2) tot += part[g2][dim];
+        a.out[(size_t)head * HD + dim] = tot / L;
+    }
 }
 
-// Splits per kv head: about two workgroups per CU over the whole grid, and
-// never more splits than 32-key blocks.
-int target_splits(int n_kv) { return min(MAX_SPLITS, (2 * 256 + n_kv - 1) / n_kv); }
+// Splits per kv head: about ATT_WGCU (default 2) workgroups per CU over the
+// whole grid, and never more splits than 32-key blocks.
+int target_splits(int n_kv) {
+    const int per_cu = max(1, min(16, mxd::tunable("ATT_WGCU", 2)));
+    return min(MAX_SPLITS, (per_cu * 256 + n_kv - 1) / n_kv);
+}
 
-// Short contexts (up to 4 blocks per wave) take one split: the waves of one
-// workgroup cover every key and write the output without a merge launch.
+// Up to 4 blocks per wave take one split, which writes the output without a
+// merge launch (measured: a second launch costs more than the serial blocks
+// it saves). Longer contexts take enough splits that every wave has at most
+// one block, capped by the occupancy target.
 int splits_for(int max_keys, int n_kv) {
     const int nblocks = (max_keys + BLK - 1) / BLK;
     if (nblocks <= 4 * ATT_WAVES) return 1;
-    const int t = target_splits(n_kv);
-    return nblocks < t ? nblocks : t;
+    const int one_per_wave = (nblocks + ATT_WAVES - 1) / ATT_WAVES;
+    return max(1, min(one_per_wave, target_splits(n_kv)));
 }
 
 }  // namespace
@@ -397,10 +433,10 @@ extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint1
     const dim3 grid(n_splits, n_kv_heads);
     if (head_dim == 128) {
         hipLaunchKernelGGL(attn_split_kernel<128>, grid, dim3(ATT_THREADS), 0, s, a);
-        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(n_heads), dim3(128), 0, s, a);
+        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(n_heads), dim3(MG * 128), 0, s, a);
     } else {
         hipLaunchKernelGGL(attn_split_kernel<256>, grid, dim3(ATT_THREADS), 0, s, a);
-        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(n_heads), dim3(256), 0, s, a);
+        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(n_heads), dim3(MG * 256), 0, s, a);
     }
     return mxd::check_launch("mxd_attention");
 }

@@ -216,8 +216,9 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int r = 0; r < NR; ++r) acc[m][r] = 0.0f;
 
-    const float nscale = a.nw ? block_rms_scale<NW>(static_cast<const float*>(a.x), K, a.eps) : 1.0f;
-
+    // Fused RMSNorm: the loop accumulates w . (x * w_norm) and the row sums are
+    // scaled by rsqrt(mean(x^2) + eps) at the end, so the norm's reduction runs
+    // after the weight stream instead of delaying its first loads.
     for (int c0 = wave; c0 < nch; c0 += NW * U) {
         u4_t wv[U][NMAT][NR];
         uint16_t sv[U][NMAT][NR];
@@ -230,7 +231,7 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
             ok[u] = (c < nch) && (col < K);
             if (ok[u]) {
                 if (a.nw)
-                    xf[u].load_norm(a.x, a.nw, col, nscale, a.plus_one);
+                    xf[u].load_norm(a.x, a.nw, col, 1.0f, a.plus_one);
                 else
                     xf[u].load(a.x, col);
 #pragma unroll
@@ -257,6 +258,7 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
         }
     }
 
+    const float nscale = a.nw ? block_rms_scale<NW>(static_cast<const float*>(a.x), K, a.eps) : 1.0f;
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
@@ -281,6 +283,12 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
                 for (int w = 1; w < NW; ++w) s += red[w][m][r];
                 acc[m][r] = s;
             }
+    }
+    if (a.nw) {
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int r = 0; r < NR; ++r) acc[m][r] *= nscale;
     }
 
     if constexpr (OP == EPI_ROPE_KV) {
@@ -478,15 +486,157 @@ int launch_rows(const GemvArgs& a, int nw, int cpw, int wg_per_cu, hipStream_t s
     return mxd::fail(MXD_ERR_INVALID_ARG, "matvec: row streaming has no (waves %d, chunks/wave %d) variant", nw, cpw);
 }
 
+// ---------------------------------------------------------------------------
+// Sweep variant. Workgroup b of a grid of G owns rows b, b + G, b + 2G, ...,
+// and wave w owns chunks w, w + NW, ... (CPW of them) of each of those rows,
+// so its x fragments stay in registers and at any moment the whole grid reads
+// one compact window of W that moves front to back (the access pattern of a
+// plain grid-stride read, the fastest way to stream HBM here). A wave keeps
+// the next row's loads in flight while it reduces the current row; its
+// per-row partial sums go to LDS slots (no barrier per row) and are added in
+// a fixed order once at the end, so results are deterministic.
+// ---------------------------------------------------------------------------
+constexpr int SW_MAX_ROWS = 256;
+
+template <int WF, typename XT, int NMAT, int OP, int NW, int CPW>
+__global__ void __launch_bounds__(NW * 64) gemv_sweep_kernel(GemvArgs a) {
+    constexpr int EPL = WT<WF>::EPL;
+    constexpr int CH = 64 * EPL;
+    __shared__ float part[SW_MAX_ROWS][NMAT][NW];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int M = a.M, K = a.K, G = gridDim.x, b = blockIdx.x;
+    const int nch = (K + CH - 1) / CH;
+    const int nrows = b < M ? (M - b + G - 1) / G : 0;  // <= SW_MAX_ROWS (host)
+    const size_t row_bytes = (size_t)K * welem_bytes<WF>();
+
+    int col[CPW];
+    bool ok[CPW];
+    XFrag<XT, EPL> xf[CPW];
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+        col[j] = (wave + j * NW) * CH + lane * EPL;
+        ok[j] = (wave + j * NW) < nch && col[j] < K;
+        if (ok[j]) {
+            if (a.nw)
+                xf[j].load_norm(a.x, a.nw, col[j], 1.0f, a.plus_one);
+            else
+                xf[j].load(a.x, col[j]);
+        }
+    }
+
+    auto issue = [&](u4_t (&wv)[CPW][NMAT], uint16_t (&sv)[CPW][NMAT], int row) {
+#pragma unroll
+        for (int j = 0; j < CPW; ++j)
+            if (ok[j]) {
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) {
+                    const unsigned char* base = static_cast<const unsigned char*>(a.W[m]) + (size_t)row * row_bytes;
+                    wv[j][m] = ld_stream<WF>(base + (size_t)col[j] * welem_bytes<WF>());
+                    if (WF == MXD_W_Q8B32) sv[j][m] = a.S[m][(size_t)row * (K / 32) + col[j] / 32];
+                }
+            }
+    };
+    auto consume = [&](const u4_t (&wv)[CPW][NMAT], const uint16_t (&sv)[CPW][NMAT], int i) {
+        float acc[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) acc[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPW; ++j)
+            if (ok[j]) {
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) {
+                    if constexpr (WF == MXD_W_Q8B32)
+                        acc[m] = fmaf(dot16q(wv[j][m], xf[j]), mxd::h2f(sv[j][m]), acc[m]);
+                    else
+                        acc[m] = dot16(wv[j][m], xf[j], acc[m]);
+                }
+            }
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            acc[m] = mxd::wave_sum(acc[m]);
+            if (lane == 0) part[i][m][wave] = acc[m];
+        }
+    };
+
+    u4_t wa[CPW][NMAT], wb[CPW][NMAT];
+    uint16_t sa[CPW][NMAT], sb[CPW][NMAT];
+    if (nrows > 0) issue(wa, sa, b);
+    for (int i = 0; i < nrows; i += 2) {
+        if (i + 1 < nrows) issue(wb, sb, b + (i + 1) * G);
+        consume(wa, sa, i);
+        if (i + 1 >= nrows) break;
+        if (i + 2 < nrows) issue(wa, sa, b + (i + 2) * G);
+        consume(wb, sb, i + 1);
+    }
+
+    const float nscale = a.nw ? block_rms_scale<NW>(static_cast<const float*>(a.x), K, a.eps) : 1.0f;
+    __syncthreads();
+    for (int i = threadIdx.x; i < nrows; i += NW * 64) {
+        const int row = b + i * G;
+        float v[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            float t = part[i][m][0];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) t += part[i][m][w];
+            v[m] = a.nw ? t * nscale : t;
+        }
+        if constexpr (NMAT == 2) {
+            a.y[row] = (OP == MXD_ACT_SILU ? mxd::silu(v[0]) : mxd::gelu_tanh(v[0])) * v[1];
+        } else if constexpr (OP == MXD_EPI_ADD) {
+            a.y[row] += v[0];
+        } else if constexpr (OP == MXD_EPI_GELU_MUL) {
+            a.y[row] = mxd::gelu_tanh(v[0]) * a.aux[row];
+        } else {
+            a.y[row] = v[0];
+        }
+    }
+}
+
+template <int WF, typename XT, int NMAT, int OP, int NW, int CPW>
+int launch_sweep_k(const GemvArgs& a, int wg_per_cu, hipStream_t s) {
+    auto kern = gemv_sweep_kernel<WF, XT, NMAT, OP, NW, CPW>;
+    int fit = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&fit, kern, NW * 64, 0) != hipSuccess || fit < 1) fit = 1;
+    if (wg_per_cu > fit) wg_per_cu = fit;
+    int grid = 256 * wg_per_cu;
+    const int min_grid = (a.M + SW_MAX_ROWS - 1) / SW_MAX_ROWS;  // LDS holds SW_MAX_ROWS rows per workgroup
+    if (grid < min_grid) grid = min_grid;
+    if (grid > a.M) grid = a.M;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), 0, s, a);
+    return mxd::check_launch("matvec");
+}
+
+template <int WF, typename XT, int NMAT, int OP>
+int launch_sweep(const GemvArgs& a, int nw, int cpw, int wg_per_cu, hipStream_t s) {
+    if (nw == 4 && cpw == 1) return launch_sweep_k<WF, XT, NMAT, OP, 4, 1>(a, wg_per_cu, s);
+    if (nw == 4 && cpw == 2) return launch_sweep_k<WF, XT, NMAT, OP, 4, 2>(a, wg_per_cu, s);
+    if (nw == 4 && cpw == 4) return launch_sweep_k<WF, XT, NMAT, OP, 4, 4>(a, wg_per_cu, s);
+    if (nw == 8 && cpw == 1) return launch_sweep_k<WF, XT, NMAT, OP, 8, 1>(a, wg_per_cu, s);
+    if (nw == 8 && cpw == 2) return launch_sweep_k<WF, XT, NMAT, OP, 8, 2>(a, wg_per_cu, s);
+    if (nw == 8 && cpw == 4) return launch_sweep_k<WF, XT, NMAT, OP, 8, 4>(a, wg_per_cu, s);
+    if (nw == 16 && cpw == 1) return launch_sweep_k<WF, XT, NMAT, OP, 16, 1>(a, wg_per_cu, s);
+    if (nw == 16 && cpw == 2) return launch_sweep_k<WF, XT, NMAT, OP, 16, 2>(a, wg_per_cu, s);
+    if (nw == 16 && cpw == 4) return launch_sweep_k<WF, XT, NMAT, OP, 16, 4>(a, wg_per_cu, s);
+    return mxd::fail(MXD_ERR_INVALID_ARG, "matvec: sweep has no (waves %d, chunks/wave %d) variant", nw, cpw);
+}
+
 // Rows per workgroup and waves per workgroup for a shape, overridable through
-// the MV_NR / MV_NW tunables.
-// Measured on MI355X (fp16 weights, 117 MB to 1 GB matrices): four rows per
-// workgroup with up to eight waves across K is within a few percent of the
-// best tiling for every decode shape, and far better than one-row tiles on
-// the long-K shapes (2048 x 16384: 5.0 vs 2.6 TB/s).
-void pick_tiling(int M, int nch, int& nr, int& nw) {
-    nw = nch >= 8 ? 8 : nch >= 4 ? 4 : nch >= 2 ? 2 : 1;
-    nr = M >= 1024 ? 4 : M >= 256 ? 2 : 1;
+// the MV_NR / MV_NW tunables. From sweeps on MI355X (117 MB to 1 GB matrices,
+// every tiling timed back to back): four waves across K for rows of up to 8
+// chunks, eight for longer rows; two rows per workgroup with fp16 x, four with
+// fp32 x (more x registers per chunk), eight for int8 weights (half the bytes
+// per row). Small M keeps enough workgroups to fill the GPU.
+void pick_tiling(int M, int nch, bool q8, bool x_half, int& nr, int& nw) {
+    if (nch > 8) {
+        nw = 8;
+        nr = q8 ? 8 : 4;
+    } else {
+        nw = nch >= 4 ? 4 : nch >= 2 ? 2 : 1;
+        nr = q8 ? 8 : x_half ? 2 : 4;
+    }
+    if (M < 1024) nr = M >= 256 ? (nr < 2 ? nr : 2) : 1;
     nr = mxd::tunable("MV_NR", nr);
     nw = mxd::tunable("MV_NW", nw);
 }
@@ -518,11 +668,23 @@ int launch(const GemvArgs& a, hipStream_t s) {
         const int nw = mxd::tunable("MV_RS_NW", nch <= 4 ? 4 : nch <= 8 ? 8 : 16);
         int cpw = (nch + nw - 1) / nw;
         cpw = cpw <= 1 ? 1 : cpw <= 2 ? 2 : 4;
+        MXD_REQUIRE(nw * cpw >= nch, MXD_ERR_UNSUPPORTED,
+                    "matvec: row streaming with %d waves covers at most %d chunks", nw, nw * 4);
         const int wg_per_cu = mxd::tunable("MV_RS_WGCU", 32 / nw > 0 ? 32 / nw : 1);
         return launch_rows<WF, XT, NMAT, OP>(a, nw, cpw, wg_per_cu, s);
     }
+    if (algo == 2) {
+        MXD_REQUIRE(nch <= RS_MAX_CHUNKS, MXD_ERR_UNSUPPORTED, "matvec: sweep needs K <= %d", RS_MAX_CHUNKS * CH);
+        const int nw = mxd::tunable("MV_SW_NW", nch <= 4 ? 4 : nch <= 8 ? 8 : 16);
+        int cpw = (nch + nw - 1) / nw;
+        cpw = cpw <= 1 ? 1 : cpw <= 2 ? 2 : 4;
+        MXD_REQUIRE(nw * cpw >= nch, MXD_ERR_UNSUPPORTED, "matvec: sweep with %d waves covers at most %d chunks",
+                    nw, nw * 4);
+        const int wg_per_cu = mxd::tunable("MV_SW_WGCU", 32 / nw > 0 ? 32 / nw : 1);
+        return launch_sweep<WF, XT, NMAT, OP>(a, nw, cpw, wg_per_cu, s);
+    }
     int nr, nw;
-    pick_tiling(a.M, nch, nr, nw);
+    pick_tiling(a.M, nch, WF == MXD_W_Q8B32, sizeof(XT) == 2, nr, nw);
     switch (nr) {
         case 1: return launch_nw<WF, XT, NMAT, OP, 1>(a, nw, s);
         case 2: return launch_nw<WF, XT, NMAT, OP, 2>(a, nw, s);
@@ -686,7 +848,7 @@ extern "C" int mxd_qkv_rope_kv(const uint16_t* Wqkv, const float* x, const float
     a.hd = head_dim;
     a.max_ctx = max_ctx;
     int nr, nw;
-    pick_tiling(M, (K + 511) / 512, nr, nw);
+    pick_tiling(M, (K + 511) / 512, false, false, nr, nw);
     nr = nr < 2 ? 2 : (nr & ~1);  // rotation pairs stay inside one workgroup
     hipStream_t s = mxd::as_stream(stream);
     switch (nr) {

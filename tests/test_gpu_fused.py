@@ -105,3 +105,40 @@ def test_qkv_rope_kv(dev, rng, nh, nkv, hd, D, pos, device_pos):
     _f16_close(v_rows[:, pos], vc[:, pos])
     assert np.count_nonzero(k_rows) == np.count_nonzero(k_rows[:, pos])  # only position pos written
     assert np.count_nonzero(v_rows) == np.count_nonzero(v_rows[:, pos])
+
+
+@pytest.mark.parametrize("algo", [0, 1, 2])
+def test_every_matvec_variant(dev, rng, algo):
+    """The three matvec work layouts (row tiles, row streaming, grid sweep) give
+    the oracle's answer for int8 weights, the two-matrix GLU, the fused norm
+    and the residual-add epilogue, including ragged M and K tails."""
+    from gemmagemini4hackathon2026_10_2425_amd import ops
+    from gemmagemini4hackathon2026_10_2425_amd.quant import quantize_q8b32
+
+    L = _lib()
+    M, K = 1037, 4096 + 1024 + 64
+    W = (rng.standard_normal((M, K), dtype=np.float32) * 0.02).astype(np.float16)
+    Wu = (rng.standard_normal((M, K), dtype=np.float32) * 0.02).astype(np.float16)
+    x = rng.standard_normal(K, dtype=np.float32)
+    nw_ = rng.standard_normal(K, dtype=np.float32) * 0.02
+    q, s = quantize_q8b32(W)
+    x16 = x.astype(np.float16)
+    Wd, Wud, xd, x16d, nwd = _d(W, dev), _d(Wu, dev), _d(x, dev), _d(x16, dev), _d(nw_, dev)
+    qd, sd = _d(q, dev), _d(s, dev)
+    try:
+        L.set_tunable("MV_ALGO", algo)
+        y = ops.matvec_q8b32(qd, sd, x16d)
+        assert rel_err(y.cpu().numpy(), ref.matvec_q8b32(q, s, x16)) <= 1e-4
+        h = ops.matvec_gate_up(Wd, Wud, xd, "silu")
+        assert rel_err(h.cpu().numpy(), ref.gate_up(W, Wu, x, "silu")) <= 1e-4
+        base = rng.standard_normal(M, dtype=np.float32)
+        yd = _d(base, dev)
+        ops.matvec_f16_add(Wd, xd, yd)
+        assert rel_err(yd.cpu().numpy(), base + ref.matvec(W, x)) <= 1e-4
+        yn = torch.empty(M, dtype=torch.float32, device=dev)
+        L.call("mxd_matvec_f16_rmsnorm", Wd.data_ptr(), xd.data_ptr(), nwd.data_ptr(), 1e-6, 1, yn.data_ptr(), M, K,
+               L.MXD_EPI_STORE, None, _stream())
+        xn = ref.rmsnorm(x, nw_, 1e-6, True).astype(np.float32)
+        assert rel_err(yn.cpu().numpy(), ref.matvec(W, xn)) <= 1e-4
+    finally:
+        L.set_tunable("MV_ALGO", 0)

@@ -121,8 +121,14 @@ def test_matvec_f16_tunables(dev, rng):
                 _lib.set_tunable("MV_RS_NW", nw)
                 _lib.set_tunable("MV_RS_WGCU", wgcu)
                 _close(ops.matvec_f16(Wd, xd).cpu().numpy(), want)
+        _lib.set_tunable("MV_ALGO", 2)  # grid sweep
+        for nw in (4, 8, 16):
+            for wgcu in (1, 2, 8):
+                _lib.set_tunable("MV_SW_NW", nw)
+                _lib.set_tunable("MV_SW_WGCU", wgcu)
+                _close(ops.matvec_f16(Wd, xd).cpu().numpy(), want)
     finally:
-        for name in ("MV_NR", "MV_NW", "MV_ALGO", "MV_RS_NW", "MV_RS_WGCU"):
+        for name in ("MV_NR", "MV_NW", "MV_ALGO", "MV_RS_NW", "MV_RS_WGCU", "MV_SW_NW", "MV_SW_WGCU"):
             _lib.set_tunable(name, 0)
 
 
