@@ -29,6 +29,21 @@ import time
 
 PEAK_HBM_GBS = 8000.0
 ROTATE_MIN_BYTES = 600 * 2**20
+# HBM bytes per launch of the headline kernel from rocprofv3 FETCH_SIZE /
+# WRITE_SIZE passes (calibrated against a copy of known size), committed as a
+# text summary beside the other profiles.
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_f16_ffn_hbm_traffic.md")
+
+
+def measured_traffic() -> int | None:
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg: str) -> None:
@@ -302,7 +317,8 @@ def main(argv=None) -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(g["gbs"] / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
+            "algorithmic_bytes_per_launch": g["step_bytes"] // 2,
         },
         "cpu_baseline": cpu,
         "detail": detail,

@@ -15,6 +15,6 @@ Modules:
                 full-size decode runs and CPU timing
 
 How each function is pinned (closed forms, library routines, brute force,
-HF transformers' Gemma) is listed in tests/test_oracle_*.py; every oracle
+HF transformers' Gemma) is listed in tests/test_oracle.py; every oracle
 function has at least one such check.
 """
