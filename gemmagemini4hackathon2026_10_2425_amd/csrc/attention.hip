@@ -32,6 +32,10 @@
 //    kernel with the log-sum-exp rule; a single split writes the output
 //    directly. (A merge by the last-arriving split needs device-scope fences
 //    in every workgroup, which on a multi-XCD part costs more than a launch.)
+//  * the paged variant (a ragged batch of sequences over a pool of 16-key
+//    pages) runs the same core: a 32-key block is two pages, tile t of the
+//    scores is page t, and each lane addresses its own page, so a block is
+//    still one 1 KiB load per K operand and two 512-byte halves per V operand.
 #include "common.hpp"
 
 namespace {
@@ -40,16 +44,21 @@ constexpr int ATT_WAVES = 4;
 constexpr int ATT_THREADS = ATT_WAVES * 64;
 constexpr int BLK = 32;  // keys per wave step
 constexpr int MAX_SPLITS = 512;
+constexpr int PAGED_BPS = 16;  // 32-key blocks per split of a paged sequence (4 per wave)
 constexpr float LOG2E = 1.4426950408889634f;
 
 struct AttnArgs {
     const float* q;
-    const uint16_t* k;
+    const uint16_t* k;  // contiguous tiled cache, or the page pool
     const uint16_t* v;
     float* out;
-    float* ws_o;   // [n_splits][n_heads][HD]
-    float* ws_ml;  // [n_splits][n_heads][2]
+    float* ws_o;   // [seqs][n_splits][n_heads][HD]
+    float* ws_ml;  // [seqs][n_splits][n_heads][2]
     const int32_t* pos_dev;
+    // paged: page_table [seqs][max_pages] of pool pages, seq_lens [seqs] keys
+    const int32_t* page_table = nullptr;
+    const int32_t* seq_lens = nullptr;
+    int max_pages = 0, n_pages = 0, q_stride = 0, out_stride = 0;
     int n_heads, n_kv, G, max_ctx, n_keys, n_splits;
     float qscale;  // scale * log2(e): scores live in the log2 domain
 };
@@ -88,8 +97,62 @@ __device__ __forceinline__ void load_block(KVBlock<HD>& kv, const uint16_t* kbas
     for (int d = 0; d < HD / 16; ++d) kv.v[d] = *reinterpret_cast<const h8_t*>(vt + d * 512);
 }
 
+// A contiguous (tiled) cache of one kv head.
 template <int HD>
-__global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
+struct ContigKV {
+    const uint16_t* kbase;
+    const uint16_t* vbase;
+    __device__ __forceinline__ void load(KVBlock<HD>& kv, int b, int lane) const {
+        load_block<HD>(kv, kbase, vbase, b * BLK, lane);
+    }
+    // Key (within the block) of score slot j of lane group g; the same slot
+    // order is the k order of the P.V operands.
+    static __device__ __forceinline__ int key(int g, int j) { return 8 * g + j; }
+};
+
+// One sequence's pages of one kv head in the page pool (slab layouts in
+// common.hpp). Block b is pages 2b (score tile 0) and 2b + 1 (tile 1); row r
+// of tile t is key 16t + r, so slot j of lane group g is key
+// 16 (j >> 2) + 4g + (j & 3), which is also the order V's slab stores keys in.
+template <int HD>
+struct PagedKV {
+    const uint16_t* kpool;
+    const uint16_t* vpool;
+    const int32_t* table;  // this sequence's page-table row
+    int npages;            // pages holding its keys
+    int n_pages;           // pages in the pool
+    size_t page_stride;    // n_kv * PAGE_KEYS * HD halfs
+    int kvh;
+    __device__ __forceinline__ size_t slab(int logical) const {
+        int p = table[logical];
+        p = p < 0 ? 0 : (p >= n_pages ? n_pages - 1 : p);  // a bad entry still addresses inside the pool
+        return (size_t)p * page_stride + (size_t)kvh * mxd::PAGE_KEYS * HD;
+    }
+    __device__ __forceinline__ void load(KVBlock<HD>& kv, int b, int lane) const {
+        // A ragged last block has one page: its second tile re-reads the first
+        // page, and every key of it is masked.
+        const size_t s0 = slab(2 * b), s1 = slab(min(2 * b + 1, npages - 1));
+#pragma unroll
+        for (int c = 0; c < HD / 32; ++c) {
+            kv.k[0][c] = *reinterpret_cast<const h8_t*>(kpool + s0 + (size_t)(c * 64 + lane) * 8);
+            kv.k[1][c] = *reinterpret_cast<const h8_t*>(kpool + s1 + (size_t)(c * 64 + lane) * 8);
+        }
+#pragma unroll
+        for (int d = 0; d < HD / 16; ++d) {
+            const u2_t lo = *reinterpret_cast<const u2_t*>(vpool + s0 + (size_t)(d * 64 + lane) * 4);
+            const u2_t hi = *reinterpret_cast<const u2_t*>(vpool + s1 + (size_t)(d * 64 + lane) * 4);
+            const u4_t w = {lo.x, lo.y, hi.x, hi.y};
+            __builtin_memcpy(&kv.v[d], &w, 16);
+        }
+    }
+    static __device__ __forceinline__ int key(int g, int j) { return 16 * (j >> 2) + 4 * g + (j & 3); }
+};
+
+// One split of one kv head of one sequence: keys [0, n), S splits, q and out
+// rows of this sequence, partials of this sequence.
+template <int HD, typename KV>
+__device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int n, int S, int split, int kvh,
+                                          const float* qrow, float* orow, float* ws_o, float* ws_ml) {
     constexpr int NC = HD / 32;  // MFMA k-chunks over head_dim for Q.K
     constexpr int ND = HD / 16;  // 16-wide dim tiles for P.V
     // Prefetching the next block doubles the K/V registers; it fits the
@@ -99,17 +162,17 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
     __shared__ float sm_m[ATT_WAVES][8];
     __shared__ float sm_l[ATT_WAVES][8];
 
-    const int n = n_keys_of(a);
     const int nblocks = (n + BLK - 1) / BLK;
-    const int S = a.n_splits, split = blockIdx.x, kvh = blockIdx.y;
-    if (split >= nblocks) return;  // an empty split
+    const int G = a.G;
+    if (nblocks == 0) {  // no keys (an empty sequence): the output is zero
+        if (split == 0)
+            for (int idx = threadIdx.x; idx < G * HD; idx += ATT_THREADS) orow[(size_t)kvh * G * HD + idx] = 0.0f;
+        return;
+    }
+    if (split >= min(S, nblocks)) return;  // an empty split
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, g = lane >> 4;
-    const int G = a.G;
-
-    const uint16_t* kbase = a.k + (size_t)kvh * a.max_ctx * HD;
-    const uint16_t* vbase = a.v + (size_t)kvh * a.max_ctx * HD;
 
     // Blocks are dealt round-robin: split s owns global blocks s, s+S, s+2S, ...
     // and wave w takes every 4th of those, so at any moment the splits of a kv
@@ -118,7 +181,7 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
     const int step = S * ATT_WAVES;
     int b = split + S * wave;
     KVBlock<HD> cur, nxt;
-    if (b < nblocks) load_block<HD>(cur, kbase, vbase, b * BLK, lane);
+    if (b < nblocks) src.load(cur, b, lane);
 
     // Q^T operand: column h holds fp16(q) of head kvh*G + h and column h + 8
     // the remainder fp16(q - hi) (h < G <= 8); the rest are zero. k-slot (g, j)
@@ -127,7 +190,7 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
     {
         const int h = col & 7;
         const bool live = h < G;
-        const float* qh = a.q + (size_t)(kvh * G + (live ? h : 0)) * HD;
+        const float* qh = qrow + (size_t)(kvh * G + (live ? h : 0)) * HD;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const f4_t q0 = *reinterpret_cast<const f4_t*>(qh + 32 * c + 8 * g);
@@ -155,10 +218,11 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
     for (; b < nblocks; b += step) {
         const int key0 = b * BLK;
         if constexpr (PREFETCH) {
-            if (b + step < nblocks) load_block<HD>(nxt, kbase, vbase, (b + step) * BLK, lane);
+            if (b + step < nblocks) src.load(nxt, b + step, lane);
         }
 
-        // ---- scores (log2 domain): S^T tile t, row 4g+i = key key0 + 8g + 4t + i
+        // ---- scores (log2 domain): lane group g, slot j = 4t + i (tile t,
+        // row 4g + i) is key key0 + KV::key(g, j)
         float s[8];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
@@ -169,12 +233,12 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
             for (int i = 0; i < 4; ++i) s[4 * t + i] = acc[i];
         }
         const bool tail = key0 + BLK > n;
-        const int nvalid = n - key0 - 8 * g;  // keys of this lane group still inside [0, n)
+        const int nvalid = n - key0;  // keys of this block inside [0, n)
         float mb = -INFINITY;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             s[j] += mxd::dpp_f32<0x128>(s[j]);  // row_ror:8 = column h + 8: hi + lo
-            if (tail) s[j] = j < nvalid ? s[j] : -INFINITY;
+            if (tail) s[j] = KV::key(g, j) < nvalid ? s[j] : -INFINITY;
             mb = fmaxf(mb, s[j]);
         }
         mb = fmaxf(mb, __shfl_xor(mb, 16));
@@ -210,7 +274,8 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
             u4_t keep;
 #pragma unroll
             for (int w = 0; w < 4; ++w)
-                keep[w] = (2 * w < nvalid ? 0x0000FFFFu : 0u) | (2 * w + 1 < nvalid ? 0xFFFF0000u : 0u);
+                keep[w] = (KV::key(g, 2 * w) < nvalid ? 0x0000FFFFu : 0u) |
+                          (KV::key(g, 2 * w + 1) < nvalid ? 0xFFFF0000u : 0u);
 #pragma unroll
             for (int d = 0; d < ND; ++d) {
                 u4_t v;
@@ -225,7 +290,7 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
         if constexpr (PREFETCH) {
             cur = nxt;
         } else if (b + step < nblocks) {
-            load_block<HD>(cur, kbase, vbase, (b + step) * BLK, lane);
+            src.load(cur, b + step, lane);
         }
     }
 
@@ -265,15 +330,43 @@ __global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
         }
         const int head = kvh * G + h;
         if (n_active == 1) {
-            a.out[(size_t)head * HD + dim] = so / sl;
+            orow[(size_t)head * HD + dim] = so / sl;
         } else {
-            a.ws_o[((size_t)split * a.n_heads + head) * HD + dim] = so;
+            ws_o[((size_t)split * a.n_heads + head) * HD + dim] = so;
             if (dim == 0) {
-                a.ws_ml[((size_t)split * a.n_heads + head) * 2 + 0] = M;
-                a.ws_ml[((size_t)split * a.n_heads + head) * 2 + 1] = sl;
+                ws_ml[((size_t)split * a.n_heads + head) * 2 + 0] = M;
+                ws_ml[((size_t)split * a.n_heads + head) * 2 + 1] = sl;
             }
         }
     }
+}
+
+template <int HD>
+__global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
+    const int kvh = blockIdx.y;
+    const ContigKV<HD> src{a.k + (size_t)kvh * a.max_ctx * HD, a.v + (size_t)kvh * a.max_ctx * HD};
+    attn_core<HD>(a, src, n_keys_of(a), a.n_splits, blockIdx.x, kvh, a.q, a.out, a.ws_o, a.ws_ml);
+}
+
+// Keys and splits of paged sequence seq (clamped so a bad length can never
+// address past its page-table row).
+__device__ __forceinline__ int paged_keys(const AttnArgs& a, int seq) {
+    return max(0, min(a.seq_lens[seq], a.max_pages * mxd::PAGE_KEYS));
+}
+__device__ __forceinline__ int paged_splits(const AttnArgs& a, int n) {
+    const int nblocks = (n + BLK - 1) / BLK;
+    return min(a.n_splits, max(1, (nblocks + PAGED_BPS - 1) / PAGED_BPS));
+}
+
+template <int HD>
+__global__ void __launch_bounds__(ATT_THREADS) attn_paged_kernel(AttnArgs a) {
+    const int kvh = blockIdx.y, seq = blockIdx.z;
+    const int n = paged_keys(a, seq);
+    const PagedKV<HD> src{a.k, a.v, a.page_table + (size_t)seq * a.max_pages, (n + mxd::PAGE_KEYS - 1) / mxd::PAGE_KEYS,
+                          a.n_pages, (size_t)a.n_kv * mxd::PAGE_KEYS * HD, kvh};
+    const size_t ws_rows = (size_t)seq * a.n_splits * a.n_heads;
+    attn_core<HD>(a, src, n, paged_splits(a, n), blockIdx.x, kvh, a.q + (size_t)seq * a.q_stride,
+                  a.out + (size_t)seq * a.out_stride, a.ws_o + ws_rows * HD, a.ws_ml + ws_rows * 2);
 }
 
 // out[h] = sum_s 2^(M_s - M) O_s / sum_s 2^(M_s - M) L_s over the active
@@ -286,18 +379,17 @@ constexpr int MG = 4;
 constexpr int PRE = 16;
 
 template <int HD>
-__global__ void __launch_bounds__(MG * HD) attn_merge_kernel(AttnArgs a) {
+__device__ __forceinline__ void attn_merge_core(const AttnArgs& a, int n_active, int head, float* orow,
+                                                const float* ws_o, const float* ws_ml) {
     constexpr int NT = MG * HD;
     __shared__ float sw[MAX_SPLITS];
     __shared__ float sl[MAX_SPLITS];
     __shared__ float red[2][NT / 64];
     __shared__ float part[MG - 1][HD];
-    const int n = n_keys_of(a);
-    const int n_active = min(a.n_splits, (n + BLK - 1) / BLK);
     if (n_active <= 1) return;
-    const int head = blockIdx.x, tid = threadIdx.x;
+    const int tid = threadIdx.x;
     const int grp = tid / HD, dim = tid - grp * HD;
-    const float* po = a.ws_o + (size_t)head * HD + dim;
+    const float* po = ws_o + (size_t)head * HD + dim;
     const size_t stride = (size_t)a.n_heads * HD;
 
     float pre[PRE];
@@ -308,9 +400,9 @@ __global__ void __launch_bounds__(MG * HD) attn_merge_kernel(AttnArgs a) {
     }
     float mloc = -INFINITY;
     for (int sp = tid; sp < n_active; sp += NT) {
-        const float m = a.ws_ml[((size_t)sp * a.n_heads + head) * 2];
+        const float m = ws_ml[((size_t)sp * a.n_heads + head) * 2];
         sw[sp] = m;
-        sl[sp] = a.ws_ml[((size_t)sp * a.n_heads + head) * 2 + 1];
+        sl[sp] = ws_ml[((size_t)sp * a.n_heads + head) * 2 + 1];
         mloc = fmaxf(mloc, m);
     }
     mloc = mxd::wave_max(mloc);
@@ -355,8 +447,24 @@ __global__ void __launch_bounds__(MG * HD) attn_merge_kernel(AttnArgs a) {
         float tot = acc;
 #pragma unroll
         for (int g2 = 0; g2 < MG - 1; ++g2) tot += part[g2][dim];
-        a.out[(size_t)head * HD + dim] = tot / L;
+        orow[(size_t)head * HD + dim] = tot / L;
     }
+}
+
+template <int HD>
+__global__ void __launch_bounds__(MG * HD) attn_merge_kernel(AttnArgs a) {
+    const int n_active = min(a.n_splits, (n_keys_of(a) + BLK - 1) / BLK);
+    attn_merge_core<HD>(a, n_active, blockIdx.x, a.out, a.ws_o, a.ws_ml);
+}
+
+template <int HD>
+__global__ void __launch_bounds__(MG * HD) attn_paged_merge_kernel(AttnArgs a) {
+    const int seq = blockIdx.y;
+    const int n = paged_keys(a, seq);
+    const int n_active = min(paged_splits(a, n), (n + BLK - 1) / BLK);
+    const size_t ws_rows = (size_t)seq * a.n_splits * a.n_heads;
+    attn_merge_core<HD>(a, n_active, blockIdx.x, a.out + (size_t)seq * a.out_stride, a.ws_o + ws_rows * HD,
+                        a.ws_ml + ws_rows * 2);
 }
 
 // Splits per kv head: about ATT_WGCU (default 2) workgroups per CU over the
@@ -439,4 +547,85 @@ extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint1
         if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(n_heads), dim3(MG * 256), 0, s, a);
     }
     return mxd::check_launch("mxd_attention");
+}
+
+namespace {
+int paged_split_max(int max_keys) {
+    const int nblocks = (max_keys + BLK - 1) / BLK;
+    return min(MAX_SPLITS, max(1, (nblocks + PAGED_BPS - 1) / PAGED_BPS));
+}
+}  // namespace
+
+extern "C" size_t mxd_attention_paged_workspace_size(int n_heads, int n_kv_heads, int head_dim, int n_seqs,
+                                                     int max_keys) {
+    if (n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || n_seqs <= 0 || max_keys <= 0) return 0;
+    return (size_t)n_seqs * paged_split_max(max_keys) * n_heads * (head_dim + 2) * sizeof(float);
+}
+
+extern "C" int mxd_attention_paged(const float* q, int q_stride, const uint16_t* kpool, const uint16_t* vpool,
+                                   int n_pages, const int32_t* page_table, int max_pages, const int32_t* seq_lens,
+                                   int n_seqs, float* out, int out_stride, int n_heads, int n_kv_heads, int head_dim,
+                                   int max_keys, float scale, void* workspace, size_t ws_bytes,
+                                   mxd_stream_t stream) {
+    MXD_REQUIRE(q && kpool && vpool && page_table && seq_lens && out, MXD_ERR_INVALID_ARG,
+                "mxd_attention_paged: null pointer");
+    MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, MXD_ERR_INVALID_ARG,
+                "mxd_attention_paged: n_heads=%d must be a positive multiple of n_kv_heads=%d", n_heads, n_kv_heads);
+    const int G = n_heads / n_kv_heads;
+    MXD_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_paged: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", G);
+    MXD_REQUIRE(head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_paged: head_dim %d (128 or 256)", head_dim);
+    MXD_REQUIRE(n_pages > 0 && max_pages > 0 && n_seqs > 0 && n_seqs <= 65535, MXD_ERR_INVALID_ARG,
+                "mxd_attention_paged: n_pages=%d max_pages=%d n_seqs=%d", n_pages, max_pages, n_seqs);
+    MXD_REQUIRE(max_keys >= 1 && max_keys <= max_pages * mxd::PAGE_KEYS, MXD_ERR_INVALID_ARG,
+                "mxd_attention_paged: max_keys=%d outside [1, max_pages*16=%d]", max_keys,
+                max_pages * mxd::PAGE_KEYS);
+    MXD_REQUIRE(q_stride >= n_heads * head_dim && out_stride >= n_heads * head_dim && q_stride % 4 == 0,
+                MXD_ERR_INVALID_ARG, "mxd_attention_paged: q_stride=%d / out_stride=%d below n_heads*head_dim=%d "
+                "(q_stride a multiple of 4)", q_stride, out_stride, n_heads * head_dim);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kpool) |
+                         reinterpret_cast<uintptr_t>(vpool);
+    MXD_REQUIRE((al & 15) == 0, MXD_ERR_UNSUPPORTED, "mxd_attention_paged: q, kpool, vpool must be 16-byte aligned");
+    const int s_max = paged_split_max(max_keys);
+    const size_t need = (size_t)n_seqs * s_max * n_heads * (head_dim + 2) * sizeof(float);
+    MXD_REQUIRE(s_max == 1 || (workspace && ws_bytes >= need), MXD_ERR_WORKSPACE,
+                "mxd_attention_paged: workspace of %zu bytes needed (got %zu)", need, ws_bytes);
+    MXD_REQUIRE(!workspace || (reinterpret_cast<uintptr_t>(workspace) & 15) == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_paged: workspace must be 16-byte aligned");
+
+    AttnArgs a;
+    a.q = q;
+    a.k = kpool;
+    a.v = vpool;
+    a.out = out;
+    a.ws_o = static_cast<float*>(workspace);
+    a.ws_ml = workspace ? a.ws_o + (size_t)n_seqs * s_max * n_heads * head_dim : nullptr;
+    a.pos_dev = nullptr;
+    a.page_table = page_table;
+    a.seq_lens = seq_lens;
+    a.max_pages = max_pages;
+    a.n_pages = n_pages;
+    a.q_stride = q_stride;
+    a.out_stride = out_stride;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv_heads;
+    a.G = G;
+    a.max_ctx = max_pages * mxd::PAGE_KEYS;
+    a.n_keys = 0;
+    a.n_splits = s_max;
+    a.qscale = scale * LOG2E;
+
+    hipStream_t s = mxd::as_stream(stream);
+    const dim3 grid(s_max, n_kv_heads, n_seqs);
+    if (head_dim == 128) {
+        hipLaunchKernelGGL(attn_paged_kernel<128>, grid, dim3(ATT_THREADS), 0, s, a);
+        if (s_max > 1)
+            hipLaunchKernelGGL(attn_paged_merge_kernel<128>, dim3(n_heads, n_seqs), dim3(MG * 128), 0, s, a);
+    } else {
+        hipLaunchKernelGGL(attn_paged_kernel<256>, grid, dim3(ATT_THREADS), 0, s, a);
+        if (s_max > 1)
+            hipLaunchKernelGGL(attn_paged_merge_kernel<256>, dim3(n_heads, n_seqs), dim3(MG * 256), 0, s, a);
+    }
+    return mxd::check_launch("mxd_attention_paged");
 }

@@ -97,6 +97,46 @@ rope_kv_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kcache, uint16_t*
     }
 }
 
+// Batched decode over a paged cache: row b of qkv is sequence b's new token,
+// at position seq_lens[b] - 1. q and k are rotated in place (as rope_kv does)
+// and k, v go to that position's page (slab layouts in common.hpp). A row
+// whose position is outside its page-table row, or whose page id is outside
+// the pool, is left untouched.
+__global__ void __launch_bounds__(256)
+rope_kv_paged_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kpool, uint16_t* __restrict__ vpool,
+                     const float* __restrict__ inv_freq, int n_heads, int n_kv, int hd,
+                     const int32_t* __restrict__ page_table, int max_pages, const int32_t* __restrict__ seq_lens,
+                     int n_pages) {
+    const int half_d = hd >> 1;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;  // pair index over heads
+    const int b = blockIdx.y;                              // sequence
+    const int h = i / half_d, p = i - h * half_d;
+    if (h >= n_heads + n_kv) return;
+    const int pos = seq_lens[b] - 1;
+    if (pos < 0 || pos >= max_pages * mxd::PAGE_KEYS) return;
+    const int phys = page_table[(size_t)b * max_pages + (pos >> 4)];
+    if (phys < 0 || phys >= n_pages) return;
+    float* row = qkv + (size_t)b * (n_heads + 2 * n_kv) * hd;
+    float* v = row + h * hd;
+    const float ang = (float)pos * inv_freq[p];
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    const float x0 = v[p], x1 = v[p + half_d];
+    const float ra = x0 * cs - x1 * sn;
+    const float rb = x1 * cs + x0 * sn;
+    v[p] = ra;
+    v[p + half_d] = rb;
+    if (h >= n_heads) {
+        const int kvh = h - n_heads, r = pos & (mxd::PAGE_KEYS - 1);
+        const size_t slab = ((size_t)phys * n_kv + kvh) * mxd::PAGE_KEYS * hd;
+        kpool[slab + mxd::k_page_offset(r, p)] = mxd::f2h_bits(ra);
+        kpool[slab + mxd::k_page_offset(r, p + half_d)] = mxd::f2h_bits(rb);
+        const float* vv = row + (n_heads + n_kv + kvh) * hd;
+        vpool[slab + mxd::v_page_offset(r, p)] = mxd::f2h_bits(vv[p]);
+        vpool[slab + mxd::v_page_offset(r, p + half_d)] = mxd::f2h_bits(vv[p + half_d]);
+    }
+}
+
 }  // namespace
 
 namespace mxd {
@@ -172,4 +212,21 @@ extern "C" int mxd_rope_kv(float* qkv, uint16_t* kcache, uint16_t* vcache, const
     (void)pairs;
     return mxd::rope_kv_dev(qkv, kcache, vcache, inv_freq, n_heads, n_kv_heads, head_dim, max_ctx, pos0, rows, nullptr,
                             mxd::as_stream(stream));
+}
+
+extern "C" int mxd_rope_kv_paged(float* qkv, uint16_t* kpool, uint16_t* vpool, int n_pages, const float* inv_freq,
+                                 int n_heads, int n_kv_heads, int head_dim, const int32_t* page_table, int max_pages,
+                                 const int32_t* seq_lens, int n_seqs, mxd_stream_t stream) {
+    MXD_REQUIRE(qkv && kpool && vpool && inv_freq && page_table && seq_lens, MXD_ERR_INVALID_ARG,
+                "mxd_rope_kv_paged: null pointer");
+    MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_seqs > 0 && n_seqs <= 65535 && n_pages > 0 && max_pages > 0,
+                MXD_ERR_INVALID_ARG, "mxd_rope_kv_paged: n_heads=%d n_kv_heads=%d n_seqs=%d n_pages=%d max_pages=%d",
+                n_heads, n_kv_heads, n_seqs, n_pages, max_pages);
+    MXD_REQUIRE(head_dim > 0 && head_dim % 32 == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_rope_kv_paged: head_dim=%d must be a multiple of 32 (page slab layout)", head_dim);
+    const int pairs = (n_heads + n_kv_heads) * (head_dim / 2);
+    hipLaunchKernelGGL(rope_kv_paged_kernel, dim3((pairs + 255) / 256, n_seqs), dim3(256), 0, mxd::as_stream(stream),
+                       qkv, kpool, vpool, inv_freq, n_heads, n_kv_heads, head_dim, page_table, max_pages, seq_lens,
+                       n_pages);
+    return mxd::check_launch("mxd_rope_kv_paged");
 }

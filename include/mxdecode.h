@@ -192,6 +192,66 @@ size_t mxd_argmax_workspace_size(int N);
 int mxd_argmax(const float* logits, int32_t* tokens, int N, int out_idx, void* workspace,
                size_t ws_bytes, mxd_stream_t stream);
 
+/* ---- ragged batch over a paged KV cache ----------------------------------------
+ * The reference decodes one sequence over a contiguous cache and has no paging
+ * or batching (ios_kernels/surfaces/DESIGN_AND_LIMITATIONS.md:48,87-88); these
+ * entry points decode a batch of sequences of different lengths in one launch
+ * per op.
+ *
+ * Page pool (per layer): n_pages pages of 16 positions of every kv head; the
+ * (page, kv head) slab of 16 * head_dim fp16 values starts at element
+ * (page * n_kv_heads + kvh) * 16 * head_dim and is stored in MFMA operand order:
+ *   K: key r (0..15), dim d at (((d >> 5) * 4 + ((d >> 3) & 3)) * 16 + r) * 8 + (d & 7)
+ *   V: key r, dim d at (((d >> 4) * 4 + (r >> 2)) * 16 + (d & 15)) * 4 + (r & 3)
+ * page_table is int32 [n_seqs][max_pages]: entry [b][i] is the pool page that
+ * holds positions 16i .. 16i + 15 of sequence b (any order; the pool is shared).
+ * seq_lens is int32 [n_seqs]: the keys of sequence b after this step's append,
+ * so its new token sits at position seq_lens[b] - 1. Row b of every activation
+ * matrix belongs to sequence b. Device-side values are clamped so that a bad
+ * table entry or length cannot address outside the pool or the table. */
+
+/* Rotates q and k of row b of qkv [n_seqs][(n_heads + 2 n_kv_heads) head_dim]
+ * in place at position seq_lens[b] - 1 and appends fp16 k and v there.
+ * Replaces rope_kv (KL/kernels.metal:182-224) for a batch of sequences, each at
+ * its own position, over the page pool. */
+int mxd_rope_kv_paged(float* qkv, uint16_t* kpool, uint16_t* vpool, int n_pages, const float* inv_freq,
+                      int n_heads, int n_kv_heads, int head_dim, const int32_t* page_table, int max_pages,
+                      const int32_t* seq_lens, int n_seqs, mxd_stream_t stream);
+
+/* Workspace bytes mxd_attention_paged needs (max_keys bounds every seq_lens). */
+size_t mxd_attention_paged_workspace_size(int n_heads, int n_kv_heads, int head_dim, int n_seqs, int max_keys);
+
+/* out[b][h] = softmax(scale * q[b][h] · K_b[kvh]) · V_b[kvh] over the seq_lens[b]
+ * keys of sequence b, for all sequences in one launch. q rows are q_stride
+ * floats apart (the q part of a qkv row works in place), out rows out_stride.
+ * Replaces attention (KL/kernels.metal:235-305) for a paged ragged batch; same
+ * group sizes and head dims as mxd_attention. A sequence with no keys gets a
+ * zero output. */
+int mxd_attention_paged(const float* q, int q_stride, const uint16_t* kpool, const uint16_t* vpool, int n_pages,
+                        const int32_t* page_table, int max_pages, const int32_t* seq_lens, int n_seqs, float* out,
+                        int out_stride, int n_heads, int n_kv_heads, int head_dim, int max_keys, float scale,
+                        void* workspace, size_t ws_bytes, mxd_stream_t stream);
+
+/* Workspace bytes mxd_gemm_q8b32 needs (0 when it does not split K). */
+size_t mxd_gemm_q8b32_workspace_size(int n_rows, int M, int K);
+
+/* Y[b] (op)= dequant(Wq, scales) · X[b] for the n_rows rows of X (fp16
+ * [n_rows][K]); Y fp32 [n_rows][M]; epilogue MXD_EPI_STORE or MXD_EPI_ADD.
+ * From 16 rows on (and K % 128 == 0) this runs on the matrix cores; below, one
+ * matvec per row. The batched-matrix counterpart of gemm_f16 / gemm_f16_add
+ * (KL/kernels.metal:376-441), with int8 block-32 weights. */
+int mxd_gemm_q8b32(const int8_t* Wq, const uint16_t* scales, const uint16_t* X, float* Y, int n_rows, int M,
+                   int K, int epilogue, void* workspace, size_t ws_bytes, mxd_stream_t stream);
+
+/* Workspace bytes mxd_gemm_gate_up_q8b32 needs (0 when it does not split K). */
+size_t mxd_gemm_gate_up_q8b32_workspace_size(int n_rows, int F, int K);
+
+/* H[b] = act(Wg · X[b]) ⊙ (Wu · X[b]) for int8 block-32 Wg, Wu [F][K]; H fp32
+ * [n_rows][F]. Counterpart of gemm_gate_up_silu (KL/kernels.metal:445-510). */
+int mxd_gemm_gate_up_q8b32(const int8_t* Wg, const uint16_t* sg, const int8_t* Wu, const uint16_t* su,
+                           const uint16_t* X, float* H, int n_rows, int F, int K, int act, void* workspace,
+                           size_t ws_bytes, mxd_stream_t stream);
+
 /* ---- decode engine ---------------------------------------------------------- */
 
 /* Model shape. Replaces the reference's Config read from the weight file's JSON

@@ -1,0 +1,90 @@
+"""Ragged-batch decode of one transformer layer, composed from oracle.ops.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
+
+B sequences decode one token each; sequence b has seq_lens[b] - 1 cached
+positions before the step and appends its new token at position
+seq_lens[b] - 1. The layer is Llama-shaped (plain-w RMSNorm, SwiGLU, GQA)
+with int8 block-32 weights, the shape of the batched decode the library runs
+on a paged KV cache. The step order is the reference's per-layer order
+(KL/main.swift:321-347): rmsnorm -> qkv -> rope_kv -> attention -> o (+x) ->
+rmsnorm -> gate/up -> down (+x). Values are rounded where the GPU path stores
+them: the normed activations, the attention output and the GLU output to fp16
+(the fp16 operands of the batched matrix products, f32_to_f16 at
+KL/kernels.metal:361-365), the projections and the residual to fp32, K/V to
+fp16. Caches here are per sequence in the reference's layout [n_kv, ctx, hd].
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import ops
+
+F16, F32, F64 = np.float16, np.float32, np.float64
+
+
+@dataclass(frozen=True)
+class LayerConfig:
+    dim: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    ffn_dim: int
+    eps: float = 1e-5
+    rope_theta: float = 10000.0
+    act: str = "silu"
+    plus_one: bool = False
+
+    @property
+    def qkv_dim(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+
+LLAMA3_8B_LAYER = LayerConfig(dim=4096, n_heads=32, n_kv_heads=8, head_dim=128, ffn_dim=14336)
+
+
+def dequant(q: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """fp64 weights q * s (exact: an fp16 scale times an int8 fits in fp64)."""
+    M, K = q.shape
+    return (q.reshape(M, K // 32, 32).astype(F64) * s.astype(F64)[:, :, None]).reshape(M, K)
+
+
+def gemm_q8b32(q: np.ndarray, s: np.ndarray, X: np.ndarray) -> np.ndarray:
+    """Y[b] = matvec_q8b32(q, s, X[b]) for every row b, in fp64 (one
+    dequantisation, one BLAS product)."""
+    return np.asarray(X, dtype=F64) @ dequant(q, s).T
+
+
+def gate_up_rows(qg, sg, qu, su, X, act: str) -> np.ndarray:
+    g, u = gemm_q8b32(qg, sg, X), gemm_q8b32(qu, su, X)
+    return (ops.gelu_tanh(g) if act == "gelu_tanh" else ops.silu(g)) * u
+
+
+def layer_step(cfg: LayerConfig, W: dict, X: np.ndarray, kcaches: list, vcaches: list,
+               seq_lens: np.ndarray) -> np.ndarray:
+    """One decode step of the layer for every sequence; returns the new residual
+    rows (fp32 [B, D]) and appends each sequence's k, v (fp16) to its caches.
+
+    W: attn_norm, ffn_norm (fp32 [D]); wqkv, wo, wgate, wup, wdown as (q int8,
+    s fp16) pairs. kcaches[b], vcaches[b]: fp16 [n_kv, ctx_b, hd], ctx_b >=
+    seq_lens[b]."""
+    B = X.shape[0]
+    NH, NKV, hd = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+    invf = ops.inv_freq(hd, cfg.rope_theta)
+    scale = 1.0 / math.sqrt(hd)
+    X = np.asarray(X, dtype=F32)
+    xn = ops.rmsnorm(X, W["attn_norm"], cfg.eps, cfg.plus_one).astype(F16)
+    qkv = gemm_q8b32(*W["wqkv"], xn).astype(F32)
+    att = np.empty((B, NH * hd), dtype=F32)
+    for b in range(B):
+        pos = int(seq_lens[b]) - 1
+        q = ops.rope_kv(qkv[b], kcaches[b], vcaches[b], invf, NH, NKV, pos).astype(F32)
+        att[b] = ops.attention(q, kcaches[b], vcaches[b], pos + 1, NH, scale)
+    x1 = (X.astype(F64) + gemm_q8b32(*W["wo"], att.astype(F16))).astype(F32)
+    xn2 = ops.rmsnorm(x1, W["ffn_norm"], cfg.eps, cfg.plus_one).astype(F16)
+    h = gate_up_rows(*W["wgate"], *W["wup"], xn2, cfg.act).astype(F32).astype(F16)
+    return (x1.astype(F64) + gemm_q8b32(*W["wdown"], h)).astype(F32)

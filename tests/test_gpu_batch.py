@@ -1,0 +1,237 @@
+"""GPU parity of the ragged-batch path over the paged KV cache against the
+oracle: paged RoPE + append, paged split-L attention, the int8 block-32
+batched products (matrix cores from 16 rows, matvec per row below) and a
+whole Llama-shaped layer stepping a ragged batch, up to the full shape of 64
+sequences with KV lengths uniform in [128, 8192].
+
+Tolerances: relative 1e-4 on single-op fp32 outputs; 2e-3 on a whole layer
+(three fp16 roundings of activations can land one ulp apart between the GPU's
+fp32 and the oracle's fp64 arithmetic); appended cache entries within one fp16
+ulp. The contract is 1e-2.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import batch as obatch
+from oracle import ops as ref
+from tests.conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+F16, F32 = np.float16, np.float32
+
+
+def _d(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _bm():
+    from gemmagemini4hackathon2026_10_2425_amd import batch
+
+    return batch
+
+
+def _f16_close(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    assert np.max(np.abs(got - want) / np.maximum(np.abs(want), 6e-5)) <= 2**-10
+
+
+def _cache_with_rows(dev, rng, lens, nkv, hd, seed=11, stale=float("nan")):
+    """A one-layer page pool whose unused slots hold `stale`, with random rows
+    at positions 0..len-1 of every sequence; returns the cache and the rows."""
+    B = _bm()
+    table, n_pages = B.pack_ragged(lens, seed=seed)
+    cache = B.PagedCache(1, nkv, hd, table, n_pages, device=dev)
+    cache.k.fill_(stale)
+    cache.v.fill_(stale)
+    rows = []
+    for b, n in enumerate(lens):
+        k = rng.standard_normal((nkv, n, hd), dtype=F32).astype(F16)
+        v = rng.standard_normal((nkv, n, hd), dtype=F32).astype(F16)
+        cache.write(0, b, k, v)
+        rows.append((k, v))
+    return cache, rows
+
+
+@pytest.mark.parametrize("nh,nkv,hd", [(32, 8, 128), (8, 1, 256), (16, 16, 128)])
+@pytest.mark.parametrize("max_keys", [None, 32])
+def test_attention_paged(dev, rng, nh, nkv, hd, max_keys):
+    """Ragged lengths around page and block edges, shuffled pages, NaN in every
+    unused slot; max_keys below the longest sequence only changes the split
+    count, never the result."""
+    B = _bm()
+    lens = [1, 15, 16, 17, 31, 32, 33, 100, 513, 2048, 5000]
+    cache, rows = _cache_with_rows(dev, rng, lens, nkv, hd)
+    q = rng.standard_normal((len(lens), nh * hd), dtype=F32)
+    seq = _d(np.array(lens, np.int32), dev)
+    out = B.attention_paged(_d(q, dev), cache.k[0], cache.v[0], cache.table, seq, nh,
+                            max_keys=max_keys or max(lens))
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    for b, n in enumerate(lens):
+        want = ref.attention(q[b], rows[b][0], rows[b][1], n, nh, 1.0 / math.sqrt(hd))
+        assert rel_err(got[b], want) <= 1e-4, (b, n)
+
+
+def test_attention_paged_empty_sequence_and_strided_q(dev, rng):
+    """A sequence with no keys gets zeros; q read from qkv rows (stride > NH*hd)."""
+    B = _bm()
+    nh, nkv, hd = 8, 2, 128
+    lens = [0, 40, 7]
+    cache, rows = _cache_with_rows(dev, rng, [max(n, 1) for n in lens], nkv, hd)
+    stride = (nh + 2 * nkv) * hd
+    qkv = rng.standard_normal((len(lens), stride), dtype=F32)
+    out = B.attention_paged(_d(qkv, dev), cache.k[0], cache.v[0], cache.table, _d(np.array(lens, np.int32), dev),
+                            nh, max_keys=40, q_stride=stride).cpu().numpy()
+    assert (out[0] == 0).all()
+    for b in (1, 2):
+        want = ref.attention(qkv[b, : nh * hd], rows[b][0], rows[b][1], lens[b], nh, 1.0 / math.sqrt(hd))
+        assert rel_err(out[b], want) <= 1e-4
+
+
+def test_rope_kv_paged(dev, rng):
+    B = _bm()
+    nh, nkv, hd = 32, 8, 128
+    lens = [1, 16, 17, 40, 300]  # keys after the append: the new token sits at len - 1
+    table, n_pages = B.pack_ragged(lens, seed=5)
+    cache = B.PagedCache(1, nkv, hd, table, n_pages, device=dev)
+    qkv = rng.standard_normal((len(lens), (nh + 2 * nkv) * hd), dtype=F32)
+    invf = ref.inv_freq(hd, 10000.0)
+    qkv_d = _d(qkv, dev)
+    B.rope_kv_paged(qkv_d, cache.k[0], cache.v[0], _d(invf, dev), nh, nkv, cache.table,
+                    _d(np.array(lens, np.int32), dev))
+    got = qkv_d.cpu().numpy()
+    for b, n in enumerate(lens):
+        kc = np.zeros((nkv, n, hd), F16)
+        vc = np.zeros((nkv, n, hd), F16)
+        q_want = ref.rope_kv(qkv[b], kc, vc, invf, nh, nkv, n - 1)
+        assert rel_err(got[b, : nh * hd], q_want) <= 1e-5
+        k_rows, v_rows = cache.read(0, b, n)
+        _f16_close(k_rows[:, n - 1], kc[:, n - 1])
+        _f16_close(v_rows[:, n - 1], vc[:, n - 1])
+        assert not k_rows[:, : n - 1].any() and not v_rows[:, : n - 1].any()  # only the new position written
+
+
+def _qweights(rng, M, K):
+    from gemmagemini4hackathon2026_10_2425_amd.quant import quantize_q8b32
+
+    return quantize_q8b32((rng.standard_normal((M, K), dtype=F32) * 0.02).astype(F16))
+
+
+@pytest.mark.parametrize("rows", [1, 15, 16, 17, 64, 100])
+@pytest.mark.parametrize("M,K", [(1000, 4096), (96, 256), (257, 4160)])
+def test_gemm_q8b32(dev, rng, rows, M, K):
+    """Both sides of the matvec/matrix-core switch (16 rows; K % 128 for the
+    matrix cores) and both epilogues."""
+    B = _bm()
+    q, s = _qweights(rng, M, K)
+    X = rng.standard_normal((rows, K), dtype=F32).astype(F16)
+    want = obatch.gemm_q8b32(q, s, X)
+    qd, sd, Xd = _d(q, dev), _d(s, dev), _d(X, dev)
+    assert rel_err(B.gemm_q8b32(qd, sd, Xd).cpu().numpy(), want) <= 1e-4
+    Y0 = rng.standard_normal((rows, M), dtype=F32)
+    Yd = _d(Y0, dev)
+    B.gemm_q8b32(qd, sd, Xd, Yd, "add")
+    assert rel_err(Yd.cpu().numpy(), Y0 + want) <= 1e-4
+
+
+@pytest.mark.parametrize("splits", [1, 3, 32])
+def test_gemm_q8b32_k_splits(dev, rng, splits):
+    """Every K split (partials added in split order by the second kernel)."""
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
+    B = _bm()
+    M, K, rows = 300, 4096, 40
+    q, s = _qweights(rng, M, K)
+    X = rng.standard_normal((rows, K), dtype=F32).astype(F16)
+    want = obatch.gemm_q8b32(q, s, X)
+    try:
+        _lib.set_tunable("GM_SPLITS", splits)
+        Y0 = rng.standard_normal((rows, M), dtype=F32)
+        Yd = _d(Y0, dev)
+        B.gemm_q8b32(_d(q, dev), _d(s, dev), _d(X, dev), Yd, "add")
+        assert rel_err(Yd.cpu().numpy(), Y0 + want) <= 1e-4
+    finally:
+        _lib.set_tunable("GM_SPLITS", 0)
+
+
+@pytest.mark.parametrize("rows", [8, 16, 64])
+@pytest.mark.parametrize("act", ["silu", "gelu_tanh"])
+def test_gemm_gate_up_q8b32(dev, rng, rows, act):
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
+    B = _bm()
+    F, K = 1000, 1024
+    qg, sg = _qweights(rng, F, K)
+    qu, su = _qweights(rng, F, K)
+    X = rng.standard_normal((rows, K), dtype=F32).astype(F16)
+    want = obatch.gate_up_rows(qg, sg, qu, su, X, act)
+    args = [_d(a, dev) for a in (qg, sg, qu, su, X)]
+    for splits in (0, 4):  # as chosen, and forced partials
+        try:
+            _lib.set_tunable("GM_SPLITS", splits)
+            assert rel_err(B.gemm_gate_up_q8b32(*args, act).cpu().numpy(), want) <= 1e-4
+        finally:
+            _lib.set_tunable("GM_SPLITS", 0)
+
+
+def _layer_parity(dev, shape, lens, seed):
+    """Step a ragged batch through RaggedLayerQ8 and through the oracle; compare
+    the new residual rows and every sequence's appended K/V."""
+    from gemmagemini4hackathon2026_10_2425_amd import ops
+
+    B = _bm()
+    ocfg = obatch.LayerConfig(shape.dim, shape.n_heads, shape.n_kv_heads, shape.head_dim, shape.ffn_dim,
+                              shape.eps, shape.rope_theta, shape.act, shape.plus_one)
+    W = B.random_layer_weights(shape, seed)
+    table, n_pages = B.pack_ragged(lens, seed=seed)
+    cache = B.PagedCache(1, shape.n_kv_heads, shape.head_dim, table, n_pages, device=dev)
+    for pool, tid in ((cache.k, 1), (cache.v, 2)):  # every slot random, as a long-lived pool would hold
+        pool.copy_(ops.fill_normal(tuple(pool.shape), torch.float16, seed, tid, 1.0, dev))
+    rng = np.random.default_rng(seed)
+    X = rng.standard_normal((len(lens), shape.dim), dtype=F32)
+    kc, vc = zip(*[cache.read(0, b, n) for b, n in enumerate(lens)])
+    kc, vc = [k.copy() for k in kc], [v.copy() for v in vc]
+    want = obatch.layer_step(ocfg, W, X, kc, vc, np.array(lens))
+
+    layer = B.RaggedLayerQ8(shape, W, max_batch=len(lens), max_keys=max(lens), device=dev)
+    Xd = _d(X, dev)
+    layer.step(Xd, cache.k[0], cache.v[0], cache.table, _d(np.array(lens, np.int32), dev))
+    got = Xd.cpu().numpy()
+    assert rel_err(got, want) <= 2e-3
+    for b, n in enumerate(lens):
+        k, v = cache.read(0, b, n)
+        # the appended k/v derive from the fp16 normed activations, so they
+        # carry the same few-ulp spread as the outputs
+        assert rel_err(k[:, n - 1], kc[b][:, n - 1]) <= 2e-3
+        assert rel_err(v[:, n - 1], vc[b][:, n - 1]) <= 2e-3
+        assert np.array_equal(k[:, : n - 1], kc[b][:, : n - 1])  # older positions untouched
+
+
+def test_ragged_layer_small(dev):
+    B = _bm()
+    shape = B.LayerShape(dim=512, n_heads=8, n_kv_heads=2, head_dim=128, ffn_dim=1024)
+    lens = list(np.random.default_rng(3).integers(1, 300, 20)) + [1, 16, 17, 33]
+    _layer_parity(dev, shape, [int(n) for n in lens], seed=3)
+
+
+def test_ragged_layer_below_matrix_core_threshold(dev):
+    """Fewer than 16 sequences: the same layer through the per-row matvecs."""
+    B = _bm()
+    shape = B.LayerShape(dim=512, n_heads=8, n_kv_heads=2, head_dim=128, ffn_dim=1024)
+    _layer_parity(dev, shape, [5, 100, 37], seed=4)
+
+
+def test_ragged_layer_llama8b_64_sequences(dev):
+    """The full batched shape: one Llama-3-8B layer (hidden 4096, 32 Q / 8 KV
+    heads, head_dim 128, SwiGLU 14336, int8 block-32), 64 sequences with KV
+    lengths uniform in [128, 8192] in a shuffled 16-key page pool."""
+    B = _bm()
+    lens = np.random.default_rng(20261201).integers(128, 8193, 64) + 1  # + this step's token
+    _layer_parity(dev, B.LLAMA3_8B_LAYER, [int(n) for n in lens], seed=5)

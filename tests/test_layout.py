@@ -52,3 +52,70 @@ def test_to_from_tiles_roundtrip():
         tt = ops.to_tiles(torch.from_numpy(rows), which)
         assert np.array_equal(tt.numpy(), t)
         assert np.array_equal(ops.from_tiles(tt, which).numpy(), rows)
+
+
+# ---- paged KV cache (16-key pages, one slab per (page, kv head)) -------------
+
+
+@pytest.mark.parametrize("hd", [128, 256])
+@pytest.mark.parametrize("which", ["k", "v"])
+def test_page_offsets_are_a_slab_permutation(hd, which):
+    from gemmagemini4hackathon2026_10_2425_amd import batch
+
+    off = batch.page_offsets(hd, which)
+    assert off.shape == (16, hd)
+    assert np.array_equal(np.sort(off.reshape(-1)), np.arange(16 * hd))
+
+
+def test_page_operands_are_contiguous():
+    """K chunk c is one 1 KiB wave load (lane (r, g): dims 32c + 8g .. +7 of key r);
+    V dim tile t is one 512-byte load (lane (d, g): keys 4g .. 4g + 3 of dim 16t + d)."""
+    from gemmagemini4hackathon2026_10_2425_amd import batch
+
+    hd = 128
+    k, v = batch.page_offsets(hd, "k"), batch.page_offsets(hd, "v")
+    for lane in range(64):
+        r, g = lane & 15, lane >> 4
+        for c in range(hd // 32):
+            assert np.array_equal(k[r, 32 * c + 8 * g : 32 * c + 8 * g + 8], (c * 64 + lane) * 8 + np.arange(8))
+        for t in range(hd // 16):
+            assert np.array_equal(v[4 * g : 4 * g + 4, 16 * t + r], (t * 64 + lane) * 4 + np.arange(4))
+
+
+def test_pack_ragged_gives_each_sequence_its_own_pages():
+    from gemmagemini4hackathon2026_10_2425_amd import batch
+
+    lens = [0, 1, 15, 16, 17, 100, 4097]
+    table, n_pages = batch.pack_ragged(lens, seed=3)
+    need = [(n + 15) // 16 for n in lens]
+    assert n_pages == sum(need) and table.shape == (len(lens), max(need))
+    used = np.concatenate([table[b, : need[b]] for b in range(len(lens))])
+    assert np.array_equal(np.sort(used), np.arange(n_pages))  # a permutation of the pool
+    for b in range(len(lens)):
+        assert (table[b, need[b] :] == -1).all()
+    assert not np.array_equal(used, np.arange(n_pages))  # shuffled
+
+
+def test_paged_cache_write_read_roundtrip():
+    """Host-side fill and read of the pools invert each other (runs on the CPU)."""
+    from gemmagemini4hackathon2026_10_2425_amd import batch
+
+    rng = np.random.default_rng(1)
+    lens = [5, 33, 16]
+    table, n_pages = batch.pack_ragged(lens, seed=7)
+    cache = batch.PagedCache(2, 2, 128, table, n_pages, device="cpu")
+    rows = {}
+    for b, n in enumerate(lens):
+        k = rng.standard_normal((2, n, 128)).astype(np.float16)
+        v = rng.standard_normal((2, n, 128)).astype(np.float16)
+        cache.write(1, b, k, v)
+        rows[b] = (k, v)
+    for b, n in enumerate(lens):
+        k, v = cache.read(1, b, n)
+        assert np.array_equal(k, rows[b][0]) and np.array_equal(v, rows[b][1])
+    assert not cache.k[0].any()  # the other layer is untouched
+    # slab addressing: position p of sequence b, kv head h, dim d
+    b, p, h, d = 1, 20, 1, 77
+    page = table[b, p // 16]
+    flat = (page * 2 + h) * 16 * 128 + batch.page_offsets(128, "k")[p % 16, d]
+    assert cache.k[1].reshape(-1)[flat] == torch.tensor(rows[b][0][h, p, d])
