@@ -187,6 +187,48 @@ def copy_leg(steps: int, warmup: int, dev) -> dict:
     return {"bytes_read": 2 * n, "bytes_written": 2 * n, "us": ms * 1e3, "gbs": 4 * n / ms / 1e6}
 
 
+def ragged_layer_leg(steps: int, warmup: int, dev, n_seqs: int = 64) -> dict:
+    """One Llama-3-8B-shaped layer (hidden 4096, 32 Q / 8 KV heads, head_dim
+    128, SwiGLU 14336, int8 block-32 weights) stepping a ragged batch of 64
+    sequences with KV lengths uniform in [128, 8192] over a shuffled pool of
+    16-key pages. The step (10 launches) is captured once into a graph and
+    replayed; every replay appends at the same positions, so the work per
+    step is fixed. Bytes per step: the layer's weights once plus every
+    sequence's K and V once."""
+    import numpy as np
+    import torch
+
+    from gemmagemini4hackathon2026_10_2425_amd import _lib, batch, ops
+
+    shape = batch.LLAMA3_8B_LAYER
+    lens = np.random.default_rng(20261201).integers(128, 8193, n_seqs) + 1  # + this step's token
+    table, n_pages = batch.pack_ragged(lens, seed=5)
+    cache = batch.PagedCache(1, shape.n_kv_heads, shape.head_dim, table, n_pages, device=dev)
+    st = _stream()
+    for pool, tid in ((cache.k, 1), (cache.v, 2)):
+        _lib.call("mxd_fill_normal", pool.data_ptr(), _lib.MXD_F16, pool.numel(), 5, tid, 1.0, st)
+    layer = batch.RaggedLayerQ8(shape, batch.random_layer_weights(shape, 5), n_seqs, int(lens.max()), dev)
+    X = ops.fill_normal((n_seqs, shape.dim), torch.float32, 5, 3, 1.0, dev)
+    seq = torch.from_numpy(lens.astype(np.int32)).to(dev)
+
+    def step():
+        layer.step(X, cache.k[0], cache.v[0], cache.table, seq)
+
+    step()  # eager once (argument checks)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    ms = _events_time(lambda i: graph.replay(), steps, warmup)
+    kv_bytes = int(lens.sum()) * shape.n_kv_heads * shape.head_dim * 2 * 2
+    act_bytes = n_seqs * (shape.dim * 4 * 4 + shape.qkv_dim * 4 * 2 + shape.ffn_dim * 6)
+    nb = shape.weight_bytes + kv_bytes + act_bytes
+    flops = 2 * n_seqs * (shape.weight_bytes - 2 * shape.dim * 4) * 16 // 17
+    return {"us": ms * 1e3, "bytes": nb, "weight_bytes": shape.weight_bytes, "kv_bytes": kv_bytes,
+            "gbs": nb / ms / 1e6, "frac": nb / ms / 1e6 / PEAK_HBM_GBS, "seqs": n_seqs,
+            "kv_tokens": int(lens.sum()), "tok_s": n_seqs / ms * 1e3, "gemm_tflops": flops / ms / 1e9}
+
+
 def decode_leg(n_new: int = 256, prompt_len: int = 128, reps: int = 3) -> dict:
     """Gemma-2B-shaped greedy decode, timed like the reference's --bench-tg
     (KL/main.swift:605-618): wall clock over a run of pipelined steps that
@@ -249,7 +291,8 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="gemv_f16", choices=["gemv_f16", "gemv_q8", "attention", "decode", "copy"])
+    ap.add_argument("--workload", default="gemv_f16",
+                    choices=["gemv_f16", "gemv_q8", "attention", "decode", "ragged_layer", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-detail", action="store_true", help="skip the int8 / attention detail legs")
     args = ap.parse_args(argv)
@@ -273,6 +316,7 @@ def main(argv=None) -> int:
         legs = {"gemv_q8": lambda: gemv_q8_leg(args.steps, args.warmup, dev),
                 "attention": lambda: attention_leg(args.steps, args.warmup, dev),
                 "decode": decode_leg,
+                "ragged_layer": lambda: ragged_layer_leg(args.steps, args.warmup, dev),
                 "copy": lambda: copy_leg(args.steps, args.warmup, dev)}
         print(json.dumps({"workload": args.workload, **legs[args.workload]()}))
         return 0
@@ -287,6 +331,9 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
         log("decode leg")
         detail["decode_gemma2b"] = decode_leg()
+        torch.cuda.empty_cache()
+        log("ragged batch leg")
+        detail["ragged_layer_llama8b_64seq"] = ragged_layer_leg(args.steps, args.warmup, dev)
     detail["gemv_f16"] = g["per_shape"]
     cpu = None
     if not args.no_cpu:

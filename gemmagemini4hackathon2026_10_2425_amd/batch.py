@@ -37,13 +37,15 @@ PAGE = 16
 
 def page_offsets(head_dim: int, which: str) -> np.ndarray:
     """Offset (in halfs) of (key r, dim d) inside a (page, kv head) slab, as a
-    [16, head_dim] int64 array."""
+    [16, head_dim] int64 array: the slab holds one half of a 32-position tile
+    of the contiguous layout, each MFMA operand piece contiguous."""
     r = np.arange(PAGE)[:, None]
     d = np.arange(head_dim)[None, :]
     if which == "k":
-        return (((d >> 5) * 4 + ((d >> 3) & 3)) * 16 + r) * 8 + (d & 7)
+        rr = ((r >> 3) << 2) | (r & 3)
+        return ((((d >> 5) * 2 + ((r >> 2) & 1)) * 4 + ((d >> 3) & 3)) * 8 + rr) * 8 + (d & 7)
     if which == "v":
-        return (((d >> 4) * 4 + (r >> 2)) * 16 + (d & 15)) * 4 + (r & 3)
+        return (((d >> 4) * 2 + (r >> 3)) * 16 + (d & 15)) * 8 + (r & 7)
     raise ValueError(which)
 
 

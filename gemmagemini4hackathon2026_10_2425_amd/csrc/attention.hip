@@ -33,9 +33,10 @@
 //    directly. (A merge by the last-arriving split needs device-scope fences
 //    in every workgroup, which on a multi-XCD part costs more than a launch.)
 //  * the paged variant (a ragged batch of sequences over a pool of 16-key
-//    pages) runs the same core: a 32-key block is two pages, tile t of the
-//    scores is page t, and each lane addresses its own page, so a block is
-//    still one 1 KiB load per K operand and two 512-byte halves per V operand.
+//    pages) runs the same core: a 32-key block is two pages, each page holds
+//    one half of a contiguous tile, and each lane addresses its own page, so
+//    every operand is two 512-byte runs;
+//  * K and V are read with nontemporal loads: they stream through once.
 #include "common.hpp"
 
 namespace {
@@ -91,10 +92,10 @@ __device__ __forceinline__ void load_block(KVBlock<HD>& kv, const uint16_t* kbas
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int c = 0; c < HD / 32; ++c)
-            kv.k[t][c] = *reinterpret_cast<const h8_t*>(kt + (t * (HD / 32) + c) * 512);
+            kv.k[t][c] = __builtin_nontemporal_load(reinterpret_cast<const h8_t*>(kt + (t * (HD / 32) + c) * 512));
     const uint16_t* vt = vbase + (size_t)key0 * HD + 8 * lane;
 #pragma unroll
-    for (int d = 0; d < HD / 16; ++d) kv.v[d] = *reinterpret_cast<const h8_t*>(vt + d * 512);
+    for (int d = 0; d < HD / 16; ++d) kv.v[d] = __builtin_nontemporal_load(reinterpret_cast<const h8_t*>(vt + d * 512));
 }
 
 // A contiguous (tiled) cache of one kv head.
@@ -111,9 +112,10 @@ struct ContigKV {
 };
 
 // One sequence's pages of one kv head in the page pool (slab layouts in
-// common.hpp). Block b is pages 2b (score tile 0) and 2b + 1 (tile 1); row r
-// of tile t is key 16t + r, so slot j of lane group g is key
-// 16 (j >> 2) + 4g + (j & 3), which is also the order V's slab stores keys in.
+// common.hpp). Block b is pages 2b (keys 0..15 of the block) and 2b + 1 (keys
+// 16..31): a slab holds that half of the contiguous tile, so the key of each
+// score slot is the same as in ContigKV and only the addresses differ. Lanes
+// with col < 8 read K from the first page, lane groups g < 2 read V from it.
 template <int HD>
 struct PagedKV {
     const uint16_t* kpool;
@@ -129,23 +131,22 @@ struct PagedKV {
         return (size_t)p * page_stride + (size_t)kvh * mxd::PAGE_KEYS * HD;
     }
     __device__ __forceinline__ void load(KVBlock<HD>& kv, int b, int lane) const {
-        // A ragged last block has one page: its second tile re-reads the first
+        // A ragged last block has one page: its second half re-reads the first
         // page, and every key of it is masked.
         const size_t s0 = slab(2 * b), s1 = slab(min(2 * b + 1, npages - 1));
+        const int col = lane & 15, g = lane >> 4;
+        const uint16_t* kp = kpool + ((col >> 3) ? s1 : s0) + (size_t)(g * 8 + (col & 7)) * 8;
+        const uint16_t* vp = vpool + ((g >> 1) ? s1 : s0) + (size_t)((g & 1) * 16 + col) * 8;
 #pragma unroll
-        for (int c = 0; c < HD / 32; ++c) {
-            kv.k[0][c] = *reinterpret_cast<const h8_t*>(kpool + s0 + (size_t)(c * 64 + lane) * 8);
-            kv.k[1][c] = *reinterpret_cast<const h8_t*>(kpool + s1 + (size_t)(c * 64 + lane) * 8);
-        }
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int d = 0; d < HD / 16; ++d) {
-            const u2_t lo = *reinterpret_cast<const u2_t*>(vpool + s0 + (size_t)(d * 64 + lane) * 4);
-            const u2_t hi = *reinterpret_cast<const u2_t*>(vpool + s1 + (size_t)(d * 64 + lane) * 4);
-            const u4_t w = {lo.x, lo.y, hi.x, hi.y};
-            __builtin_memcpy(&kv.v[d], &w, 16);
-        }
+            for (int c = 0; c < HD / 32; ++c)
+                kv.k[t][c] = __builtin_nontemporal_load(reinterpret_cast<const h8_t*>(kp + (c * 2 + t) * 256));
+#pragma unroll
+        for (int d = 0; d < HD / 16; ++d)
+            kv.v[d] = __builtin_nontemporal_load(reinterpret_cast<const h8_t*>(vp + d * 256));
     }
-    static __device__ __forceinline__ int key(int g, int j) { return 16 * (j >> 2) + 4 * g + (j & 3); }
+    static __device__ __forceinline__ int key(int g, int j) { return 8 * g + j; }
 };
 
 // One split of one kv head of one sequence: keys [0, n), S splits, q and out

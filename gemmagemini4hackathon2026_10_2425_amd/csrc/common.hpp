@@ -127,20 +127,22 @@ __device__ __forceinline__ int v_tile_offset(int k, int d) {
 
 // Paged KV cache: a page holds PAGE_KEYS positions of every kv head; the
 // (page, kv head) slab of PAGE_KEYS * hd fp16 values starts at
-// (page * n_kv + kvh) * PAGE_KEYS * hd and is stored in MFMA operand order.
-// Offsets (in halfs) of key r (0..15) and dim d inside a slab:
-//   K: (((d >> 5) * 4 + ((d >> 3) & 3)) * 16 + r) * 8 + (d & 7)
-//      (chunk d >> 5 is one 1 KiB wave load: lane (r, (d >> 3) & 3) holds 8 dims)
-//   V: (((d >> 4) * 4 + (r >> 2)) * 16 + (d & 15)) * 4 + (r & 3)
-//      (dim tile d >> 4 is one 512-byte wave load: lane (d & 15, r >> 2) holds 4 keys)
+// (page * n_kv + kvh) * PAGE_KEYS * hd. A slab is one half of a 32-position
+// tile of the contiguous layout above, with that half's pieces made
+// contiguous, so a 32-key block is two pages and every MFMA operand is two
+// 512-byte runs. Offsets (in halfs) of key r (0..15) and dim d in a slab:
+//   K: ((((d >> 5) * 2 + ((r >> 2) & 1)) * 4 + ((d >> 3) & 3)) * 8 + rr) * 8 + (d & 7),
+//      rr = ((r >> 3) << 2) | (r & 3)
+//   V: (((d >> 4) * 2 + (r >> 3)) * 16 + (d & 15)) * 8 + (r & 7)
 constexpr int PAGE_KEYS = 16;
 
 __host__ __device__ __forceinline__ int k_page_offset(int r, int d) {
-    return (((d >> 5) * 4 + ((d >> 3) & 3)) * 16 + r) * 8 + (d & 7);
+    const int rr = ((r >> 3) << 2) | (r & 3);
+    return ((((d >> 5) * 2 + ((r >> 2) & 1)) * 4 + ((d >> 3) & 3)) * 8 + rr) * 8 + (d & 7);
 }
 
 __host__ __device__ __forceinline__ int v_page_offset(int r, int d) {
-    return (((d >> 4) * 4 + (r >> 2)) * 16 + (d & 15)) * 4 + (r & 3);
+    return (((d >> 4) * 2 + (r >> 3)) * 16 + (d & 15)) * 8 + (r & 7);
 }
 
 }  // namespace mxd

@@ -11,28 +11,32 @@
 // int8 (exact in fp16), products exact in fp32 and fp32 accumulation.
 //
 // Work layout (gfx950, v_mfma_f32_16x16x32_f16):
-//  * a workgroup of 4 waves owns 64 weight rows (16 per wave; for the
-//    gate/up pair 32 rows of each matrix) x 64 activation rows x one split of K;
-//  * K advances in steps of 128 (4 quantisation blocks): the 64 x 128 fp16
-//    activation tile is staged in LDS once per workgroup (rows padded by
-//    16 bytes so the 16-byte MFMA-operand reads are conflict-free) while every
-//    wave streams its own weight rows straight from HBM into registers, one
-//    step ahead of the math;
+//  * a workgroup of 8 waves owns 128 weight rows (16 per wave; for the
+//    gate/up pair 64 rows of each matrix) x 64 activation rows x one split of
+//    K of at most 1024 (8 steps of 128 = 4 quantisation blocks);
+//  * the split's whole 64 x <=1024 fp16 activation slice is loaded into LDS
+//    once (rows padded by 16 bytes so the 16-byte MFMA-operand reads are
+//    conflict-free); after that one barrier the waves never synchronise
+//    again: each streams its own weight rows straight from HBM through a
+//    register ring GM_PD steps ahead of the math;
 //  * one MFMA per (block, 16 activation rows) with the activations as the A
 //    operand and the weights as B, so each lane's four results share one
 //    weight row and one scale: acc += s * mfma(x, q, 0);
-//  * small weight matrices split K across workgroups to fill the GPU; the
-//    fp32 partials are added in a fixed order by a second kernel that also
-//    applies the epilogue, so results are deterministic.
+//  * K is split across workgroups (as many splits as the LDS slice needs, and
+//    enough workgroups to fill the GPU); the fp32 partials are added in a
+//    fixed order by a second kernel that also applies the epilogue, so
+//    results are deterministic.
 #include "common.hpp"
 
 namespace {
 
-constexpr int GM_THREADS = 256;  // 4 waves
-constexpr int GM_ROWS = 64;      // weight rows per workgroup (over both matrices)
-constexpr int GM_BATCH = 64;     // activation rows per workgroup
-constexpr int GM_KC = 128;       // K per step (4 blocks)
-constexpr int GM_XP = GM_KC + 8; // LDS pitch in halfs (+16 bytes)
+constexpr int GM_WAVES = 8;
+constexpr int GM_THREADS = GM_WAVES * 64;
+constexpr int GM_ROWS = 16 * GM_WAVES;  // weight rows per workgroup (over both matrices)
+constexpr int GM_BATCH = 64;            // activation rows per workgroup
+constexpr int GM_KC = 128;              // K per step (4 blocks)
+constexpr int GM_SMAX = 8;              // steps per split (LDS slice of 64 x 1024 halfs)
+constexpr int GM_XP = GM_SMAX * GM_KC + 8;  // LDS pitch in halfs (+16 bytes)
 
 struct GemmArgs {
     const int8_t* W[2];
@@ -54,77 +58,122 @@ __device__ __forceinline__ float epilogue(float g, float u, float old) {
     }
 }
 
-// One K step of weights for one lane: 4 blocks x 8 int8 and the 4 scales.
-struct WStep {
-    u2_t q[4];
-    u2_t s;
-};
+
+
+// Weight steps kept in flight per lane (a register ring), and the per-wave
+// LDS staging of one step's weights (16 rows of 128 bytes, rows padded by 16
+// bytes: the 8-byte MFMA-operand reads are conflict-free) and of the split's
+// scales (16 rows x up to 32 blocks).
+constexpr int GM_PD = 4;
+constexpr int GM_WP = GM_KC + 16;
+constexpr size_t GM_LDS_X = (size_t)GM_BATCH * GM_XP * 2;
+constexpr size_t GM_LDS_W = (size_t)GM_WAVES * 16 * GM_WP;
+constexpr size_t GM_LDS_S = (size_t)GM_WAVES * 16 * GM_SMAX * 4 * 2;
+constexpr size_t GM_LDS = GM_LDS_X + GM_LDS_W + GM_LDS_S;  // 155 KiB of the CU's 160
 
 template <int NMAT, int OP>
 __global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
-    constexpr int ROWS_PER_MAT = GM_ROWS / NMAT;      // 64 or 32
-    constexpr int WAVES_PER_MAT = 4 / NMAT;           // 4 or 2
-    __shared__ __attribute__((aligned(16))) _Float16 xs[GM_BATCH * GM_XP];
+    constexpr int ROWS_PER_MAT = GM_ROWS / NMAT;       // 128 or 64
+    constexpr int WAVES_PER_MAT = GM_WAVES / NMAT;     // 8 or 4
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    _Float16* xs = reinterpret_cast<_Float16*>(smem);  // [GM_BATCH][GM_XP]
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, g = lane >> 4;
+    unsigned char* wst = smem + GM_LDS_X + (size_t)wave * 16 * GM_WP;                          // [16][GM_WP]
+    uint16_t* sst = reinterpret_cast<uint16_t*>(smem + GM_LDS_X + GM_LDS_W) + wave * 16 * GM_SMAX * 4;  // [16][32]
     const int m = wave / WAVES_PER_MAT;  // which matrix this wave reads
     const int row0 = blockIdx.x * ROWS_PER_MAT + 16 * (wave % WAVES_PER_MAT);
     const int split = blockIdx.y, b0 = blockIdx.z * GM_BATCH;
     const int M = a.M, K = a.K;
-    const int ks0 = split * a.ksteps / a.splits, ks1 = (split + 1) * a.ksteps / a.splits;
+    const int ks0 = split * a.ksteps / a.splits, ks1 = (split + 1) * a.ksteps / a.splits;  // <= GM_SMAX steps
+    const int nst = ks1 - ks0;
 
-    // This lane's weight row (clamped: rows past M compute garbage that is
-    // never stored) and its scale row.
-    const int wrow = min(row0 + col, M - 1);
-    const int8_t* wq = a.W[m] + (size_t)wrow * K + 8 * g;
-    const uint16_t* ws = a.S[m] + (size_t)wrow * (K / 32);
-
-    auto load_w = [&](WStep& st, int ks) {
-        const int8_t* p = wq + (size_t)ks * GM_KC;
+    // Weights are read row-contiguously: load u of a step gives lane l the 16
+    // bytes at 16 (l & 7) of row 8u + (l >> 3)'s 128-byte step segment, so each
+    // load is 8 whole 128-byte lines. Rows past M are clamped (never stored).
+    const int8_t* wbase[2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) st.q[j] = __builtin_nontemporal_load(reinterpret_cast<const u2_t*>(p + 32 * j));
-        st.s = *reinterpret_cast<const u2_t*>(ws + ks * 4);
+    for (int u = 0; u < 2; ++u)
+        wbase[u] = a.W[m] + (size_t)min(row0 + 8 * u + (lane >> 3), M - 1) * K + (size_t)ks0 * GM_KC + 16 * (lane & 7);
+    auto load_w = [&](u4_t (&st)[2], int t) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            st[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wbase[u] + (size_t)t * GM_KC));
     };
+    u4_t w[GM_PD][2];
+#pragma unroll
+    for (int p = 0; p < GM_PD; ++p)
+        if (p < nst) load_w(w[p], p);
+
+    // The split's scales: lane (col, g) fetches the 4 scales of steps g and
+    // g + 4 of its row col.
+    {
+        const uint16_t* srow = a.S[m] + (size_t)min(row0 + col, M - 1) * (K / 32) + (size_t)ks0 * 4;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int t = g + 4 * h;
+            if (t < nst)
+                *reinterpret_cast<u2_t*>(&sst[col * GM_SMAX * 4 + 4 * t]) = *reinterpret_cast<const u2_t*>(srow + 4 * t);
+        }
+    }
+
+    // Activation slice: 64 rows x nst * 128 halfs, 16-byte pieces, rows past
+    // n_rows zero. At most 64 * 8 * 16 = 8192 pieces, 16 per thread.
+    {
+        const int per_row = nst * (GM_KC / 8);
+        const int total = GM_BATCH * per_row;
+#pragma unroll
+        for (int u = 0; u < GM_BATCH * GM_SMAX * (GM_KC / 8) / GM_THREADS; ++u) {
+            const int idx = threadIdx.x + GM_THREADS * u;
+            if (idx < total) {
+                const int r = idx / per_row, piece = idx - r * per_row;
+                u4_t v = {0u, 0u, 0u, 0u};
+                if (b0 + r < a.n_rows)
+                    v = *reinterpret_cast<const u4_t*>(a.X + (size_t)(b0 + r) * K + (size_t)ks0 * GM_KC + piece * 8);
+                *reinterpret_cast<u4_t*>(&xs[r * GM_XP + piece * 8]) = v;
+            }
+        }
+    }
+    __syncthreads();
 
     f4_t acc[4];
 #pragma unroll
     for (int bg = 0; bg < 4; ++bg) acc[bg] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-    WStep cur, nxt;
-    if (ks0 < ks1) load_w(cur, ks0);
-    for (int ks = ks0; ks < ks1; ++ks) {
-        if (ks + 1 < ks1) load_w(nxt, ks + 1);
-        // Stage the 64 x 128 activation tile: 1024 16-byte pieces, 4 per thread.
+    const f4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kb = 0; kb < nst; kb += GM_PD) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int idx = threadIdx.x + GM_THREADS * u;
-            const int r = idx >> 4, seg = idx & 15;
-            u4_t v = {0u, 0u, 0u, 0u};
-            if (b0 + r < a.n_rows)
-                v = *reinterpret_cast<const u4_t*>(a.X + (size_t)(b0 + r) * K + (size_t)ks * GM_KC + seg * 8);
-            *reinterpret_cast<u4_t*>(&xs[r * GM_XP + seg * 8]) = v;
-        }
-        __syncthreads();
-        const f4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int p = 0; p < GM_PD; ++p) {
+            const int t = kb + p;  // step within the split
+            if (t < nst) {
+                // The step's weights through this wave's LDS slab into MFMA
+                // operand order (only this wave touches the slab: LDS accesses
+                // of one wave are ordered, the wave barrier orders the code).
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            h2_t h[4];
-            mxd::i8x4_to_h2x2(cur.q[j].x, h[0], h[1]);
-            mxd::i8x4_to_h2x2(cur.q[j].y, h[2], h[3]);
-            const h8_t wop = {h[0].x, h[0].y, h[1].x, h[1].y, h[2].x, h[2].y, h[3].x, h[3].y};
-            const uint16_t sb = (uint16_t)((j & 1) ? (cur.s[j >> 1] >> 16) : (cur.s[j >> 1] & 0xFFFFu));
-            const float sc = mxd::h2f(sb);
+                for (int u = 0; u < 2; ++u)
+                    *reinterpret_cast<u4_t*>(wst + (8 * u + (lane >> 3)) * GM_WP + 16 * (lane & 7)) = w[p][u];
+                if (t + GM_PD < nst) load_w(w[p], t + GM_PD);
+                __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int bg = 0; bg < 4; ++bg) {
-                const h8_t xop = *reinterpret_cast<const h8_t*>(&xs[(bg * 16 + col) * GM_XP + 32 * j + 8 * g]);
-                const f4_t c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xop, wop, zero, 0, 0, 0);
+                for (int j = 0; j < 4; ++j) {
+                    const u2_t q = *reinterpret_cast<const u2_t*>(wst + col * GM_WP + 32 * j + 8 * g);
+                    h2_t h[4];
+                    mxd::i8x4_to_h2x2(q.x, h[0], h[1]);
+                    mxd::i8x4_to_h2x2(q.y, h[2], h[3]);
+                    const h8_t wop = {h[0].x, h[0].y, h[1].x, h[1].y, h[2].x, h[2].y, h[3].x, h[3].y};
+                    const float sc = mxd::h2f(sst[col * GM_SMAX * 4 + 4 * t + j]);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[bg][i] = fmaf(sc, c[i], acc[bg][i]);
+                    for (int bg = 0; bg < 4; ++bg) {
+                        const h8_t xop = *reinterpret_cast<const h8_t*>(
+                            &xs[(bg * 16 + col) * GM_XP + t * GM_KC + 32 * j + 8 * g]);
+                        const f4_t c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xop, wop, zero, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[bg][i] = fmaf(sc, c[i], acc[bg][i]);
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
             }
         }
-        __syncthreads();  // the tile is rewritten next step
-        cur = nxt;
     }
 
     // Lane (col, g) holds rows b0 + 16 bg + 4 g + i of weight row row0 + col.
@@ -142,14 +191,16 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
         return;
     }
     if constexpr (NMAT == 2) {
-        // The up waves (2, 3) hand their sums to the gate waves (0, 1) holding
-        // the same rows through LDS (the activation tile is no longer needed).
-        float* xf = reinterpret_cast<float*>(xs);
+        // The up waves hand their sums to the gate waves holding the same rows
+        // through LDS (the activation slice is no longer needed).
+        float* xf = reinterpret_cast<float*>(smem);
+        __syncthreads();
         if (m == 1) {
 #pragma unroll
             for (int bg = 0; bg < 4; ++bg)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) xf[(((wave - 2) * 4 + bg) * 4 + i) * 64 + lane] = acc[bg][i];
+                for (int i = 0; i < 4; ++i)
+                    xf[(((wave - WAVES_PER_MAT) * 4 + bg) * 4 + i) * 64 + lane] = acc[bg][i];
         }
         __syncthreads();
         if (m == 1 || wr >= M) return;
@@ -197,12 +248,15 @@ bool use_mfma(int n_rows, int K) {
     return n_rows >= mxd::tunable("GM_MIN_ROWS", 16) && K % GM_KC == 0;
 }
 
-// K splits: enough workgroups for about two per CU, at least one K step each.
+// K splits: at least enough that a split's activation slice fits the LDS
+// (GM_SMAX steps), and enough workgroups for one per CU; the GM_SPLITS tunable
+// can ask for more (up to one step per split), never fewer.
 int pick_splits(int n_rows, int M, int K, int nmat) {
     const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + GM_BATCH - 1) / GM_BATCH);
     const int ksteps = K / GM_KC;
-    int s = mxd::tunable("GM_SPLITS", max(1, 512 / tiles));
-    return max(1, min(s, ksteps));
+    const int min_s = (ksteps + GM_SMAX - 1) / GM_SMAX;
+    int s = mxd::tunable("GM_SPLITS", max(min_s, (256 + tiles - 1) / tiles));
+    return max(min_s, min(s, ksteps));
 }
 
 size_t ws_bytes_for(int n_rows, int M, int K, int nmat) {
@@ -220,7 +274,12 @@ int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char
                 fn, need, ws_bytes);
     a.part = static_cast<float*>(ws);
     const dim3 grid((a.M + GM_ROWS / NMAT - 1) / (GM_ROWS / NMAT), a.splits, (a.n_rows + GM_BATCH - 1) / GM_BATCH);
-    hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP>), grid, dim3(GM_THREADS), 0, s, a);
+    const size_t lds = GM_LDS;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_q8_kernel<NMAT, OP>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    MXD_REQUIRE(attr == hipSuccess, MXD_ERR_HIP, "%s: cannot enable %zu bytes of LDS: %s", fn, lds,
+                hipGetErrorString(attr));
+    hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP>), grid, dim3(GM_THREADS), lds, s, a);
     if (a.splits > 1) {
         const size_t n = (size_t)a.n_rows * a.M;
         const size_t nb = (n + 255) / 256;

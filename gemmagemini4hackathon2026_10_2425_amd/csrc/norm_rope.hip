@@ -22,12 +22,43 @@ __device__ __forceinline__ float block_sum(float v, float* scratch) {
 
 // y = x * rsqrt(mean(x^2) + eps) * (1 + w | w), one workgroup per row
 // (KL/kernels.metal:71-96).
+// Rows of up to NORM_CACHE * 4 * NORM_THREADS floats (D % 4 == 0) are read once
+// with 16-byte loads, all in flight together, and kept in registers for the
+// second pass; other rows take the plain two-pass loop.
+constexpr int NORM_CACHE = 8;
+
 template <typename YT, bool PLUS_ONE>
 __global__ void __launch_bounds__(NORM_THREADS)
 rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w, YT* __restrict__ y, int D, float eps) {
     __shared__ float scratch[NORM_THREADS / 64];
     const float* xr = x + (size_t)blockIdx.x * D;
     YT* yr = y + (size_t)blockIdx.x * D;
+    if (D % 4 == 0 && D <= NORM_CACHE * 4 * NORM_THREADS) {
+        f4_t v[NORM_CACHE];
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < NORM_CACHE; ++u) {
+            const int i = (threadIdx.x + u * NORM_THREADS) * 4;
+            v[u] = i < D ? *reinterpret_cast<const f4_t*>(xr + i) : f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < NORM_CACHE; ++u)
+            ss = fmaf(v[u].x, v[u].x, fmaf(v[u].y, v[u].y, fmaf(v[u].z, v[u].z, fmaf(v[u].w, v[u].w, ss))));
+        ss = block_sum(ss, scratch);
+        const float scale = rsqrtf(ss / (float)D + eps);
+#pragma unroll
+        for (int u = 0; u < NORM_CACHE; ++u) {
+            const int i = (threadIdx.x + u * NORM_THREADS) * 4;
+            if (i < D) {
+                const f4_t wv = *reinterpret_cast<const f4_t*>(w + i);
+                const float xs[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+                const float ws[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) yr[i + e] = (YT)(xs[e] * scale * (PLUS_ONE ? 1.0f + ws[e] : ws[e]));
+            }
+        }
+        return;
+    }
     float ss = 0.0f;
     for (int i = threadIdx.x; i < D; i += NORM_THREADS) ss = fmaf(xr[i], xr[i], ss);
     ss = block_sum(ss, scratch);

@@ -200,9 +200,11 @@ int mxd_argmax(const float* logits, int32_t* tokens, int N, int out_idx, void* w
  *
  * Page pool (per layer): n_pages pages of 16 positions of every kv head; the
  * (page, kv head) slab of 16 * head_dim fp16 values starts at element
- * (page * n_kv_heads + kvh) * 16 * head_dim and is stored in MFMA operand order:
- *   K: key r (0..15), dim d at (((d >> 5) * 4 + ((d >> 3) & 3)) * 16 + r) * 8 + (d & 7)
- *   V: key r, dim d at (((d >> 4) * 4 + (r >> 2)) * 16 + (d & 15)) * 4 + (r & 3)
+ * (page * n_kv_heads + kvh) * 16 * head_dim and is stored in MFMA operand order
+ * (one half of a 32-position tile of the contiguous layout, made contiguous):
+ *   K: key r (0..15), dim d at ((((d >> 5) * 2 + ((r >> 2) & 1)) * 4 + ((d >> 3) & 3)) * 8 + rr) * 8 + (d & 7),
+ *      rr = ((r >> 3) << 2) | (r & 3)
+ *   V: key r, dim d at (((d >> 4) * 2 + (r >> 3)) * 16 + (d & 15)) * 8 + (r & 7)
  * page_table is int32 [n_seqs][max_pages]: entry [b][i] is the pool page that
  * holds positions 16i .. 16i + 15 of sequence b (any order; the pool is shared).
  * seq_lens is int32 [n_seqs]: the keys of sequence b after this step's append,

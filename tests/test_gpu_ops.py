@@ -187,7 +187,7 @@ def test_gate_up(dev, rng, act, fmt):
 # ---------------------------------------------------------------- norms, embed
 
 
-@pytest.mark.parametrize("D", [2048, 4096, 100])
+@pytest.mark.parametrize("D", [2048, 4096, 100, 102, 16384])
 @pytest.mark.parametrize("plus_one", [False, True])
 @pytest.mark.parametrize("out", [torch.float32, torch.float16])
 def test_rmsnorm(dev, rng, D, plus_one, out):

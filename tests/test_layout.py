@@ -67,19 +67,29 @@ def test_page_offsets_are_a_slab_permutation(hd, which):
     assert np.array_equal(np.sort(off.reshape(-1)), np.arange(16 * hd))
 
 
-def test_page_operands_are_contiguous():
-    """K chunk c is one 1 KiB wave load (lane (r, g): dims 32c + 8g .. +7 of key r);
-    V dim tile t is one 512-byte load (lane (d, g): keys 4g .. 4g + 3 of dim 16t + d)."""
+def test_page_operands_are_two_runs():
+    """Every K and V MFMA operand of a block is two 512-byte runs, one per page,
+    and each lane gets the same (key, dims) as from the contiguous tile (the
+    key of the block it holds is checked against the contiguous layout's):
+    lane (col, g) of K chunk (t, c) reads page col >> 3, of V tile d page g >> 1."""
     from gemmagemini4hackathon2026_10_2425_amd import batch
 
     hd = 128
     k, v = batch.page_offsets(hd, "k"), batch.page_offsets(hd, "v")
-    for lane in range(64):
-        r, g = lane & 15, lane >> 4
+    for t in range(2):
         for c in range(hd // 32):
-            assert np.array_equal(k[r, 32 * c + 8 * g : 32 * c + 8 * g + 8], (c * 64 + lane) * 8 + np.arange(8))
-        for t in range(hd // 16):
-            assert np.array_equal(v[4 * g : 4 * g + 4, 16 * t + r], (t * 64 + lane) * 4 + np.arange(4))
+            for lane in range(64):
+                col, g = lane & 15, lane >> 4
+                key = 8 * (col >> 2) + 4 * t + (col & 3)  # the contiguous tile's key of this lane
+                assert key >> 4 == col >> 3
+                got = k[key & 15, 32 * c + 8 * g : 32 * c + 8 * g + 8]
+                assert np.array_equal(got, (c * 2 + t) * 256 + (g * 8 + (col & 7)) * 8 + np.arange(8))
+    for d in range(hd // 16):
+        for lane in range(64):
+            col, g = lane & 15, lane >> 4
+            keys = np.arange(8 * g, 8 * g + 8)
+            got = v[keys & 15, 16 * d + col]
+            assert np.array_equal(got, d * 256 + ((g & 1) * 16 + col) * 8 + np.arange(8))
 
 
 def test_pack_ragged_gives_each_sequence_its_own_pages():
