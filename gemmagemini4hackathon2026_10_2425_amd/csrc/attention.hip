@@ -27,7 +27,8 @@
 //    8 KiB (hd 128) run per cache.
 //  * 32-key blocks are dealt round-robin to the splits of a kv head (split s
 //    takes blocks s, s+S, ...), so the grid streams the cache front to back;
-//    for head_dim 128 each wave prefetches its next block while it computes.
+//    each wave keeps one block in flight (prefetching the next one is a
+//    tunable, measured slower).
 //  * splits write unnormalised (O, max, sum) partials, merged by a second small
 //    kernel with the log-sum-exp rule; a single split writes the output
 //    directly. (A merge by the last-arriving split needs device-scope fences
@@ -41,8 +42,7 @@
 
 namespace {
 
-constexpr int ATT_WAVES = 4;
-constexpr int ATT_THREADS = ATT_WAVES * 64;
+constexpr int ATT_WAVES = 4;  // default waves per workgroup
 constexpr int BLK = 32;  // keys per wave step
 constexpr int MAX_SPLITS = 512;
 constexpr int PAGED_BPS = 16;  // 32-key blocks per split of a paged sequence (4 per wave)
@@ -151,23 +151,21 @@ struct PagedKV {
 
 // One split of one kv head of one sequence: keys [0, n), S splits, q and out
 // rows of this sequence, partials of this sequence.
-template <int HD, typename KV>
+template <int HD, int W, bool PREFETCH, typename KV>
 __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int n, int S, int split, int kvh,
                                           const float* qrow, float* orow, float* ws_o, float* ws_ml) {
     constexpr int NC = HD / 32;  // MFMA k-chunks over head_dim for Q.K
     constexpr int ND = HD / 16;  // 16-wide dim tiles for P.V
-    // Prefetching the next block doubles the K/V registers; it fits the
-    // register budget (2 waves per SIMD either way) for head_dim 128 only.
-    constexpr bool PREFETCH = HD == 128;
-    __shared__ float sm_o[ATT_WAVES][8][HD];
-    __shared__ float sm_m[ATT_WAVES][8];
-    __shared__ float sm_l[ATT_WAVES][8];
+    constexpr int NT = W * 64;
+    __shared__ float sm_o[W][8][HD];
+    __shared__ float sm_m[W][8];
+    __shared__ float sm_l[W][8];
 
     const int nblocks = (n + BLK - 1) / BLK;
     const int G = a.G;
     if (nblocks == 0) {  // no keys (an empty sequence): the output is zero
         if (split == 0)
-            for (int idx = threadIdx.x; idx < G * HD; idx += ATT_THREADS) orow[(size_t)kvh * G * HD + idx] = 0.0f;
+            for (int idx = threadIdx.x; idx < G * HD; idx += NT) orow[(size_t)kvh * G * HD + idx] = 0.0f;
         return;
     }
     if (split >= min(S, nblocks)) return;  // an empty split
@@ -179,7 +177,7 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
     // and wave w takes every 4th of those, so at any moment the splits of a kv
     // head stream one contiguous run of the cache. The first block's loads go
     // out before the q operand is built so the two latencies overlap.
-    const int step = S * ATT_WAVES;
+    const int step = S * W;
     int b = split + S * wave;
     KVBlock<HD> cur, nxt;
     if (b < nblocks) src.load(cur, b, lane);
@@ -317,14 +315,14 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
 
     // ---- merge the 4 waves (and write the split's partial or the output)
     const int n_active = min(S, nblocks);
-    for (int idx = threadIdx.x; idx < G * HD; idx += ATT_THREADS) {
+    for (int idx = threadIdx.x; idx < G * HD; idx += NT) {
         const int h = idx / HD, dim = idx - h * HD;
         float M = sm_m[0][h];
 #pragma unroll
-        for (int w = 1; w < ATT_WAVES; ++w) M = fmaxf(M, sm_m[w][h]);
+        for (int w = 1; w < W; ++w) M = fmaxf(M, sm_m[w][h]);
         float so = 0.0f, sl = 0.0f;
 #pragma unroll
-        for (int w = 0; w < ATT_WAVES; ++w) {
+        for (int w = 0; w < W; ++w) {
             const float f = exp2f(sm_m[w][h] - M);
             so += f * sm_o[w][h][dim];
             sl += f * sm_l[w][h];
@@ -342,11 +340,11 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
     }
 }
 
-template <int HD>
-__global__ void __launch_bounds__(ATT_THREADS) attn_split_kernel(AttnArgs a) {
+template <int HD, int W, bool PF>
+__global__ void __launch_bounds__(W * 64) attn_split_kernel(AttnArgs a) {
     const int kvh = blockIdx.y;
     const ContigKV<HD> src{a.k + (size_t)kvh * a.max_ctx * HD, a.v + (size_t)kvh * a.max_ctx * HD};
-    attn_core<HD>(a, src, n_keys_of(a), a.n_splits, blockIdx.x, kvh, a.q, a.out, a.ws_o, a.ws_ml);
+    attn_core<HD, W, PF>(a, src, n_keys_of(a), a.n_splits, blockIdx.x, kvh, a.q, a.out, a.ws_o, a.ws_ml);
 }
 
 // Keys and splits of paged sequence seq (clamped so a bad length can never
@@ -359,37 +357,39 @@ __device__ __forceinline__ int paged_splits(const AttnArgs& a, int n) {
     return min(a.n_splits, max(1, (nblocks + PAGED_BPS - 1) / PAGED_BPS));
 }
 
-template <int HD>
-__global__ void __launch_bounds__(ATT_THREADS) attn_paged_kernel(AttnArgs a) {
+template <int HD, int W, bool PF>
+__global__ void __launch_bounds__(W * 64) attn_paged_kernel(AttnArgs a) {
     const int kvh = blockIdx.y, seq = blockIdx.z;
     const int n = paged_keys(a, seq);
     const PagedKV<HD> src{a.k, a.v, a.page_table + (size_t)seq * a.max_pages, (n + mxd::PAGE_KEYS - 1) / mxd::PAGE_KEYS,
                           a.n_pages, (size_t)a.n_kv * mxd::PAGE_KEYS * HD, kvh};
     const size_t ws_rows = (size_t)seq * a.n_splits * a.n_heads;
-    attn_core<HD>(a, src, n, paged_splits(a, n), blockIdx.x, kvh, a.q + (size_t)seq * a.q_stride,
+    attn_core<HD, W, PF>(a, src, n, paged_splits(a, n), blockIdx.x, kvh, a.q + (size_t)seq * a.q_stride,
                   a.out + (size_t)seq * a.out_stride, a.ws_o + ws_rows * HD, a.ws_ml + ws_rows * 2);
 }
 
 // out[h] = sum_s 2^(M_s - M) O_s / sum_s 2^(M_s - M) L_s over the active
-// splits (log-sum-exp rule). One workgroup of MG * HD threads per query head:
-// thread (grp, dim) sums dim over splits grp, grp + MG, ...; its first PRE
-// partials are loaded before the (M_s, L_s) pass so the two latencies overlap,
-// which makes the common case (up to MG * PRE = 64 splits) one round trip.
-// The groups are combined in LDS in a fixed order (deterministic).
-constexpr int MG = 4;
-constexpr int PRE = 16;
+// splits (log-sum-exp rule). A workgroup of MG_T = 256 threads merges MG_D = 32
+// dims of one query head: thread (grp, d) sums its dim over splits grp,
+// grp + MG, ...; its first PRE partials are loaded before the (M_s, L_s) pass
+// so the two latencies overlap, which makes the common case (up to MG * PRE =
+// 64 splits) one round trip. The groups are combined in LDS in a fixed order
+// (deterministic).
+constexpr int MG_D = 32;
+constexpr int MG = 8;
+constexpr int MG_T = MG * MG_D;
+constexpr int PRE = 8;
 
 template <int HD>
-__device__ __forceinline__ void attn_merge_core(const AttnArgs& a, int n_active, int head, float* orow,
+__device__ __forceinline__ void attn_merge_core(const AttnArgs& a, int n_active, int head, int dchunk, float* orow,
                                                 const float* ws_o, const float* ws_ml) {
-    constexpr int NT = MG * HD;
     __shared__ float sw[MAX_SPLITS];
     __shared__ float sl[MAX_SPLITS];
-    __shared__ float red[2][NT / 64];
-    __shared__ float part[MG - 1][HD];
+    __shared__ float red[2][MG_T / 64];
+    __shared__ float part[MG - 1][MG_D];
     if (n_active <= 1) return;
     const int tid = threadIdx.x;
-    const int grp = tid / HD, dim = tid - grp * HD;
+    const int grp = tid / MG_D, dim = dchunk * MG_D + (tid - grp * MG_D);
     const float* po = ws_o + (size_t)head * HD + dim;
     const size_t stride = (size_t)a.n_heads * HD;
 
@@ -400,7 +400,7 @@ __device__ __forceinline__ void attn_merge_core(const AttnArgs& a, int n_active,
         pre[u] = sp < n_active ? po[(size_t)sp * stride] : 0.0f;
     }
     float mloc = -INFINITY;
-    for (int sp = tid; sp < n_active; sp += NT) {
+    for (int sp = tid; sp < n_active; sp += MG_T) {
         const float m = ws_ml[((size_t)sp * a.n_heads + head) * 2];
         sw[sp] = m;
         sl[sp] = ws_ml[((size_t)sp * a.n_heads + head) * 2 + 1];
@@ -411,9 +411,9 @@ __device__ __forceinline__ void attn_merge_core(const AttnArgs& a, int n_active,
     __syncthreads();
     float M = red[0][0];
 #pragma unroll
-    for (int w = 1; w < NT / 64; ++w) M = fmaxf(M, red[0][w]);
+    for (int w = 1; w < MG_T / 64; ++w) M = fmaxf(M, red[0][w]);
     float lloc = 0.0f;
-    for (int sp = tid; sp < n_active; sp += NT) {
+    for (int sp = tid; sp < n_active; sp += MG_T) {
         const float f = exp2f(sw[sp] - M);
         sw[sp] = f;
         lloc += f * sl[sp];
@@ -423,7 +423,7 @@ __device__ __forceinline__ void attn_merge_core(const AttnArgs& a, int n_active,
     __syncthreads();
     float L = 0.0f;
 #pragma unroll
-    for (int w = 0; w < NT / 64; ++w) L += red[1][w];
+    for (int w = 0; w < MG_T / 64; ++w) L += red[1][w];
 
     float acc = 0.0f;
 #pragma unroll
@@ -442,30 +442,68 @@ __device__ __forceinline__ void attn_merge_core(const AttnArgs& a, int n_active,
         for (int u = 0; u < 4; ++u) acc += sw[sp + MG * u] * v[u];
     }
     for (; sp < n_active; sp += MG) acc += sw[sp] * po[(size_t)sp * stride];
-    if (grp > 0) part[grp - 1][dim] = acc;
+    if (grp > 0) part[grp - 1][dim - dchunk * MG_D] = acc;
     __syncthreads();
     if (grp == 0) {
         float tot = acc;
 #pragma unroll
-        for (int g2 = 0; g2 < MG - 1; ++g2) tot += part[g2][dim];
+        for (int g2 = 0; g2 < MG - 1; ++g2) tot += part[g2][dim - dchunk * MG_D];
         orow[(size_t)head * HD + dim] = tot / L;
     }
 }
 
+// Grid (n_heads * HD / MG_D): workgroup x merges dims (x % (HD/MG_D)) * MG_D ..
+// of head x / (HD/MG_D).
 template <int HD>
-__global__ void __launch_bounds__(MG * HD) attn_merge_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(MG_T) attn_merge_kernel(AttnArgs a) {
     const int n_active = min(a.n_splits, (n_keys_of(a) + BLK - 1) / BLK);
-    attn_merge_core<HD>(a, n_active, blockIdx.x, a.out, a.ws_o, a.ws_ml);
+    constexpr int NCH = HD / MG_D;
+    attn_merge_core<HD>(a, n_active, blockIdx.x / NCH, blockIdx.x % NCH, a.out, a.ws_o, a.ws_ml);
 }
 
 template <int HD>
-__global__ void __launch_bounds__(MG * HD) attn_paged_merge_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(MG_T) attn_paged_merge_kernel(AttnArgs a) {
     const int seq = blockIdx.y;
     const int n = paged_keys(a, seq);
     const int n_active = min(paged_splits(a, n), (n + BLK - 1) / BLK);
     const size_t ws_rows = (size_t)seq * a.n_splits * a.n_heads;
-    attn_merge_core<HD>(a, n_active, blockIdx.x, a.out + (size_t)seq * a.out_stride, a.ws_o + ws_rows * HD,
+    constexpr int NCH = HD / MG_D;
+    attn_merge_core<HD>(a, n_active, blockIdx.x / NCH, blockIdx.x % NCH, a.out + (size_t)seq * a.out_stride,
+                        a.ws_o + ws_rows * HD,
                         a.ws_ml + ws_rows * 2);
+}
+
+// Waves per workgroup (ATT_W: 4 or 8) and whether each wave prefetches its
+// next block (ATT_PF = 1; off by default: measured on MI355X, one block in
+// flight per wave with nontemporal loads streams faster, 29.5 vs 31.0 us at
+// L = 32768 and 230 vs 265 us on the 64-sequence paged batch).
+int att_waves() { return mxd::tunable("ATT_W", ATT_WAVES) == 8 ? 8 : 4; }
+bool att_prefetch(int hd) { (void)hd; return mxd::tunable("ATT_PF", 2) == 1; }
+
+template <int HD>
+void launch_split(const dim3& grid, hipStream_t s, const AttnArgs& a) {
+    const int w = att_waves();
+    const bool pf = att_prefetch(HD);
+    if (w == 8) {
+        if (pf) hipLaunchKernelGGL((attn_split_kernel<HD, 8, true>), grid, dim3(512), 0, s, a);
+        else hipLaunchKernelGGL((attn_split_kernel<HD, 8, false>), grid, dim3(512), 0, s, a);
+    } else {
+        if (pf) hipLaunchKernelGGL((attn_split_kernel<HD, 4, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((attn_split_kernel<HD, 4, false>), grid, dim3(256), 0, s, a);
+    }
+}
+
+template <int HD>
+void launch_paged(const dim3& grid, hipStream_t s, const AttnArgs& a) {
+    const int w = att_waves();
+    const bool pf = att_prefetch(HD);
+    if (w == 8) {
+        if (pf) hipLaunchKernelGGL((attn_paged_kernel<HD, 8, true>), grid, dim3(512), 0, s, a);
+        else hipLaunchKernelGGL((attn_paged_kernel<HD, 8, false>), grid, dim3(512), 0, s, a);
+    } else {
+        if (pf) hipLaunchKernelGGL((attn_paged_kernel<HD, 4, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((attn_paged_kernel<HD, 4, false>), grid, dim3(256), 0, s, a);
+    }
 }
 
 // Splits per kv head: about ATT_WGCU (default 2) workgroups per CU over the
@@ -481,8 +519,9 @@ int target_splits(int n_kv) {
 // one block, capped by the occupancy target.
 int splits_for(int max_keys, int n_kv) {
     const int nblocks = (max_keys + BLK - 1) / BLK;
-    if (nblocks <= 4 * ATT_WAVES) return 1;
-    const int one_per_wave = (nblocks + ATT_WAVES - 1) / ATT_WAVES;
+    const int w = att_waves();
+    if (nblocks <= mxd::tunable("ATT_SINGLE", 4 * w)) return 1;
+    const int one_per_wave = (nblocks + w - 1) / w;
     return max(1, min(one_per_wave, target_splits(n_kv)));
 }
 
@@ -541,11 +580,11 @@ extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint1
     hipStream_t s = mxd::as_stream(stream);
     const dim3 grid(n_splits, n_kv_heads);
     if (head_dim == 128) {
-        hipLaunchKernelGGL(attn_split_kernel<128>, grid, dim3(ATT_THREADS), 0, s, a);
-        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(n_heads), dim3(MG * 128), 0, s, a);
+        launch_split<128>(grid, s, a);
+        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(n_heads * 128 / MG_D), dim3(MG_T), 0, s, a);
     } else {
-        hipLaunchKernelGGL(attn_split_kernel<256>, grid, dim3(ATT_THREADS), 0, s, a);
-        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(n_heads), dim3(MG * 256), 0, s, a);
+        launch_split<256>(grid, s, a);
+        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(n_heads * 256 / MG_D), dim3(MG_T), 0, s, a);
     }
     return mxd::check_launch("mxd_attention");
 }
@@ -620,13 +659,13 @@ extern "C" int mxd_attention_paged(const float* q, int q_stride, const uint16_t*
     hipStream_t s = mxd::as_stream(stream);
     const dim3 grid(s_max, n_kv_heads, n_seqs);
     if (head_dim == 128) {
-        hipLaunchKernelGGL(attn_paged_kernel<128>, grid, dim3(ATT_THREADS), 0, s, a);
+        launch_paged<128>(grid, s, a);
         if (s_max > 1)
-            hipLaunchKernelGGL(attn_paged_merge_kernel<128>, dim3(n_heads, n_seqs), dim3(MG * 128), 0, s, a);
+            hipLaunchKernelGGL(attn_paged_merge_kernel<128>, dim3(n_heads * 128 / MG_D, n_seqs), dim3(MG_T), 0, s, a);
     } else {
-        hipLaunchKernelGGL(attn_paged_kernel<256>, grid, dim3(ATT_THREADS), 0, s, a);
+        launch_paged<256>(grid, s, a);
         if (s_max > 1)
-            hipLaunchKernelGGL(attn_paged_merge_kernel<256>, dim3(n_heads, n_seqs), dim3(MG * 256), 0, s, a);
+            hipLaunchKernelGGL(attn_paged_merge_kernel<256>, dim3(n_heads * 256 / MG_D, n_seqs), dim3(MG_T), 0, s, a);
     }
     return mxd::check_launch("mxd_attention_paged");
 }
