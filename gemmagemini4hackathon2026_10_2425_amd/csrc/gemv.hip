@@ -658,10 +658,12 @@ template <int WF, typename XT, int NMAT, int OP>
 int launch(const GemvArgs& a, hipStream_t s) {
     constexpr int CH = 64 * WT<WF>::EPL;
     const int nch = (a.K + CH - 1) / CH;
-    // MV_ALGO: 0 = row-tiled workgroups (default), 1 = row streaming (while a
-    // row fits 16 waves x 4 chunks). Both sustain about the same HBM rate on
-    // the FFN shapes; the tiled kernel needs no persistent-grid sizing.
-    const int algo = mxd::tunable("MV_ALGO", 0);
+    // MV_ALGO: 0 = row-tiled workgroups, 1 = row streaming (while a row fits
+    // 16 waves x 4 chunks), 2 = grid sweep. Defaults from back-to-back sweeps
+    // on MI355X: row tiles for rows of up to 8 chunks, row streaming with 16
+    // waves for longer rows (4096 x 14336: 6.1 vs 5.8 TB/s fp16, 5.3 vs 4.9
+    // TB/s int8).
+    const int algo = mxd::tunable("MV_ALGO", nch > 8 && nch <= RS_MAX_CHUNKS ? 1 : 0);
     if (algo == 1) {
         MXD_REQUIRE(nch <= RS_MAX_CHUNKS, MXD_ERR_UNSUPPORTED, "matvec: row streaming needs K <= %d",
                     RS_MAX_CHUNKS * CH);
@@ -670,7 +672,7 @@ int launch(const GemvArgs& a, hipStream_t s) {
         cpw = cpw <= 1 ? 1 : cpw <= 2 ? 2 : 4;
         MXD_REQUIRE(nw * cpw >= nch, MXD_ERR_UNSUPPORTED,
                     "matvec: row streaming with %d waves covers at most %d chunks", nw, nw * 4);
-        const int wg_per_cu = mxd::tunable("MV_RS_WGCU", 32 / nw > 0 ? 32 / nw : 1);
+        const int wg_per_cu = mxd::tunable("MV_RS_WGCU", nw >= 16 ? 2 : 32 / nw);
         return launch_rows<WF, XT, NMAT, OP>(a, nw, cpw, wg_per_cu, s);
     }
     if (algo == 2) {
