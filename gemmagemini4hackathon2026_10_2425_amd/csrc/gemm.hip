@@ -119,19 +119,28 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
     }
 
     // Activation slice: 64 rows x nst * 128 halfs, 16-byte pieces, rows past
-    // n_rows zero. At most 64 * 8 * 16 = 8192 pieces, 16 per thread.
+    // n_rows zero. At most 64 * 8 * 16 = 8192 pieces, 16 per thread: all 16
+    // loads are issued before any store (from clamped, always valid
+    // addresses), so their latencies overlap.
     {
+        constexpr int NPT = GM_BATCH * GM_SMAX * (GM_KC / 8) / GM_THREADS;
         const int per_row = nst * (GM_KC / 8);
         const int total = GM_BATCH * per_row;
+        u4_t v[NPT];
 #pragma unroll
-        for (int u = 0; u < GM_BATCH * GM_SMAX * (GM_KC / 8) / GM_THREADS; ++u) {
+        for (int u = 0; u < NPT; ++u) {
             const int idx = threadIdx.x + GM_THREADS * u;
+            const int r = idx / per_row, piece = idx - r * per_row;
+            const int rr = min(b0 + r, a.n_rows - 1);
+            v[u] = *reinterpret_cast<const u4_t*>(a.X + (size_t)rr * K + (size_t)ks0 * GM_KC + piece * 8);
+        }
+#pragma unroll
+        for (int u = 0; u < NPT; ++u) {
+            const int idx = threadIdx.x + GM_THREADS * u;
+            const int r = idx / per_row, piece = idx - r * per_row;
             if (idx < total) {
-                const int r = idx / per_row, piece = idx - r * per_row;
-                u4_t v = {0u, 0u, 0u, 0u};
-                if (b0 + r < a.n_rows)
-                    v = *reinterpret_cast<const u4_t*>(a.X + (size_t)(b0 + r) * K + (size_t)ks0 * GM_KC + piece * 8);
-                *reinterpret_cast<u4_t*>(&xs[r * GM_XP + piece * 8]) = v;
+                const u4_t z = {0u, 0u, 0u, 0u};
+                *reinterpret_cast<u4_t*>(&xs[r * GM_XP + piece * 8]) = b0 + r < a.n_rows ? v[u] : z;
             }
         }
     }
@@ -154,23 +163,40 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
                     *reinterpret_cast<u4_t*>(wst + (8 * u + (lane >> 3)) * GM_WP + 16 * (lane & 7)) = w[p][u];
                 if (t + GM_PD < nst) load_w(w[p], t + GM_PD);
                 __builtin_amdgcn_wave_barrier();
+                // All operands of the step first, then the 16 independent
+                // MFMAs back to back, then the per-block scaling, so no MFMA
+                // result is waited for while the matrix core could be busy.
+                h8_t wop[4];
+                float sc[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const u2_t q = *reinterpret_cast<const u2_t*>(wst + col * GM_WP + 32 * j + 8 * g);
                     h2_t h[4];
                     mxd::i8x4_to_h2x2(q.x, h[0], h[1]);
                     mxd::i8x4_to_h2x2(q.y, h[2], h[3]);
-                    const h8_t wop = {h[0].x, h[0].y, h[1].x, h[1].y, h[2].x, h[2].y, h[3].x, h[3].y};
-                    const float sc = mxd::h2f(sst[col * GM_SMAX * 4 + 4 * t + j]);
-#pragma unroll
-                    for (int bg = 0; bg < 4; ++bg) {
-                        const h8_t xop = *reinterpret_cast<const h8_t*>(
-                            &xs[(bg * 16 + col) * GM_XP + t * GM_KC + 32 * j + 8 * g]);
-                        const f4_t c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xop, wop, zero, 0, 0, 0);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[bg][i] = fmaf(sc, c[i], acc[bg][i]);
-                    }
+                    wop[j] = h8_t{h[0].x, h[0].y, h[1].x, h[1].y, h[2].x, h[2].y, h[3].x, h[3].y};
+                    sc[j] = mxd::h2f(sst[col * GM_SMAX * 4 + 4 * t + j]);
                 }
+                h8_t xop[4][4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int bg = 0; bg < 4; ++bg)
+                        xop[j][bg] = *reinterpret_cast<const h8_t*>(
+                            &xs[(bg * 16 + col) * GM_XP + t * GM_KC + 32 * j + 8 * g]);
+                f4_t c[4][4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int bg = 0; bg < 4; ++bg)
+                        c[j][bg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xop[j][bg], wop[j], zero, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int bg = 0; bg < 4; ++bg)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[bg][i] = fmaf(sc[j], c[j][bg][i], acc[bg][i]);
                 __builtin_amdgcn_wave_barrier();
             }
         }
