@@ -83,8 +83,11 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
     unsigned char* wst = smem + GM_LDS_X + (size_t)wave * 16 * GM_WP;                          // [16][GM_WP]
     uint16_t* sst = reinterpret_cast<uint16_t*>(smem + GM_LDS_X + GM_LDS_W) + wave * 16 * GM_SMAX * 4;  // [16][32]
     const int m = wave / WAVES_PER_MAT;  // which matrix this wave reads
-    const int row0 = blockIdx.x * ROWS_PER_MAT + 16 * (wave % WAVES_PER_MAT);
-    const int split = blockIdx.y, b0 = blockIdx.z * GM_BATCH;
+    // Grid (splits, row tiles, batch tiles): consecutive workgroups take the
+    // consecutive K splits of one row tile, so the workgroups running at once
+    // read whole contiguous stretches of the weight rows (HBM-page friendly).
+    const int row0 = blockIdx.y * ROWS_PER_MAT + 16 * (wave % WAVES_PER_MAT);
+    const int split = blockIdx.x, b0 = blockIdx.z * GM_BATCH;
     const int M = a.M, K = a.K;
     const int ks0 = split * a.ksteps / a.splits, ks1 = (split + 1) * a.ksteps / a.splits;  // <= GM_SMAX steps
     const int nst = ks1 - ks0;
@@ -118,29 +121,29 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
         }
     }
 
-    // Activation slice: 64 rows x nst * 128 halfs, 16-byte pieces, rows past
-    // n_rows zero. At most 64 * 8 * 16 = 8192 pieces, 16 per thread: all 16
-    // loads are issued before any store (from clamped, always valid
-    // addresses), so their latencies overlap.
+    // Activation slice: 64 rows x nst * 128 halfs in 16-byte pieces, rows past
+    // n_rows zero. Thread t takes row t / 8 and pieces t % 8 + 8u (no integer
+    // division); all its loads are issued before any store (from clamped,
+    // always valid addresses), so their latencies overlap.
     {
-        constexpr int NPT = GM_BATCH * GM_SMAX * (GM_KC / 8) / GM_THREADS;
+        constexpr int TPR = GM_THREADS / GM_BATCH;           // threads per row (8)
+        constexpr int NPT = GM_SMAX * (GM_KC / 8) / TPR;     // pieces per thread (16)
         const int per_row = nst * (GM_KC / 8);
-        const int total = GM_BATCH * per_row;
+        const int r = threadIdx.x / TPR, sub = threadIdx.x % TPR;
+        const uint16_t* xrow = a.X + (size_t)min(b0 + r, a.n_rows - 1) * K + (size_t)ks0 * GM_KC;
         u4_t v[NPT];
 #pragma unroll
         for (int u = 0; u < NPT; ++u) {
-            const int idx = threadIdx.x + GM_THREADS * u;
-            const int r = idx / per_row, piece = idx - r * per_row;
-            const int rr = min(b0 + r, a.n_rows - 1);
-            v[u] = *reinterpret_cast<const u4_t*>(a.X + (size_t)rr * K + (size_t)ks0 * GM_KC + piece * 8);
+            const int piece = min(sub + TPR * u, per_row - 1);
+            v[u] = *reinterpret_cast<const u4_t*>(xrow + piece * 8);
         }
+        const bool live = b0 + r < a.n_rows;
 #pragma unroll
         for (int u = 0; u < NPT; ++u) {
-            const int idx = threadIdx.x + GM_THREADS * u;
-            const int r = idx / per_row, piece = idx - r * per_row;
-            if (idx < total) {
+            const int piece = sub + TPR * u;
+            if (piece < per_row) {
                 const u4_t z = {0u, 0u, 0u, 0u};
-                *reinterpret_cast<u4_t*>(&xs[r * GM_XP + piece * 8]) = b0 + r < a.n_rows ? v[u] : z;
+                *reinterpret_cast<u4_t*>(&xs[r * GM_XP + piece * 8]) = live ? v[u] : z;
             }
         }
     }
@@ -299,7 +302,7 @@ int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char
     MXD_REQUIRE(need == 0 || (ws && ws_bytes >= need), MXD_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)",
                 fn, need, ws_bytes);
     a.part = static_cast<float*>(ws);
-    const dim3 grid((a.M + GM_ROWS / NMAT - 1) / (GM_ROWS / NMAT), a.splits, (a.n_rows + GM_BATCH - 1) / GM_BATCH);
+    const dim3 grid(a.splits, (a.M + GM_ROWS / NMAT - 1) / (GM_ROWS / NMAT), (a.n_rows + GM_BATCH - 1) / GM_BATCH);
     const size_t lds = GM_LDS;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_q8_kernel<NMAT, OP>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
