@@ -103,7 +103,9 @@ template <int HD>
 struct ContigKV {
     const uint16_t* kbase;
     const uint16_t* vbase;
-    __device__ __forceinline__ void load(KVBlock<HD>& kv, int b, int lane) const {
+    using Addr = int;  // the block index
+    __device__ __forceinline__ Addr addr(int b) const { return b; }
+    __device__ __forceinline__ void load(KVBlock<HD>& kv, Addr b, int lane) const {
         load_block<HD>(kv, kbase, vbase, b * BLK, lane);
     }
     // Key (within the block) of score slot j of lane group g; the same slot
@@ -130,10 +132,16 @@ struct PagedKV {
         p = p < 0 ? 0 : (p >= n_pages ? n_pages - 1 : p);  // a bad entry still addresses inside the pool
         return (size_t)p * page_stride + (size_t)kvh * mxd::PAGE_KEYS * HD;
     }
-    __device__ __forceinline__ void load(KVBlock<HD>& kv, int b, int lane) const {
-        // A ragged last block has one page: its second half re-reads the first
-        // page, and every key of it is masked.
-        const size_t s0 = slab(2 * b), s1 = slab(min(2 * b + 1, npages - 1));
+    // The block's two slabs, looked up in the page table. The core asks for
+    // the next block's address one iteration early, so the table read is off
+    // the path of the K/V loads. A ragged last block has one page: its second
+    // half re-reads the first page, and every key of it is masked.
+    struct Addr {
+        size_t s0, s1;
+    };
+    __device__ __forceinline__ Addr addr(int b) const { return Addr{slab(2 * b), slab(min(2 * b + 1, npages - 1))}; }
+    __device__ __forceinline__ void load(KVBlock<HD>& kv, const Addr& ad, int lane) const {
+        const size_t s0 = ad.s0, s1 = ad.s1;
         const int col = lane & 15, g = lane >> 4;
         const uint16_t* kp = kpool + ((col >> 3) ? s1 : s0) + (size_t)(g * 8 + (col & 7)) * 8;
         const uint16_t* vp = vpool + ((g >> 1) ? s1 : s0) + (size_t)((g & 1) * 16 + col) * 8;
@@ -180,7 +188,7 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
     const int step = S * W;
     int b = split + S * wave;
     KVBlock<HD> cur, nxt;
-    if (b < nblocks) src.load(cur, b, lane);
+    if (b < nblocks) src.load(cur, src.addr(b), lane);
 
     // Q^T operand: column h holds fp16(q) of head kvh*G + h and column h + 8
     // the remainder fp16(q - hi) (h < G <= 8); the rest are zero. k-slot (g, j)
@@ -216,8 +224,12 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
 
     for (; b < nblocks; b += step) {
         const int key0 = b * BLK;
+        // The next block's address (a page-table read for the paged cache) is
+        // fetched before this block's math so its latency is hidden.
+        typename KV::Addr next_addr{};
+        if (b + step < nblocks) next_addr = src.addr(b + step);
         if constexpr (PREFETCH) {
-            if (b + step < nblocks) src.load(nxt, b + step, lane);
+            if (b + step < nblocks) src.load(nxt, next_addr, lane);
         }
 
         // ---- scores (log2 domain): lane group g, slot j = 4t + i (tile t,
@@ -289,7 +301,7 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
         if constexpr (PREFETCH) {
             cur = nxt;
         } else if (b + step < nblocks) {
-            src.load(cur, b + step, lane);
+            src.load(cur, next_addr, lane);
         }
     }
 
