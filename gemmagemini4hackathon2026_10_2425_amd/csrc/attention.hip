@@ -36,7 +36,11 @@
 //  * the paged variant (a ragged batch of sequences over a pool of 16-key
 //    pages) runs the same core: a 32-key block is two pages, each page holds
 //    one half of a contiguous tile, and each lane addresses its own page, so
-//    every operand is two 512-byte runs;
+//    every operand is two 512-byte runs. Its default schedule deals the
+//    batch's (sequence, kv head, block) items evenly over the workgroups that
+//    fit the GPU at once, whatever the spread of lengths (measured on MI355X,
+//    64 sequences of 128..8192 keys: 180 us against 251 us for a fixed number
+//    of 16-block splits per sequence, which leaves the long ones for last);
 //  * K and V are read with nontemporal loads: they stream through once.
 #include "common.hpp"
 
@@ -45,8 +49,12 @@ namespace {
 constexpr int ATT_WAVES = 4;  // default waves per workgroup
 constexpr int BLK = 32;  // keys per wave step
 constexpr int MAX_SPLITS = 512;
-constexpr int PAGED_BPS = 16;  // 32-key blocks per split of a paged sequence (4 per wave)
+constexpr int PAGED_BPS = 16;  // default 32-key blocks per split of a paged sequence (4 per wave)
 constexpr float LOG2E = 1.4426950408889634f;
+// Balanced paged schedule: at most SK_MAX_SEQS sequences (their block prefix
+// lives in LDS), and at least SK_MIN_BLOCKS blocks per workgroup.
+constexpr int SK_MAX_SEQS = 2048;
+constexpr int SK_MIN_BLOCKS = 8;
 
 struct AttnArgs {
     const float* q;
@@ -59,7 +67,11 @@ struct AttnArgs {
     // paged: page_table [seqs][max_pages] of pool pages, seq_lens [seqs] keys
     const int32_t* page_table = nullptr;
     const int32_t* seq_lens = nullptr;
-    int max_pages = 0, n_pages = 0, q_stride = 0, out_stride = 0;
+    int max_pages = 0, n_pages = 0, q_stride = 0, out_stride = 0, bps = PAGED_BPS;
+    // paged, balanced schedule: sequences, workgroups launched, and the
+    // per-sequence block prefix the attention kernel leaves for the merge
+    int n_seqs = 0, sk_wgs = 0;
+    int32_t* sk_pre = nullptr;
     int n_heads, n_kv, G, max_ctx, n_keys, n_splits;
     float qscale;  // scale * log2(e): scores live in the log2 domain
 };
@@ -157,11 +169,23 @@ struct PagedKV {
     static __device__ __forceinline__ int key(int g, int j) { return 8 * g + j; }
 };
 
-// One split of one kv head of one sequence: keys [0, n), S splits, q and out
-// rows of this sequence, partials of this sequence.
+// Where one run of the core leaves its result: the normalised output rows of
+// the kv head's G query heads ([G][HD]), or an unnormalised partial, O rows
+// [G][HD] plus (max, sum) pairs [G][2], for a later log-sum-exp merge.
+struct CoreOut {
+    float* orow;
+    float* po;
+    float* pml;
+    bool direct;
+};
+
+// One kv head of one sequence with n keys, over the 32-key blocks first,
+// first + S, first + 2S, ... below bend, dealt round-robin to the W waves
+// (wave w takes first + S*w, then steps by S*W). qg points at the q rows of
+// the kv head's G query heads. The range must hold at least one block.
 template <int HD, int W, bool PREFETCH, typename KV>
-__device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int n, int S, int split, int kvh,
-                                          const float* qrow, float* orow, float* ws_o, float* ws_ml) {
+__device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int n, int first, int S, int bend,
+                                          const float* qg, const CoreOut& out) {
     constexpr int NC = HD / 32;  // MFMA k-chunks over head_dim for Q.K
     constexpr int ND = HD / 16;  // 16-wide dim tiles for P.V
     constexpr int NT = W * 64;
@@ -169,24 +193,17 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
     __shared__ float sm_m[W][8];
     __shared__ float sm_l[W][8];
 
-    const int nblocks = (n + BLK - 1) / BLK;
     const int G = a.G;
-    if (nblocks == 0) {  // no keys (an empty sequence): the output is zero
-        if (split == 0)
-            for (int idx = threadIdx.x; idx < G * HD; idx += NT) orow[(size_t)kvh * G * HD + idx] = 0.0f;
-        return;
-    }
-    if (split >= min(S, nblocks)) return;  // an empty split
-
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, g = lane >> 4;
 
-    // Blocks are dealt round-robin: split s owns global blocks s, s+S, s+2S, ...
-    // and wave w takes every 4th of those, so at any moment the splits of a kv
-    // head stream one contiguous run of the cache. The first block's loads go
-    // out before the q operand is built so the two latencies overlap.
+    // With S splits of a kv head, split s owning blocks s, s+S, ..., the
+    // splits stream one contiguous run of the cache at any moment. The first
+    // block's loads go out before the q operand is built so the two latencies
+    // overlap.
+    const int nblocks = bend;
     const int step = S * W;
-    int b = split + S * wave;
+    int b = first + S * wave;
     KVBlock<HD> cur, nxt;
     if (b < nblocks) src.load(cur, src.addr(b), lane);
 
@@ -197,7 +214,7 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
     {
         const int h = col & 7;
         const bool live = h < G;
-        const float* qh = qrow + (size_t)(kvh * G + (live ? h : 0)) * HD;
+        const float* qh = qg + (size_t)(live ? h : 0) * HD;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
             const f4_t q0 = *reinterpret_cast<const f4_t*>(qh + 32 * c + 8 * g);
@@ -325,8 +342,7 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
     }
     __syncthreads();
 
-    // ---- merge the 4 waves (and write the split's partial or the output)
-    const int n_active = min(S, nblocks);
+    // ---- merge the waves (and write the partial or the output)
     for (int idx = threadIdx.x; idx < G * HD; idx += NT) {
         const int h = idx / HD, dim = idx - h * HD;
         float M = sm_m[0][h];
@@ -339,24 +355,44 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
             so += f * sm_o[w][h][dim];
             sl += f * sm_l[w][h];
         }
-        const int head = kvh * G + h;
-        if (n_active == 1) {
-            orow[(size_t)head * HD + dim] = so / sl;
+        if (out.direct) {
+            out.orow[idx] = so / sl;
         } else {
-            ws_o[((size_t)split * a.n_heads + head) * HD + dim] = so;
+            out.po[idx] = so;
             if (dim == 0) {
-                ws_ml[((size_t)split * a.n_heads + head) * 2 + 0] = M;
-                ws_ml[((size_t)split * a.n_heads + head) * 2 + 1] = sl;
+                out.pml[2 * h + 0] = M;
+                out.pml[2 * h + 1] = sl;
             }
         }
     }
+    __syncthreads();  // the LDS rows are free for the next run
+}
+
+// Split `split` of S over the kv head's n keys: partials at split-major rows
+// [split][n_heads] of ws_o / ws_ml, or the output directly when one split is
+// active. An empty sequence writes a zero output.
+template <int HD, int W, bool PF, typename KV>
+__device__ __forceinline__ void attn_split(const AttnArgs& a, const KV& src, int n, int S, int split, int kvh,
+                                           const float* qrow, float* orow, float* ws_o, float* ws_ml) {
+    const int nblocks = (n + BLK - 1) / BLK;
+    const size_t g0 = (size_t)kvh * a.G;
+    if (nblocks == 0) {
+        if (split == 0)
+            for (int idx = threadIdx.x; idx < a.G * HD; idx += W * 64) orow[g0 * HD + idx] = 0.0f;
+        return;
+    }
+    const int n_active = min(S, nblocks);
+    if (split >= n_active) return;  // an empty split
+    const size_t prow = (size_t)split * a.n_heads + g0;
+    const CoreOut out{orow + g0 * HD, ws_o + prow * HD, ws_ml + prow * 2, n_active == 1};
+    attn_core<HD, W, PF>(a, src, n, split, S, nblocks, qrow + g0 * HD, out);
 }
 
 template <int HD, int W, bool PF>
 __global__ void __launch_bounds__(W * 64) attn_split_kernel(AttnArgs a) {
     const int kvh = blockIdx.y;
     const ContigKV<HD> src{a.k + (size_t)kvh * a.max_ctx * HD, a.v + (size_t)kvh * a.max_ctx * HD};
-    attn_core<HD, W, PF>(a, src, n_keys_of(a), a.n_splits, blockIdx.x, kvh, a.q, a.out, a.ws_o, a.ws_ml);
+    attn_split<HD, W, PF>(a, src, n_keys_of(a), a.n_splits, blockIdx.x, kvh, a.q, a.out, a.ws_o, a.ws_ml);
 }
 
 // Keys and splits of paged sequence seq (clamped so a bad length can never
@@ -366,7 +402,7 @@ __device__ __forceinline__ int paged_keys(const AttnArgs& a, int seq) {
 }
 __device__ __forceinline__ int paged_splits(const AttnArgs& a, int n) {
     const int nblocks = (n + BLK - 1) / BLK;
-    return min(a.n_splits, max(1, (nblocks + PAGED_BPS - 1) / PAGED_BPS));
+    return min(a.n_splits, max(1, (nblocks + a.bps - 1) / a.bps));
 }
 
 template <int HD, int W, bool PF>
@@ -376,8 +412,158 @@ __global__ void __launch_bounds__(W * 64) attn_paged_kernel(AttnArgs a) {
     const PagedKV<HD> src{a.k, a.v, a.page_table + (size_t)seq * a.max_pages, (n + mxd::PAGE_KEYS - 1) / mxd::PAGE_KEYS,
                           a.n_pages, (size_t)a.n_kv * mxd::PAGE_KEYS * HD, kvh};
     const size_t ws_rows = (size_t)seq * a.n_splits * a.n_heads;
-    attn_core<HD, W, PF>(a, src, n, paged_splits(a, n), blockIdx.x, kvh, a.q + (size_t)seq * a.q_stride,
-                  a.out + (size_t)seq * a.out_stride, a.ws_o + ws_rows * HD, a.ws_ml + ws_rows * 2);
+    attn_split<HD, W, PF>(a, src, n, paged_splits(a, n), blockIdx.x, kvh, a.q + (size_t)seq * a.q_stride,
+                          a.out + (size_t)seq * a.out_stride, a.ws_o + ws_rows * HD, a.ws_ml + ws_rows * 2);
+}
+
+// ---------------------------------------------------------------------------
+// Paged attention with a balanced schedule. The work is the list of every
+// (sequence, kv head, 32-key block), ordered by sequence, then kv head, then
+// block: sequence s contributes n_kv segments of nb(s) blocks. Workgroup w of
+// NW takes items [w*T/NW, (w+1)*T/NW) of the T items, so every workgroup
+// streams the same number of blocks whatever the spread of lengths. The range
+// of a workgroup cuts the segments into pieces; a segment inside one range is
+// written out directly, any other leaves one partial per piece, at slot w + sg
+// (sg = the segment's index; along the monotone path of (workgroup, segment)
+// pieces that sum strictly increases, so slots never collide, and there are
+// at most NW + n_seqs * n_kv of them).
+// ---------------------------------------------------------------------------
+
+// Exclusive prefix of per-sequence blocks into pre[0..n_seqs]; returns the
+// total. Every thread of the workgroup calls it.
+template <int NT>
+__device__ __forceinline__ int sk_block_prefix(const AttnArgs& a, int* pre) {
+    __shared__ int wsum[NT / 64];
+    const int ns = a.n_seqs;
+    const int per = (ns + NT - 1) / NT;
+    const int s0 = min(ns, (int)threadIdx.x * per), s1 = min(ns, s0 + per);
+    int local = 0;
+    for (int s = s0; s < s1; ++s) {
+        const int nb = (paged_keys(a, s) + BLK - 1) / BLK;
+        pre[s + 1] = nb;  // lengths first, turned into a prefix below
+        local += nb;
+    }
+    // inclusive scan of the per-thread sums across the wave, then the waves
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int inc = local;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(inc, d);
+        if (lane >= d) inc += v;
+    }
+    if (lane == 63) wsum[wave] = inc;
+    __syncthreads();
+    int base = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) {
+        base += w < wave ? wsum[w] : 0;
+        total += wsum[w];
+    }
+    // each thread rewrites only its own entries pre[s0+1 .. s1] (length ->
+    // inclusive prefix), so no entry is read after another thread wrote it
+    int run = base + inc - local;
+    for (int s = s0; s < s1; ++s) {
+        run += pre[s + 1];
+        pre[s + 1] = run;
+    }
+    if (threadIdx.x == 0) pre[0] = 0;
+    __syncthreads();
+    return total;
+}
+
+// Workgroups that get work: enough that each streams at least SK_MIN_BLOCKS.
+__device__ __forceinline__ int sk_active(long long T, int nw) {
+    return (int)max(1LL, min((long long)nw, (T + SK_MIN_BLOCKS - 1) / SK_MIN_BLOCKS));
+}
+
+// The workgroup whose range holds item x (ranges are never empty: T >= nw).
+__device__ __forceinline__ int sk_owner(long long x, long long T, int nw) {
+    return (int)(((x + 1) * nw - 1) / T);
+}
+
+template <int HD, int W, bool PF>
+__global__ void __launch_bounds__(W * 64) attn_paged_sk_kernel(AttnArgs a) {
+    __shared__ int pre[SK_MAX_SEQS + 1];
+    const int total = sk_block_prefix<W * 64>(a, pre);
+    const int ns = a.n_seqs, nkv = a.n_kv;
+    if (blockIdx.x == 0)
+        for (int s = threadIdx.x; s <= ns; s += W * 64) a.sk_pre[s] = pre[s];
+    const long long T = (long long)nkv * total;
+    if (T == 0) return;
+    const int nw = sk_active(T, a.sk_wgs);
+    const int w = blockIdx.x;
+    if (w >= nw) return;
+    long long pos = (long long)w * T / nw;
+    const long long end = (long long)(w + 1) * T / nw;
+
+    // the sequence holding pos: the last s with nkv * pre[s] <= pos
+    int lo = 0, hi = ns - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if ((long long)nkv * pre[mid] <= pos) lo = mid;
+        else hi = mid - 1;
+    }
+    int seq = lo;
+    const size_t page_stride = (size_t)nkv * mxd::PAGE_KEYS * HD;
+    while (pos < end) {
+        while ((long long)nkv * pre[seq + 1] <= pos) ++seq;  // skip finished and empty sequences
+        const int nb = pre[seq + 1] - pre[seq];
+        const long long base = (long long)nkv * pre[seq];
+        const int kvh = (int)((pos - base) / nb);
+        const long long seg0 = base + (long long)kvh * nb;
+        const int b0 = (int)(pos - seg0);
+        const int b1 = (int)min((long long)nb, end - seg0);
+        const int n = paged_keys(a, seq);
+        const PagedKV<HD> src{a.k, a.v, a.page_table + (size_t)seq * a.max_pages,
+                              (n + mxd::PAGE_KEYS - 1) / mxd::PAGE_KEYS, a.n_pages, page_stride, kvh};
+        const size_t g0 = (size_t)kvh * a.G;
+        const size_t slot = (size_t)w + (size_t)seq * nkv + kvh;
+        const CoreOut out{a.out + (size_t)seq * a.out_stride + g0 * HD, a.ws_o + slot * a.G * HD,
+                          a.ws_ml + slot * a.G * 2, b0 == 0 && b1 == nb};
+        attn_core<HD, W, PF>(a, src, n, b0, 1, b1, a.q + (size_t)seq * a.q_stride + g0 * HD, out);
+        pos = seg0 + b1;
+    }
+}
+
+// Merge of the balanced schedule: one thread per (sequence, head, dim). A
+// segment inside one workgroup's range was written directly; an empty one
+// gets zeros; any other sums its pieces (slots w + sg for its workgroups
+// w0..w1) with the log-sum-exp rule.
+constexpr int SKM_T = 128;
+
+template <int HD>
+__global__ void __launch_bounds__(SKM_T) attn_paged_sk_merge_kernel(AttnArgs a) {
+    const int seq = blockIdx.y;
+    const int idx = blockIdx.x * SKM_T + threadIdx.x;  // head * HD + dim
+    if (idx >= a.n_heads * HD) return;
+    const int head = idx / HD, dim = idx - head * HD;
+    const int kvh = head / a.G, h = head - kvh * a.G;
+    const int p0 = a.sk_pre[seq], p1 = a.sk_pre[seq + 1], tot = a.sk_pre[a.n_seqs];
+    float* o = a.out + (size_t)seq * a.out_stride + idx;
+    const int nb = p1 - p0;
+    if (nb == 0) {
+        *o = 0.0f;
+        return;
+    }
+    const long long T = (long long)a.n_kv * tot;
+    const int nw = sk_active(T, a.sk_wgs);
+    const long long s0 = (long long)a.n_kv * p0 + (long long)kvh * nb;
+    const int w0 = sk_owner(s0, T, nw), w1 = sk_owner(s0 + nb - 1, T, nw);
+    if (w0 == w1) return;
+    const size_t slot0 = (size_t)w0 + (size_t)seq * a.n_kv + kvh;
+    const float* pml = a.ws_ml + (slot0 * a.G + h) * 2;
+    const float* po = a.ws_o + (slot0 * a.G + h) * HD + dim;
+    const size_t sml = (size_t)a.G * 2, so = (size_t)a.G * HD;
+    const int np = w1 - w0 + 1;
+    float M = -INFINITY;
+    for (int i = 0; i < np; ++i) M = fmaxf(M, pml[i * sml]);
+    float num = 0.0f, den = 0.0f;
+    for (int i = 0; i < np; ++i) {
+        const float f = exp2f(pml[i * sml] - M);
+        num += f * po[i * so];
+        den += f * pml[i * sml + 1];
+    }
+    *o = num / den;
 }
 
 // out[h] = sum_s 2^(M_s - M) O_s / sum_s 2^(M_s - M) L_s over the active
@@ -518,6 +704,19 @@ void launch_paged(const dim3& grid, hipStream_t s, const AttnArgs& a) {
     }
 }
 
+template <int HD>
+void launch_paged_sk(int nw, hipStream_t s, const AttnArgs& a) {
+    const int w = att_waves();
+    const bool pf = att_prefetch(HD);
+    if (w == 8) {
+        if (pf) hipLaunchKernelGGL((attn_paged_sk_kernel<HD, 8, true>), dim3(nw), dim3(512), 0, s, a);
+        else hipLaunchKernelGGL((attn_paged_sk_kernel<HD, 8, false>), dim3(nw), dim3(512), 0, s, a);
+    } else {
+        if (pf) hipLaunchKernelGGL((attn_paged_sk_kernel<HD, 4, true>), dim3(nw), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((attn_paged_sk_kernel<HD, 4, false>), dim3(nw), dim3(256), 0, s, a);
+    }
+}
+
 // Splits per kv head: about ATT_WGCU (default 2) workgroups per CU over the
 // whole grid, and never more splits than 32-key blocks.
 int target_splits(int n_kv) {
@@ -602,15 +801,67 @@ extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint1
 }
 
 namespace {
+// 32-key blocks per split of a paged sequence (ATT_BPS, 4..256).
+int paged_bps() { return max(4, min(256, mxd::tunable("ATT_BPS", PAGED_BPS))); }
 int paged_split_max(int max_keys) {
     const int nblocks = (max_keys + BLK - 1) / BLK;
-    return min(MAX_SPLITS, max(1, (nblocks + PAGED_BPS - 1) / PAGED_BPS));
+    const int bps = paged_bps();
+    return min(MAX_SPLITS, max(1, (nblocks + bps - 1) / bps));
+}
+
+// The balanced schedule serves batches of up to SK_MAX_SEQS sequences whose
+// item count fits an int (ATT_SCHED = 2 selects per-sequence splits instead).
+bool use_balanced(int n_seqs, int max_keys, int n_kv) {
+    const long long items = (long long)n_seqs * ((max_keys + BLK - 1) / BLK) * n_kv;
+    return mxd::tunable("ATT_SCHED", 1) != 2 && n_seqs <= SK_MAX_SEQS && items < (1LL << 31);
+}
+
+template <typename K>
+int resident_wgs(K kernel, int threads) {
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess) per_cu = 1;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+    return max(1, per_cu) * max(1, cus);
+}
+
+// Workgroups of the balanced schedule: ATT_SKWG per CU, by default as many as
+// stay resident at once (one round, every workgroup with the same work).
+template <int HD>
+int sk_wgs_hd() {
+    const int w = att_waves();
+    const bool pf = att_prefetch(HD);
+    int n;
+    if (w == 8) n = pf ? resident_wgs(attn_paged_sk_kernel<HD, 8, true>, 512) : resident_wgs(attn_paged_sk_kernel<HD, 8, false>, 512);
+    else n = pf ? resident_wgs(attn_paged_sk_kernel<HD, 4, true>, 256) : resident_wgs(attn_paged_sk_kernel<HD, 4, false>, 256);
+    const int per_cu = mxd::tunable("ATT_SKWG", 0);
+    if (per_cu > 0) {
+        int dev = 0, cus = 256;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            cus = 256;
+        n = min(64, per_cu) * cus;
+    }
+    return n;
+}
+int sk_wgs(int hd) { return hd == 128 ? sk_wgs_hd<128>() : sk_wgs_hd<256>(); }
+
+// Workspace of the balanced schedule: partial slots (O rows, then (max, sum)
+// pairs) and the n_seqs + 1 block prefix.
+size_t sk_slots(int nw, int n_seqs, int n_kv) { return (size_t)nw + (size_t)n_seqs * n_kv; }
+size_t sk_workspace(int nw, int n_seqs, int n_heads, int n_kv, int hd) {
+    const int G = n_heads / n_kv;
+    return sk_slots(nw, n_seqs, n_kv) * G * (hd + 2) * sizeof(float) + ((size_t)n_seqs + 1) * sizeof(int32_t);
 }
 }  // namespace
 
 extern "C" size_t mxd_attention_paged_workspace_size(int n_heads, int n_kv_heads, int head_dim, int n_seqs,
                                                      int max_keys) {
     if (n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || n_seqs <= 0 || max_keys <= 0) return 0;
+    if (n_heads % n_kv_heads == 0 && (head_dim == 128 || head_dim == 256) &&
+        use_balanced(n_seqs, max_keys, n_kv_heads))
+        return sk_workspace(sk_wgs(head_dim), n_seqs, n_heads, n_kv_heads, head_dim);
     return (size_t)n_seqs * paged_split_max(max_keys) * n_heads * (head_dim + 2) * sizeof(float);
 }
 
@@ -639,9 +890,12 @@ extern "C" int mxd_attention_paged(const float* q, int q_stride, const uint16_t*
     const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kpool) |
                          reinterpret_cast<uintptr_t>(vpool);
     MXD_REQUIRE((al & 15) == 0, MXD_ERR_UNSUPPORTED, "mxd_attention_paged: q, kpool, vpool must be 16-byte aligned");
+    const bool balanced = use_balanced(n_seqs, max_keys, n_kv_heads);
     const int s_max = paged_split_max(max_keys);
-    const size_t need = (size_t)n_seqs * s_max * n_heads * (head_dim + 2) * sizeof(float);
-    MXD_REQUIRE(s_max == 1 || (workspace && ws_bytes >= need), MXD_ERR_WORKSPACE,
+    const int nw = balanced ? sk_wgs(head_dim) : 0;
+    const size_t need = balanced ? sk_workspace(nw, n_seqs, n_heads, n_kv_heads, head_dim)
+                                 : (size_t)n_seqs * s_max * n_heads * (head_dim + 2) * sizeof(float);
+    MXD_REQUIRE((!balanced && s_max == 1) || (workspace && ws_bytes >= need), MXD_ERR_WORKSPACE,
                 "mxd_attention_paged: workspace of %zu bytes needed (got %zu)", need, ws_bytes);
     MXD_REQUIRE(!workspace || (reinterpret_cast<uintptr_t>(workspace) & 15) == 0, MXD_ERR_UNSUPPORTED,
                 "mxd_attention_paged: workspace must be 16-byte aligned");
@@ -652,7 +906,15 @@ extern "C" int mxd_attention_paged(const float* q, int q_stride, const uint16_t*
     a.v = vpool;
     a.out = out;
     a.ws_o = static_cast<float*>(workspace);
-    a.ws_ml = workspace ? a.ws_o + (size_t)n_seqs * s_max * n_heads * head_dim : nullptr;
+    if (balanced) {
+        const size_t slots = sk_slots(nw, n_seqs, n_kv_heads);
+        a.ws_ml = a.ws_o + slots * G * head_dim;
+        a.sk_pre = reinterpret_cast<int32_t*>(a.ws_ml + slots * G * 2);
+    } else {
+        a.ws_ml = workspace ? a.ws_o + (size_t)n_seqs * s_max * n_heads * head_dim : nullptr;
+    }
+    a.n_seqs = n_seqs;
+    a.sk_wgs = nw;
     a.pos_dev = nullptr;
     a.page_table = page_table;
     a.seq_lens = seq_lens;
@@ -666,9 +928,21 @@ extern "C" int mxd_attention_paged(const float* q, int q_stride, const uint16_t*
     a.max_ctx = max_pages * mxd::PAGE_KEYS;
     a.n_keys = 0;
     a.n_splits = s_max;
+    a.bps = paged_bps();
     a.qscale = scale * LOG2E;
 
     hipStream_t s = mxd::as_stream(stream);
+    if (balanced) {
+        const dim3 mgrid((n_heads * head_dim + SKM_T - 1) / SKM_T, n_seqs);
+        if (head_dim == 128) {
+            launch_paged_sk<128>(nw, s, a);
+            hipLaunchKernelGGL(attn_paged_sk_merge_kernel<128>, mgrid, dim3(SKM_T), 0, s, a);
+        } else {
+            launch_paged_sk<256>(nw, s, a);
+            hipLaunchKernelGGL(attn_paged_sk_merge_kernel<256>, mgrid, dim3(SKM_T), 0, s, a);
+        }
+        return mxd::check_launch("mxd_attention_paged");
+    }
     const dim3 grid(s_max, n_kv_heads, n_seqs);
     if (head_dim == 128) {
         launch_paged<128>(grid, s, a);

@@ -59,27 +59,47 @@ def _cache_with_rows(dev, rng, lens, nkv, hd, seed=11, stale=float("nan")):
     return cache, rows
 
 
-@pytest.mark.parametrize("nh,nkv,hd", [(32, 8, 128), (8, 1, 256), (16, 16, 128)])
-@pytest.mark.parametrize("max_keys", [None, 32])
-def test_attention_paged(dev, rng, nh, nkv, hd, max_keys):
-    """Ragged lengths around page and block edges, shuffled pages, NaN in every
-    unused slot; max_keys below the longest sequence only changes the split
-    count, never the result."""
+@pytest.fixture(params=["balanced", "splits"])
+def schedule(request):
+    """The paged attention's two schedules: items dealt evenly over the
+    resident workgroups (the default up to 2048 sequences), or a fixed number
+    of splits per sequence."""
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
+    _lib.set_tunable("ATT_SCHED", 1 if request.param == "balanced" else 2)
+    try:
+        yield request.param
+    finally:
+        _lib.set_tunable("ATT_SCHED", 0)
+
+
+def _check_paged(dev, rng, lens, nh, nkv, hd, max_keys=None, tol=1e-4):
     B = _bm()
-    lens = [1, 15, 16, 17, 31, 32, 33, 100, 513, 2048, 5000]
-    cache, rows = _cache_with_rows(dev, rng, lens, nkv, hd)
+    cache, rows = _cache_with_rows(dev, rng, [max(n, 1) for n in lens], nkv, hd)
     q = rng.standard_normal((len(lens), nh * hd), dtype=F32)
     seq = _d(np.array(lens, np.int32), dev)
     out = B.attention_paged(_d(q, dev), cache.k[0], cache.v[0], cache.table, seq, nh,
-                            max_keys=max_keys or max(lens))
+                            max_keys=max_keys or max(max(lens), 1))
     got = out.cpu().numpy()
     assert np.isfinite(got).all()
     for b, n in enumerate(lens):
+        if n == 0:
+            assert (got[b] == 0).all(), b
+            continue
         want = ref.attention(q[b], rows[b][0], rows[b][1], n, nh, 1.0 / math.sqrt(hd))
-        assert rel_err(got[b], want) <= 1e-4, (b, n)
+        assert rel_err(got[b], want) <= tol, (b, n)
 
 
-def test_attention_paged_empty_sequence_and_strided_q(dev, rng):
+@pytest.mark.parametrize("nh,nkv,hd", [(32, 8, 128), (8, 1, 256), (16, 16, 128)])
+@pytest.mark.parametrize("max_keys", [None, 32])
+def test_attention_paged(dev, rng, schedule, nh, nkv, hd, max_keys):
+    """Ragged lengths around page and block edges, shuffled pages, NaN in every
+    unused slot; max_keys below the longest sequence only changes the split
+    count, never the result."""
+    _check_paged(dev, rng, [1, 15, 16, 17, 31, 32, 33, 100, 513, 2048, 5000], nh, nkv, hd, max_keys)
+
+
+def test_attention_paged_empty_sequence_and_strided_q(dev, rng, schedule):
     """A sequence with no keys gets zeros; q read from qkv rows (stride > NH*hd)."""
     B = _bm()
     nh, nkv, hd = 8, 2, 128
@@ -93,6 +113,31 @@ def test_attention_paged_empty_sequence_and_strided_q(dev, rng):
     for b in (1, 2):
         want = ref.attention(qkv[b, : nh * hd], rows[b][0], rows[b][1], lens[b], nh, 1.0 / math.sqrt(hd))
         assert rel_err(out[b], want) <= 1e-4
+
+
+@pytest.mark.parametrize("per_cu", [1, 3, 64])
+def test_attention_paged_balanced_pieces(dev, rng, per_cu):
+    """The balanced schedule with few and with many workgroups: workgroup
+    ranges that hold several whole sequences, ranges that cut one segment into
+    many pieces, empty sequences between them, and a last sequence that ends
+    exactly on a workgroup edge."""
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
+    lens = [0, 3, 33, 0, 0, 64, 1, 900, 31, 0, 257, 2, 4096, 17, 0]
+    _lib.set_tunable("ATT_SKWG", per_cu)
+    try:
+        _check_paged(dev, rng, lens, 16, 4, 128)
+        _check_paged(dev, rng, [0, 0, 0], 8, 2, 128)  # no keys at all: every output zero
+    finally:
+        _lib.set_tunable("ATT_SKWG", 0)
+
+
+def test_attention_paged_many_sequences(dev, rng):
+    """Past 2048 sequences the paged attention falls back to per-sequence
+    splits; both sides of that edge, with short ragged lengths."""
+    for n_seqs in (2048, 2049):
+        lens = [int(n) for n in rng.integers(0, 70, n_seqs)]
+        _check_paged(dev, rng, lens, 8, 2, 128)
 
 
 def test_rope_kv_paged(dev, rng):
