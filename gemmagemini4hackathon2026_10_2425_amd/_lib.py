@@ -10,6 +10,7 @@ call raises. Return codes map to exceptions:
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from ctypes import c_char_p, c_float, c_int, c_size_t, c_uint64, c_void_p
 from pathlib import Path
@@ -136,6 +137,13 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
+        # MXD_TUNE="NAME=VALUE,..." presets kernel tunables for the process
+        # (the counterpart of the reference's `--define NAME=VALUE` knobs).
+        for item in os.environ.get("MXD_TUNE", "").split(","):
+            if item.strip():
+                key, _, val = item.partition("=")
+                if lib.mxd_set_tunable(key.strip().encode(), int(val)) != MXD_OK:
+                    raise ValueError(f"MXD_TUNE: bad entry {item!r}")
         _lib = lib
         return lib
 

@@ -10,33 +10,45 @@
 // s[r][blk] * (sum over the block's 32 k of q[r][k] * x[b][k]) with x fp16, q
 // int8 (exact in fp16), products exact in fp32 and fp32 accumulation.
 //
-// Work layout (gfx950, v_mfma_f32_16x16x32_f16):
-//  * a workgroup of 8 waves owns 128 weight rows (16 per wave; for the
+// Work layout (gfx950, v_mfma_f32_32x32x16_f16):
+//  * a workgroup of 4 waves owns 128 weight rows (32 per wave; for the
 //    gate/up pair 64 rows of each matrix) x 64 activation rows x one split of
-//    K of at most 1024 (8 steps of 128 = 4 quantisation blocks);
-//  * the split's whole 64 x <=1024 fp16 activation slice is loaded into LDS
-//    once (rows padded by 16 bytes so the 16-byte MFMA-operand reads are
-//    conflict-free); after that one barrier the waves never synchronise
-//    again: each streams its own weight rows straight from HBM through a
-//    register ring GM_PD steps ahead of the math;
-//  * one MFMA per (block, 16 activation rows) with the activations as the A
-//    operand and the weights as B, so each lane's four results share one
-//    weight row and one scale: acc += s * mfma(x, q, 0);
-//  * K is split across workgroups (as many splits as the LDS slice needs, and
-//    enough workgroups to fill the GPU); the fp32 partials are added in a
-//    fixed order by a second kernel that also applies the epilogue, so
-//    results are deterministic.
+//    K, walked in chunks of 128 k (4 quantisation blocks);
+//  * the weights are the B operand, so each lane's 16 results share one
+//    weight row and one scale, and a lane's 16-byte load (row r, bytes
+//    16h..16h+15 of a 32-byte block, h = lane / 32) feeds both MFMAs of the
+//    block: bytes 0-7 pair with activation k 16h..16h+7 and bytes 8-15 with
+//    16h+8..16h+15, so each MFMA's 16 k stay inside one block and
+//    acc += s * (q . x) stays exact;
+//  * weights go straight from HBM into registers two chunks ahead of the
+//    math; activations are loaded into registers two chunks ahead and written
+//    to a double-buffered LDS chunk (one barrier per chunk); the split's
+//    scales sit in LDS from the start;
+//  * the default kernel is fully unrolled over a compile-time number of chunks
+//    (4, 8 or 16), so every load is issued at a fixed point and the
+//    compiler's waits are exact (a runtime loop carrying in-flight registers
+//    gets a full drain at its head); a K whose chunk count no choice divides
+//    runs the same layout as a runtime loop;
+//  * K is split across workgroups; the fp32 partials are added in a fixed
+//    order by a second kernel that also applies the epilogue, so results are
+//    deterministic.
+//
+// Measured on MI355X at 64 rows (one Llama-3-8B layer, with the reduction):
+// qkv 6144x4096 21.9 us, o 4096x4096 18.4 us, gate/up 2x14336x4096 62.4 us,
+// down 4096x14336 34.8 us; an earlier layout (16x16 MFMAs, a 64 x 1024
+// activation slice resident in LDS, one workgroup per CU) took 29.3 / 19.9 /
+// 67.4 / 36.3 us.
 #include "common.hpp"
 
 namespace {
 
-constexpr int GM_WAVES = 8;
+constexpr int GM_WAVES = 4;
 constexpr int GM_THREADS = GM_WAVES * 64;
-constexpr int GM_ROWS = 16 * GM_WAVES;  // weight rows per workgroup (over both matrices)
+constexpr int GM_ROWS = 32 * GM_WAVES;  // weight rows per workgroup (over both matrices)
 constexpr int GM_BATCH = 64;            // activation rows per workgroup
-constexpr int GM_KC = 128;              // K per step (4 blocks)
-constexpr int GM_SMAX = 8;              // steps per split (LDS slice of 64 x 1024 halfs)
-constexpr int GM_XP = GM_SMAX * GM_KC + 8;  // LDS pitch in halfs (+16 bytes)
+constexpr int GM2_CK = 128;             // k per chunk (4 blocks)
+constexpr int GM2_XP = GM2_CK + 8;      // LDS pitch in halfs of the runtime-loop kernel (+16 bytes)
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 struct GemmArgs {
     const int8_t* W[2];
@@ -44,7 +56,7 @@ struct GemmArgs {
     const uint16_t* X;  // fp16 [n_rows][K]
     float* Y;           // fp32 [n_rows][M]
     float* part;        // fp32 [splits][n_rows][NMAT][M] when splits > 1
-    int n_rows, M, K, splits, ksteps;
+    int n_rows, M, K, splits;
 };
 
 template <int NMAT, int OP>
@@ -58,199 +70,368 @@ __device__ __forceinline__ float epilogue(float g, float u, float old) {
     }
 }
 
+__device__ __forceinline__ h8_t q8x8_to_h8(uint32_t lo, uint32_t hi) {
+    h2_t a[4];
+    mxd::i8x4_to_h2x2(lo, a[0], a[1]);
+    mxd::i8x4_to_h2x2(hi, a[2], a[3]);
+    return h8_t{a[0].x, a[0].y, a[1].x, a[1].y, a[2].x, a[2].y, a[3].x, a[3].y};
+}
 
-
-// Weight steps kept in flight per lane (a register ring), and the per-wave
-// LDS staging of one step's weights (16 rows of 128 bytes, rows padded by 16
-// bytes: the 8-byte MFMA-operand reads are conflict-free) and of the split's
-// scales (16 rows x up to 32 blocks).
-constexpr int GM_PD = 4;
-constexpr int GM_WP = GM_KC + 16;
-constexpr size_t GM_LDS_X = (size_t)GM_BATCH * GM_XP * 2;
-constexpr size_t GM_LDS_W = (size_t)GM_WAVES * 16 * GM_WP;
-constexpr size_t GM_LDS_S = (size_t)GM_WAVES * 16 * GM_SMAX * 4 * 2;
-constexpr size_t GM_LDS = GM_LDS_X + GM_LDS_W + GM_LDS_S;  // 155 KiB of the CU's 160
-
+// The runtime-loop form (any chunk count): activations in registers two
+// chunks ahead, a register ring of two chunks of weights and scales.
 template <int NMAT, int OP>
-__global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
-    constexpr int ROWS_PER_MAT = GM_ROWS / NMAT;       // 128 or 64
-    constexpr int WAVES_PER_MAT = GM_WAVES / NMAT;     // 8 or 4
-    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    _Float16* xs = reinterpret_cast<_Float16*>(smem);  // [GM_BATCH][GM_XP]
+__global__ void __launch_bounds__(GM_THREADS) gemm_q8_loop_kernel(GemmArgs a) {
+    constexpr int WAVES = GM_WAVES, NT = GM_THREADS;
+    constexpr int WPM = WAVES / NMAT;  // waves per matrix
+    constexpr int ROWS = 32 * WPM;     // weight rows of each matrix per workgroup
+    constexpr int XPT = GM_BATCH * GM2_CK / 8 / NT;  // 16-byte activation pieces per thread per chunk
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][GM_BATCH][GM2_XP];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int col = lane & 15, g = lane >> 4;
-    unsigned char* wst = smem + GM_LDS_X + (size_t)wave * 16 * GM_WP;                          // [16][GM_WP]
-    uint16_t* sst = reinterpret_cast<uint16_t*>(smem + GM_LDS_X + GM_LDS_W) + wave * 16 * GM_SMAX * 4;  // [16][32]
-    const int m = wave / WAVES_PER_MAT;  // which matrix this wave reads
-    // Grid (splits, row tiles, batch tiles): consecutive workgroups take the
-    // consecutive K splits of one row tile, so the workgroups running at once
-    // read whole contiguous stretches of the weight rows (HBM-page friendly).
-    const int row0 = blockIdx.y * ROWS_PER_MAT + 16 * (wave % WAVES_PER_MAT);
+    const int mc = lane & 31, h = lane >> 5;
+    const int m = wave / WPM;  // which matrix this wave reads
+    const int row0 = blockIdx.y * ROWS + 32 * (wave % WPM);
     const int split = blockIdx.x, b0 = blockIdx.z * GM_BATCH;
     const int M = a.M, K = a.K;
-    const int ks0 = split * a.ksteps / a.splits, ks1 = (split + 1) * a.ksteps / a.splits;  // <= GM_SMAX steps
-    const int nst = ks1 - ks0;
+    const int nck = K / GM2_CK;
+    const int c0 = split * nck / a.splits, c1 = (split + 1) * nck / a.splits;  // this split's chunks
 
-    // Weights are read row-contiguously: load u of a step gives lane l the 16
-    // bytes at 16 (l & 7) of row 8u + (l >> 3)'s 128-byte step segment, so each
-    // load is 8 whole 128-byte lines. Rows past M are clamped (never stored).
-    const int8_t* wbase[2];
+    // Weight row mc of the wave's 32 (clamped past M: computed, never stored).
+    const int wrow = min(row0 + mc, M - 1);
+    const int8_t* wp = a.W[m] + (size_t)wrow * K + (size_t)c0 * GM2_CK + 16 * h;
+    const uint16_t* sp = a.S[m] + (size_t)wrow * (K / 32) + (size_t)c0 * 4;
+    // Ring of two chunks: slot (par, j) holds block j of chunk c0 + 2i + par.
+    u4_t wr[2][4];
+    u2_t sr[2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
-        wbase[u] = a.W[m] + (size_t)min(row0 + 8 * u + (lane >> 3), M - 1) * K + (size_t)ks0 * GM_KC + 16 * (lane & 7);
-    auto load_w = [&](u4_t (&st)[2], int t) {
+    for (int par = 0; par < 2; ++par) {
+        if (c0 + par < c1) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-            st[u] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wbase[u] + (size_t)t * GM_KC));
+            for (int j = 0; j < 4; ++j)
+                wr[par][j] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wp + (size_t)par * GM2_CK + 32 * j));
+            sr[par] = *reinterpret_cast<const u2_t*>(sp + 4 * par);
+        }
+    }
+
+    // Activation chunk c: 64 rows x 128 halfs as 1024 pieces of 16 bytes;
+    // thread t takes pieces t + NT u (row p / 16, piece p % 16). Rows past
+    // n_rows are stored as zeros (loaded from a clamped, valid row).
+    const uint16_t* xbase = a.X + (size_t)c0 * GM2_CK;
+    auto load_x = [&](u4_t (&v)[XPT], int ci) {
+#pragma unroll
+        for (int u = 0; u < XPT; ++u) {
+            const int p = threadIdx.x + NT * u, r = p >> 4, q = p & 15;
+            v[u] = *reinterpret_cast<const u4_t*>(xbase + (size_t)min(b0 + r, a.n_rows - 1) * K + (size_t)ci * GM2_CK + 8 * q);
+        }
     };
-    u4_t w[GM_PD][2];
+    auto store_x = [&](const u4_t (&v)[XPT], int buf) {
 #pragma unroll
-    for (int p = 0; p < GM_PD; ++p)
-        if (p < nst) load_w(w[p], p);
-
-    // The split's scales: lane (col, g) fetches the 4 scales of steps g and
-    // g + 4 of its row col.
-    {
-        const uint16_t* srow = a.S[m] + (size_t)min(row0 + col, M - 1) * (K / 32) + (size_t)ks0 * 4;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int t = g + 4 * h;
-            if (t < nst)
-                *reinterpret_cast<u2_t*>(&sst[col * GM_SMAX * 4 + 4 * t]) = *reinterpret_cast<const u2_t*>(srow + 4 * t);
+        for (int u = 0; u < XPT; ++u) {
+            const int p = threadIdx.x + NT * u, r = p >> 4, q = p & 15;
+            const u4_t z = {0u, 0u, 0u, 0u};
+            *reinterpret_cast<u4_t*>(&xs[buf][r][8 * q]) = b0 + r < a.n_rows ? v[u] : z;
         }
-    }
-
-    // Activation slice: 64 rows x nst * 128 halfs in 16-byte pieces, rows past
-    // n_rows zero. Thread t takes row t / 8 and pieces t % 8 + 8u (no integer
-    // division); all its loads are issued before any store (from clamped,
-    // always valid addresses), so their latencies overlap.
-    {
-        constexpr int TPR = GM_THREADS / GM_BATCH;           // threads per row (8)
-        constexpr int NPT = GM_SMAX * (GM_KC / 8) / TPR;     // pieces per thread (16)
-        const int per_row = nst * (GM_KC / 8);
-        const int r = threadIdx.x / TPR, sub = threadIdx.x % TPR;
-        const uint16_t* xrow = a.X + (size_t)min(b0 + r, a.n_rows - 1) * K + (size_t)ks0 * GM_KC;
-        u4_t v[NPT];
-#pragma unroll
-        for (int u = 0; u < NPT; ++u) {
-            const int piece = min(sub + TPR * u, per_row - 1);
-            v[u] = *reinterpret_cast<const u4_t*>(xrow + piece * 8);
-        }
-        const bool live = b0 + r < a.n_rows;
-#pragma unroll
-        for (int u = 0; u < NPT; ++u) {
-            const int piece = sub + TPR * u;
-            if (piece < per_row) {
-                const u4_t z = {0u, 0u, 0u, 0u};
-                *reinterpret_cast<u4_t*>(&xs[r * GM_XP + piece * 8]) = live ? v[u] : z;
-            }
-        }
-    }
+    };
+    // Register ring of two chunks: set p holds chunk ci (ci & 1 == p) from its
+    // load, issued two chunks ahead, until it is stored to LDS buffer p at the
+    // end of chunk ci - 1.
+    u4_t xv[2][XPT];
+    load_x(xv[0], 0);
+    if (c0 + 1 < c1) load_x(xv[1], 1);
+    store_x(xv[0], 0);
     __syncthreads();
 
-    f4_t acc[4];
+    f32x16_t acc[2];
 #pragma unroll
-    for (int bg = 0; bg < 4; ++bg) acc[bg] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    const f4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int kb = 0; kb < nst; kb += GM_PD) {
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int p = 0; p < GM_PD; ++p) {
-            const int t = kb + p;  // step within the split
-            if (t < nst) {
-                // The step's weights through this wave's LDS slab into MFMA
-                // operand order (only this wave touches the slab: LDS accesses
-                // of one wave are ordered, the wave barrier orders the code).
-#pragma unroll
-                for (int u = 0; u < 2; ++u)
-                    *reinterpret_cast<u4_t*>(wst + (8 * u + (lane >> 3)) * GM_WP + 16 * (lane & 7)) = w[p][u];
-                if (t + GM_PD < nst) load_w(w[p], t + GM_PD);
-                __builtin_amdgcn_wave_barrier();
-                // All operands of the step first, then the 16 independent
-                // MFMAs back to back, then the per-block scaling, so no MFMA
-                // result is waited for while the matrix core could be busy.
-                h8_t wop[4];
-                float sc[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const u2_t q = *reinterpret_cast<const u2_t*>(wst + col * GM_WP + 32 * j + 8 * g);
-                    h2_t h[4];
-                    mxd::i8x4_to_h2x2(q.x, h[0], h[1]);
-                    mxd::i8x4_to_h2x2(q.y, h[2], h[3]);
-                    wop[j] = h8_t{h[0].x, h[0].y, h[1].x, h[1].y, h[2].x, h[2].y, h[3].x, h[3].y};
-                    sc[j] = mxd::h2f(sst[col * GM_SMAX * 4 + 4 * t + j]);
-                }
-                h8_t xop[4][4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int bg = 0; bg < 4; ++bg)
-                        xop[j][bg] = *reinterpret_cast<const h8_t*>(
-                            &xs[(bg * 16 + col) * GM_XP + t * GM_KC + 32 * j + 8 * g]);
-                f4_t c[4][4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int bg = 0; bg < 4; ++bg)
-                        c[j][bg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xop[j][bg], wop[j], zero, 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int bg = 0; bg < 4; ++bg)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) acc[bg][i] = fmaf(sc[j], c[j][bg][i], acc[bg][i]);
-                __builtin_amdgcn_wave_barrier();
-            }
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+    const f32x16_t zero = acc[0];
+
+    // One chunk (ci = chunk index within the split, par = ci & 1, also the LDS
+    // buffer holding it).
+    auto chunk = [&](const int ci, const int par) {
+        const bool more = c0 + ci + 1 < c1;
+        if (c0 + ci + 2 < c1) load_x(xv[par], ci + 2);
+        float sc[4];
+        {
+            const u2_t sv = sr[par];
+            sc[0] = mxd::h2f((uint16_t)(sv.x & 0xFFFFu));
+            sc[1] = mxd::h2f((uint16_t)(sv.x >> 16));
+            sc[2] = mxd::h2f((uint16_t)(sv.y & 0xFFFFu));
+            sc[3] = mxd::h2f((uint16_t)(sv.y >> 16));
         }
+        const bool refill = c0 + ci + 2 < c1;
+        if (refill) sr[par] = *reinterpret_cast<const u2_t*>(sp + 4 * (ci + 2));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u4_t w = wr[par][j];
+            if (refill)
+                wr[par][j] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u4_t*>(wp + (size_t)(ci + 2) * GM2_CK + 32 * j));
+            const h8_t w0 = q8x8_to_h8(w.x, w.y), w1 = q8x8_to_h8(w.z, w.w);
+            const int kx = 32 * j + 16 * h;
+            const h8_t x00 = *reinterpret_cast<const h8_t*>(&xs[par][mc][kx]);
+            const h8_t x01 = *reinterpret_cast<const h8_t*>(&xs[par][mc][kx + 8]);
+            const h8_t x10 = *reinterpret_cast<const h8_t*>(&xs[par][32 + mc][kx]);
+            const h8_t x11 = *reinterpret_cast<const h8_t*>(&xs[par][32 + mc][kx + 8]);
+            f32x16_t t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x00, w0, zero, 0, 0, 0);
+            f32x16_t t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, zero, 0, 0, 0);
+            t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, t0, 0, 0, 0);
+            t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, t1, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc[0][r] = fmaf(sc[j], t0[r], acc[0][r]);
+                acc[1][r] = fmaf(sc[j], t1[r], acc[1][r]);
+            }
+            // One block's products live at a time: the empty asm consumes the
+            // accumulators here, so the scaling cannot be sunk below the next
+            // block's MFMAs (which would keep all four blocks' products live).
+            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
+        }
+        if (more) store_x(xv[par ^ 1], par ^ 1);
+        __syncthreads();
+    };
+    const int nc = c1 - c0;
+    for (int ci = 0; ci < nc; ci += 2) {
+        chunk(ci, 0);
+        if (ci + 1 < nc) chunk(ci + 1, 1);
     }
 
-    // Lane (col, g) holds rows b0 + 16 bg + 4 g + i of weight row row0 + col.
-    const int wr = row0 + col;
+    // Lane (mc, h), register r of tile t: activation row b0 + 32 t + 8 (r / 4)
+    // + 4 h + r % 4, weight row row0 + mc.
+    const int wr_out = row0 + mc;
+    auto brow = [&](int t, int r) { return b0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3); };
     if (a.splits > 1) {
-        if (wr < M) {
+        if (wr_out < M) {
 #pragma unroll
-            for (int bg = 0; bg < 4; ++bg)
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int b = b0 + 16 * bg + 4 * g + i;
-                    if (b < a.n_rows) a.part[(((size_t)split * a.n_rows + b) * NMAT + m) * M + wr] = acc[bg][i];
+                for (int r = 0; r < 16; ++r) {
+                    const int b = brow(t, r);
+                    if (b < a.n_rows) a.part[(((size_t)split * a.n_rows + b) * NMAT + m) * M + wr_out] = acc[t][r];
                 }
         }
         return;
     }
     if constexpr (NMAT == 2) {
-        // The up waves hand their sums to the gate waves holding the same rows
-        // through LDS (the activation slice is no longer needed).
-        float* xf = reinterpret_cast<float*>(smem);
-        __syncthreads();
+        // The up waves hand their sums to the gate waves of the same rows
+        // through LDS (the activation buffers are free after the last barrier).
+        float* xf = reinterpret_cast<float*>(&xs[0][0][0]);
         if (m == 1) {
 #pragma unroll
-            for (int bg = 0; bg < 4; ++bg)
+            for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    xf[(((wave - WAVES_PER_MAT) * 4 + bg) * 4 + i) * 64 + lane] = acc[bg][i];
+                for (int r = 0; r < 16; ++r) xf[(((wave - WPM) * 2 + t) * 16 + r) * 64 + lane] = acc[t][r];
         }
         __syncthreads();
-        if (m == 1 || wr >= M) return;
+        if (m == 1 || wr_out >= M) return;
 #pragma unroll
-        for (int bg = 0; bg < 4; ++bg)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int b = b0 + 16 * bg + 4 * g + i;
-                const float u = xf[((wave * 4 + bg) * 4 + i) * 64 + lane];
-                if (b < a.n_rows) a.Y[(size_t)b * M + wr] = epilogue<NMAT, OP>(acc[bg][i], u, 0.0f);
+            for (int r = 0; r < 16; ++r) {
+                const int b = brow(t, r);
+                const float u = xf[((wave * 2 + t) * 16 + r) * 64 + lane];
+                if (b < a.n_rows) a.Y[(size_t)b * M + wr_out] = epilogue<NMAT, OP>(acc[t][r], u, 0.0f);
             }
     } else {
-        if (wr >= M) return;
+        if (wr_out >= M) return;
 #pragma unroll
-        for (int bg = 0; bg < 4; ++bg)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int b = b0 + 16 * bg + 4 * g + i;
+            for (int r = 0; r < 16; ++r) {
+                const int b = brow(t, r);
                 if (b < a.n_rows) {
-                    float* y = a.Y + (size_t)b * M + wr;
-                    *y = epilogue<NMAT, OP>(acc[bg][i], 0.0f, OP == MXD_EPI_ADD ? *y : 0.0f);
+                    float* y = a.Y + (size_t)b * M + wr_out;
+                    *y = epilogue<NMAT, OP>(acc[t][r], 0.0f, OP == MXD_EPI_ADD ? *y : 0.0f);
+                }
+            }
+    }
+}
+
+// Compile-time loop helpers for the fully unrolled chunk loop below.
+template <int V>
+struct ic {
+    static constexpr int value = V;
+};
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(ic<I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// The default kernel: NCH chunks per workgroup, fully unrolled.
+template <int NMAT, int OP, int NCH>
+__global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
+    constexpr int WAVES = GM_WAVES, NT = GM_THREADS;
+    constexpr int WPM = WAVES / NMAT;
+    constexpr int ROWS = 32 * WPM;
+    constexpr int XPT = GM_BATCH * GM2_CK / 8 / NT;
+    // Two activation buffers (chunk ci in xs[ci & 1]), rows swizzled: piece p
+    // of row b sits at slot p ^ (b & 15).
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][GM_BATCH][GM2_CK];
+    // the split's scales of each wave's 32 rows: [wave][row][NCH * 4 (+8 pad,
+    // keeping every row 16-byte aligned for the 16-byte stores below)]
+    constexpr int SP = NCH * 4 + 8;
+    __shared__ __attribute__((aligned(16))) uint16_t ss[WAVES][32][SP];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int mc = lane & 31, h = lane >> 5;
+    const int m = wave / WPM;
+    const int row0 = blockIdx.y * ROWS + 32 * (wave % WPM);
+    const int split = blockIdx.x, b0 = blockIdx.z * GM_BATCH;
+    const int M = a.M, K = a.K;
+    const int c0 = split * NCH;  // a.splits * NCH == K / GM2_CK
+
+    const int wrow = min(row0 + mc, M - 1);
+    const int8_t* wp = a.W[m] + (size_t)wrow * K + (size_t)c0 * GM2_CK + 16 * h;
+    const uint16_t* xbase = a.X + (size_t)c0 * GM2_CK;
+
+    // Activations of chunk ci: thread t loads pieces t + NT u (row p / 16,
+    // piece p % 16) into register set ci & 1, two chunks ahead; the set is
+    // written to LDS buffer ci & 1 at the end of chunk ci - 1.
+    u4_t xv[2][XPT];
+    auto load_x = [&](auto cic) {
+        constexpr int ci = decltype(cic)::value;
+#pragma unroll
+        for (int u = 0; u < XPT; ++u) {
+            const int p = threadIdx.x + NT * u, r = p >> 4, q = p & 15;
+            xv[ci & 1][u] = *reinterpret_cast<const u4_t*>(xbase + (size_t)min(b0 + r, a.n_rows - 1) * K +
+                                                          (size_t)ci * GM2_CK + 8 * q);
+        }
+    };
+    auto store_x = [&](auto cic) {
+        constexpr int ci = decltype(cic)::value;
+#pragma unroll
+        for (int u = 0; u < XPT; ++u) {
+            const int p = threadIdx.x + NT * u, r = p >> 4, q = p & 15;
+            *reinterpret_cast<u4_t*>(&xs[ci & 1][r][8 * (q ^ (r & 15))]) = xv[ci & 1][u];
+        }
+    };
+    u4_t wr[2][4];
+    auto load_w = [&](int ci, int j) {
+        wr[ci & 1][j] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wp + (size_t)ci * GM2_CK + 32 * j));
+    };
+    // Scales first: lane l fetches row l / 2's half (l & 1) of the split's
+    // NCH * 4 scales (NCH * 4 bytes) in 16-byte pieces.
+    constexpr int SPL = NCH * 4 / 2 / 8;  // 16-byte pieces per lane
+    u4_t sv[SPL];
+    {
+        const uint16_t* srow = a.S[m] + (size_t)min(row0 + (lane >> 1), M - 1) * (K / 32) + (size_t)c0 * 4 +
+                               (lane & 1) * (NCH * 2);
+#pragma unroll
+        for (int u = 0; u < SPL; ++u) sv[u] = *reinterpret_cast<const u4_t*>(srow + 8 * u);
+    }
+    // Every load lands in registers, so the compiler's own waits are exact.
+    load_x(ic<0>{});
+#pragma unroll
+    for (int j = 0; j < 4; ++j) load_w(0, j);
+    if constexpr (NCH > 1) {
+        load_x(ic<1>{});
+#pragma unroll
+        for (int j = 0; j < 4; ++j) load_w(1, j);
+    }
+#pragma unroll
+    for (int u = 0; u < SPL; ++u)
+        *reinterpret_cast<u4_t*>(&ss[wave][lane >> 1][(lane & 1) * (NCH * 2) + 8 * u]) = sv[u];
+    store_x(ic<0>{});
+    __syncthreads();
+    f32x16_t acc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+    const f32x16_t zero = acc[0];
+
+    static_for<0, NCH>([&](auto cic) {
+        constexpr int ci = decltype(cic)::value;
+        constexpr int par = ci & 1;
+        const _Float16(*xcur)[GM2_CK] = xs[par];
+        float sc[4];
+        {
+            const u2_t sv2 = *reinterpret_cast<const u2_t*>(&ss[wave][mc][4 * ci]);
+            sc[0] = mxd::h2f((uint16_t)(sv2.x & 0xFFFFu));
+            sc[1] = mxd::h2f((uint16_t)(sv2.x >> 16));
+            sc[2] = mxd::h2f((uint16_t)(sv2.y & 0xFFFFu));
+            sc[3] = mxd::h2f((uint16_t)(sv2.y >> 16));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (ci + 2 < NCH) load_x(ic<ci + 2>{});
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u4_t w = wr[par][j];
+            const h8_t w0 = q8x8_to_h8(w.x, w.y), w1 = q8x8_to_h8(w.z, w.w);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (ci + 2 < NCH) load_w(ci + 2, j);
+            __builtin_amdgcn_sched_barrier(0);
+            const int p0 = 4 * j + 2 * h, sw = mc & 15;
+            const h8_t x00 = *reinterpret_cast<const h8_t*>(&xcur[mc][8 * (p0 ^ sw)]);
+            const h8_t x01 = *reinterpret_cast<const h8_t*>(&xcur[mc][8 * ((p0 + 1) ^ sw)]);
+            const h8_t x10 = *reinterpret_cast<const h8_t*>(&xcur[32 + mc][8 * (p0 ^ sw)]);
+            const h8_t x11 = *reinterpret_cast<const h8_t*>(&xcur[32 + mc][8 * ((p0 + 1) ^ sw)]);
+            f32x16_t t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x00, w0, zero, 0, 0, 0);
+            f32x16_t t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, zero, 0, 0, 0);
+            t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, t0, 0, 0, 0);
+            t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, t1, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                acc[0][r] = fmaf(sc[j], t0[r], acc[0][r]);
+                acc[1][r] = fmaf(sc[j], t1[r], acc[1][r]);
+            }
+            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
+        }
+        if constexpr (ci + 1 < NCH) {
+            store_x(ic<ci + 1>{});
+            __syncthreads();
+        }
+    });
+
+    const int wr_out = row0 + mc;
+    auto brow = [&](int t, int r) { return b0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3); };
+    if (a.splits > 1) {
+        if (wr_out < M) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int b = brow(t, r);
+                    if (b < a.n_rows) a.part[(((size_t)split * a.n_rows + b) * NMAT + m) * M + wr_out] = acc[t][r];
+                }
+        }
+        return;
+    }
+    if constexpr (NMAT == 2) {
+        float* xf = reinterpret_cast<float*>(&xs[0][0][0]);  // WPM * 2048 floats: 16 KiB for 4 waves
+        __syncthreads();  // every wave is past its last LDS read
+        if (m == 1) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) xf[(((wave - WPM) * 2 + t) * 16 + r) * 64 + lane] = acc[t][r];
+        }
+        __syncthreads();
+        if (m == 1 || wr_out >= M) return;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int b = brow(t, r);
+                const float u = xf[((wave * 2 + t) * 16 + r) * 64 + lane];
+                if (b < a.n_rows) a.Y[(size_t)b * M + wr_out] = epilogue<NMAT, OP>(acc[t][r], u, 0.0f);
+            }
+    } else {
+        if (wr_out >= M) return;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int b = brow(t, r);
+                if (b < a.n_rows) {
+                    float* y = a.Y + (size_t)b * M + wr_out;
+                    *y = epilogue<NMAT, OP>(acc[t][r], 0.0f, OP == MXD_EPI_ADD ? *y : 0.0f);
                 }
             }
     }
@@ -274,18 +455,38 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a) {
 }
 
 bool use_mfma(int n_rows, int K) {
-    return n_rows >= mxd::tunable("GM_MIN_ROWS", 16) && K % GM_KC == 0;
+    return n_rows >= mxd::tunable("GM_MIN_ROWS", 16) && K % GM2_CK == 0;
 }
 
-// K splits: at least enough that a split's activation slice fits the LDS
-// (GM_SMAX steps), and enough workgroups for one per CU; the GM_SPLITS tunable
-// can ask for more (up to one step per split), never fewer.
-int pick_splits(int n_rows, int M, int K, int nmat) {
+// Chunks per workgroup of the unrolled kernel: the largest of 16, 8, 4 that
+// divides K's chunk count and still gives at least 192 workgroups (3/4 of the
+// CUs); the GM_NCH tunable (4, 8, 16) forces one, GM_NCH = 1 the runtime loop;
+// 0 (the runtime loop) when none divides.
+int pick_nch(int n_rows, int M, int K, int nmat) {
+    const int nck = K / GM2_CK;
     const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + GM_BATCH - 1) / GM_BATCH);
-    const int ksteps = K / GM_KC;
-    const int min_s = (ksteps + GM_SMAX - 1) / GM_SMAX;
-    int s = mxd::tunable("GM_SPLITS", max(min_s, (256 + tiles - 1) / tiles));
-    return max(min_s, min(s, ksteps));
+    const int forced = mxd::tunable("GM_NCH", 0);
+    if (forced == 1) return 0;
+    if (forced == 4 || forced == 8 || forced == 16) return nck % forced == 0 ? forced : 0;
+    int best = 0;
+    for (int nch : {16, 8, 4}) {
+        if (nck % nch) continue;
+        if (!best) best = nch;
+        if (tiles * (nck / nch) >= 192) return nch;
+        best = nch;
+    }
+    return best;
+}
+
+// K splits: nck / NCH for the unrolled kernel; for the runtime loop about two
+// workgroups per CU, at most one split per chunk. GM_SPLITS overrides the
+// latter.
+int pick_splits(int n_rows, int M, int K, int nmat) {
+    const int nch = pick_nch(n_rows, M, K, nmat);
+    if (nch) return (K / GM2_CK) / nch;
+    const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + GM_BATCH - 1) / GM_BATCH);
+    const int s = mxd::tunable("GM_SPLITS", (512 + tiles - 1) / tiles);
+    return max(1, min(s, K / GM2_CK));
 }
 
 size_t ws_bytes_for(int n_rows, int M, int K, int nmat) {
@@ -296,19 +497,18 @@ size_t ws_bytes_for(int n_rows, int M, int K, int nmat) {
 
 template <int NMAT, int OP>
 int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char* fn) {
-    a.ksteps = a.K / GM_KC;
     a.splits = pick_splits(a.n_rows, a.M, a.K, NMAT);
     const size_t need = a.splits > 1 ? (size_t)a.splits * a.n_rows * NMAT * a.M * sizeof(float) : 0;
     MXD_REQUIRE(need == 0 || (ws && ws_bytes >= need), MXD_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)",
                 fn, need, ws_bytes);
     a.part = static_cast<float*>(ws);
     const dim3 grid(a.splits, (a.M + GM_ROWS / NMAT - 1) / (GM_ROWS / NMAT), (a.n_rows + GM_BATCH - 1) / GM_BATCH);
-    const size_t lds = GM_LDS;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_q8_kernel<NMAT, OP>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    MXD_REQUIRE(attr == hipSuccess, MXD_ERR_HIP, "%s: cannot enable %zu bytes of LDS: %s", fn, lds,
-                hipGetErrorString(attr));
-    hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP>), grid, dim3(GM_THREADS), lds, s, a);
+    switch (pick_nch(a.n_rows, a.M, a.K, NMAT)) {
+        case 4: hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP, 4>), grid, dim3(GM_THREADS), 0, s, a); break;
+        case 8: hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP, 8>), grid, dim3(GM_THREADS), 0, s, a); break;
+        case 16: hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP, 16>), grid, dim3(GM_THREADS), 0, s, a); break;
+        default: hipLaunchKernelGGL((gemm_q8_loop_kernel<NMAT, OP>), grid, dim3(GM_THREADS), 0, s, a); break;
+    }
     if (a.splits > 1) {
         const size_t n = (size_t)a.n_rows * a.M;
         const size_t nb = (n + 255) / 256;

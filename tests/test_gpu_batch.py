@@ -170,10 +170,11 @@ def _qweights(rng, M, K):
 
 
 @pytest.mark.parametrize("rows", [1, 15, 16, 17, 64, 100])
-@pytest.mark.parametrize("M,K", [(1000, 4096), (96, 256), (257, 4160)])
+@pytest.mark.parametrize("M,K", [(1000, 4096), (96, 256), (257, 4160), (130, 640)])
 def test_gemm_q8b32(dev, rng, rows, M, K):
     """Both sides of the matvec/matrix-core switch (16 rows; K % 128 for the
-    matrix cores) and both epilogues."""
+    matrix cores), both epilogues, the unrolled kernel (K = 4096) and the
+    runtime loop (256 and 640: 2 and 5 chunks, which 4 does not divide)."""
     B = _bm()
     q, s = _qweights(rng, M, K)
     X = rng.standard_normal((rows, K), dtype=F32).astype(F16)
@@ -186,9 +187,11 @@ def test_gemm_q8b32(dev, rng, rows, M, K):
     assert rel_err(Yd.cpu().numpy(), Y0 + want) <= 1e-4
 
 
-@pytest.mark.parametrize("splits", [1, 3, 32])
-def test_gemm_q8b32_k_splits(dev, rng, splits):
-    """Every K split (partials added in split order by the second kernel)."""
+@pytest.mark.parametrize("nch,splits", [(4, 0), (8, 0), (16, 0), (1, 1), (1, 3), (1, 32)])
+def test_gemm_q8b32_k_splits(dev, rng, nch, splits):
+    """Every chunk count of the unrolled kernel (8, 4 and 2 K splits at K =
+    4096) and the runtime loop (GM_NCH = 1) at 1, 3 and 32 splits; partials
+    are added in split order by the second kernel."""
     from gemmagemini4hackathon2026_10_2425_amd import _lib
 
     B = _bm()
@@ -197,12 +200,14 @@ def test_gemm_q8b32_k_splits(dev, rng, splits):
     X = rng.standard_normal((rows, K), dtype=F32).astype(F16)
     want = obatch.gemm_q8b32(q, s, X)
     try:
+        _lib.set_tunable("GM_NCH", nch)
         _lib.set_tunable("GM_SPLITS", splits)
         Y0 = rng.standard_normal((rows, M), dtype=F32)
         Yd = _d(Y0, dev)
         B.gemm_q8b32(_d(q, dev), _d(s, dev), _d(X, dev), Yd, "add")
         assert rel_err(Yd.cpu().numpy(), Y0 + want) <= 1e-4
     finally:
+        _lib.set_tunable("GM_NCH", 0)
         _lib.set_tunable("GM_SPLITS", 0)
 
 
@@ -218,11 +223,15 @@ def test_gemm_gate_up_q8b32(dev, rng, rows, act):
     X = rng.standard_normal((rows, K), dtype=F32).astype(F16)
     want = obatch.gate_up_rows(qg, sg, qu, su, X, act)
     args = [_d(a, dev) for a in (qg, sg, qu, su, X)]
-    for splits in (0, 4):  # as chosen, and forced partials
+    # as chosen (4 chunks, 2 splits), one split of 8 unrolled chunks, and the
+    # runtime loop with and without partials
+    for nch, splits in ((0, 0), (8, 0), (1, 1), (1, 4)):
         try:
+            _lib.set_tunable("GM_NCH", nch)
             _lib.set_tunable("GM_SPLITS", splits)
             assert rel_err(B.gemm_gate_up_q8b32(*args, act).cpu().numpy(), want) <= 1e-4
         finally:
+            _lib.set_tunable("GM_NCH", 0)
             _lib.set_tunable("GM_SPLITS", 0)
 
 
