@@ -189,9 +189,13 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
     constexpr int NC = HD / 32;  // MFMA k-chunks over head_dim for Q.K
     constexpr int ND = HD / 16;  // 16-wide dim tiles for P.V
     constexpr int NT = W * 64;
-    __shared__ float sm_o[W][8][HD];
+    // per-wave O: [wave][row][dim], rows 0-7 the hi part of heads 0-7, rows
+    // 8-15 the lo part (summed in the merge); rows padded by 4 floats so both
+    // the tile writes and the merge's reads hit distinct banks
+    __shared__ float sm_o[W][16][HD + 4];
     __shared__ float sm_m[W][8];
     __shared__ float sm_l[W][8];
+    __shared__ float sm_c[W][8];  // merge weight of wave w for head h
 
     const int G = a.G;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -322,48 +326,53 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
         }
     }
 
-    // ---- per-wave results: l summed over the 4 lane groups; O hi + lo rows.
+    // ---- per-wave results: l summed over the 4 lane groups; all 16 O rows
+    // (hi and lo parts) go to LDS unmasked. Folding hi + lo here with
+    // cross-lane shuffles behind per-row branches serialised into one LDS round
+    // trip per row (~2.5 us at head_dim 256).
     l_run += __shfl_xor(l_run, 16);
     l_run += __shfl_xor(l_run, 32);
     if (lane < G) {
         sm_m[wave][lane] = m_ref;
         sm_l[wave][lane] = l_run;
     }
-    // Row h (hi, lane group h/4) + row h + 8 (lo, lane group h/4 + 2) -> head h.
 #pragma unroll
-    for (int d = 0; d < ND; ++d) {
-        const int dim = 16 * d + col;
+    for (int d = 0; d < ND; ++d)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float other = __shfl_xor(o[d][i], 32);
-            const int h = 4 * g + i;
-            if (h < G) sm_o[wave][h][dim] = o[d][i] + other;
-        }
-    }
+        for (int i = 0; i < 4; ++i) sm_o[wave][4 * g + i][16 * d + col] = o[d][i];
     __syncthreads();
 
-    // ---- merge the waves (and write the partial or the output)
-    for (int idx = threadIdx.x; idx < G * HD; idx += NT) {
-        const int h = idx / HD, dim = idx - h * HD;
+    // ---- merge the waves (and write the partial or the output). First the
+    // per-(wave, head) weights 2^(m_w - M) (over the total sum for a direct
+    // output), then each value is row h (hi) + row h + 8 (lo) of every wave,
+    // weighted.
+    if (threadIdx.x < G) {
+        const int h = threadIdx.x;
         float M = sm_m[0][h];
 #pragma unroll
         for (int w = 1; w < W; ++w) M = fmaxf(M, sm_m[w][h]);
-        float so = 0.0f, sl = 0.0f;
+        float f[W], sl = 0.0f;
 #pragma unroll
         for (int w = 0; w < W; ++w) {
-            const float f = exp2f(sm_m[w][h] - M);
-            so += f * sm_o[w][h][dim];
-            sl += f * sm_l[w][h];
+            f[w] = __builtin_amdgcn_exp2f(sm_m[w][h] - M);
+            sl += f[w] * sm_l[w][h];
         }
-        if (out.direct) {
-            out.orow[idx] = so / sl;
-        } else {
-            out.po[idx] = so;
-            if (dim == 0) {
-                out.pml[2 * h + 0] = M;
-                out.pml[2 * h + 1] = sl;
-            }
+        const float norm = out.direct ? 1.0f / sl : 1.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) sm_c[w][h] = f[w] * norm;
+        if (!out.direct) {
+            out.pml[2 * h + 0] = M;
+            out.pml[2 * h + 1] = sl;
         }
+    }
+    __syncthreads();
+    float* dst = out.direct ? out.orow : out.po;
+    for (int idx = threadIdx.x; idx < G * HD; idx += NT) {
+        const int h = idx / HD, dim = idx - h * HD;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) v += sm_c[w][h] * (sm_o[w][h][dim] + sm_o[w][h + 8][dim]);
+        dst[idx] = v;
     }
     __syncthreads();  // the LDS rows are free for the next run
 }
@@ -717,10 +726,11 @@ void launch_paged_sk(int nw, hipStream_t s, const AttnArgs& a) {
     }
 }
 
-// Splits per kv head: about ATT_WGCU (default 2) workgroups per CU over the
-// whole grid, and never more splits than 32-key blocks.
+// Splits per kv head: about ATT_WGCU (default 3, as many as stay resident at
+// head_dim 128) workgroups per CU over the whole grid, and never more splits
+// than 32-key blocks.
 int target_splits(int n_kv) {
-    const int per_cu = max(1, min(16, mxd::tunable("ATT_WGCU", 2)));
+    const int per_cu = max(1, min(16, mxd::tunable("ATT_WGCU", 3)));
     return min(MAX_SPLITS, (per_cu * 256 + n_kv - 1) / n_kv);
 }
 
