@@ -580,12 +580,12 @@ __global__ void __launch_bounds__(SKM_T) attn_paged_sk_merge_kernel(AttnArgs a) 
 // dims of one query head: thread (grp, d) sums its dim over splits grp,
 // grp + MG, ...; its first PRE partials are loaded before the (M_s, L_s) pass
 // so the two latencies overlap, which makes the common case (up to MG * PRE =
-// 64 splits) one round trip. The groups are combined in LDS in a fixed order
+// 96 splits, the long-context default) one round trip. The groups are combined in LDS in a fixed order
 // (deterministic).
 constexpr int MG_D = 32;
 constexpr int MG = 8;
 constexpr int MG_T = MG * MG_D;
-constexpr int PRE = 8;
+constexpr int PRE = 12;
 
 template <int HD>
 __device__ __forceinline__ void attn_merge_core(const AttnArgs& a, int n_active, int head, int dchunk, float* orow,
