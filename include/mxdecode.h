@@ -220,7 +220,12 @@ int mxd_rope_kv_paged(float* qkv, uint16_t* kpool, uint16_t* vpool, int n_pages,
                       int n_heads, int n_kv_heads, int head_dim, const int32_t* page_table, int max_pages,
                       const int32_t* seq_lens, int n_seqs, mxd_stream_t stream);
 
-/* Workspace bytes mxd_attention_paged needs (max_keys bounds every seq_lens). */
+/* Workspace bytes mxd_attention_paged needs (max_keys bounds every seq_lens).
+ * The size follows the schedule the call will use: up to 2048 sequences the
+ * batch's (sequence, kv head, block) items are dealt evenly over the
+ * workgroups resident on the GPU (partials per workgroup piece plus a block
+ * prefix), beyond that a fixed number of splits per sequence; query it again
+ * after changing the ATT_SCHED / ATT_SKWG / ATT_BPS tunables. */
 size_t mxd_attention_paged_workspace_size(int n_heads, int n_kv_heads, int head_dim, int n_seqs, int max_keys);
 
 /* out[b][h] = softmax(scale * q[b][h] · K_b[kvh]) · V_b[kvh] over the seq_lens[b]
