@@ -25,7 +25,7 @@
 //    to a double-buffered LDS chunk (one barrier per chunk); the split's
 //    scales sit in LDS from the start;
 //  * the default kernel is fully unrolled over a compile-time number of chunks
-//    (4, 8 or 16), so every load is issued at a fixed point and the
+//    (4, 8, 16 or 32), so every load is issued at a fixed point and the
 //    compiler's waits are exact (a runtime loop carrying in-flight registers
 //    gets a full drain at its head); a K whose chunk count no choice divides
 //    runs the same layout as a runtime loop;
@@ -34,7 +34,7 @@
 //    deterministic.
 //
 // Measured on MI355X at 64 rows (one Llama-3-8B layer, with the reduction):
-// qkv 6144x4096 21.9 us, o 4096x4096 18.4 us, gate/up 2x14336x4096 62.4 us,
+// qkv 6144x4096 21.9 us, o 4096x4096 18.4 us, gate/up 2x14336x4096 62.2 us,
 // down 4096x14336 34.8 us; an earlier layout (16x16 MFMAs, a 64 x 1024
 // activation slice resident in LDS, one workgroup per CU) took 29.3 / 19.9 /
 // 67.4 / 36.3 us.
@@ -458,18 +458,20 @@ bool use_mfma(int n_rows, int K) {
     return n_rows >= mxd::tunable("GM_MIN_ROWS", 16) && K % GM2_CK == 0;
 }
 
-// Chunks per workgroup of the unrolled kernel: the largest of 16, 8, 4 that
-// divides K's chunk count and still gives at least 192 workgroups (3/4 of the
-// CUs); the GM_NCH tunable (4, 8, 16) forces one, GM_NCH = 1 the runtime loop;
-// 0 (the runtime loop) when none divides.
+// Chunks per workgroup of the unrolled kernel: the largest of 32, 16, 8, 4
+// that divides K's chunk count and still gives at least 192 workgroups (3/4 of
+// the CUs); the GM_NCH tunable (4, 8, 16, 32) forces one, GM_NCH = 1 the runtime
+// loop; 0 (the runtime loop) when none divides. Fewer, longer splits also save
+// the partials and their reduction (gate/up at 64 rows: 62.2 us with one split
+// of 32 chunks against 65.1 us with two of 16).
 int pick_nch(int n_rows, int M, int K, int nmat) {
     const int nck = K / GM2_CK;
     const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + GM_BATCH - 1) / GM_BATCH);
     const int forced = mxd::tunable("GM_NCH", 0);
     if (forced == 1) return 0;
-    if (forced == 4 || forced == 8 || forced == 16) return nck % forced == 0 ? forced : 0;
+    if (forced == 4 || forced == 8 || forced == 16 || forced == 32) return nck % forced == 0 ? forced : 0;
     int best = 0;
-    for (int nch : {16, 8, 4}) {
+    for (int nch : {32, 16, 8, 4}) {
         if (nck % nch) continue;
         if (!best) best = nch;
         if (tiles * (nck / nch) >= 192) return nch;
@@ -507,6 +509,7 @@ int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char
         case 4: hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP, 4>), grid, dim3(GM_THREADS), 0, s, a); break;
         case 8: hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP, 8>), grid, dim3(GM_THREADS), 0, s, a); break;
         case 16: hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP, 16>), grid, dim3(GM_THREADS), 0, s, a); break;
+        case 32: hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP, 32>), grid, dim3(GM_THREADS), 0, s, a); break;
         default: hipLaunchKernelGGL((gemm_q8_loop_kernel<NMAT, OP>), grid, dim3(GM_THREADS), 0, s, a); break;
     }
     if (a.splits > 1) {

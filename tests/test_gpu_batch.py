@@ -187,9 +187,9 @@ def test_gemm_q8b32(dev, rng, rows, M, K):
     assert rel_err(Yd.cpu().numpy(), Y0 + want) <= 1e-4
 
 
-@pytest.mark.parametrize("nch,splits", [(4, 0), (8, 0), (16, 0), (1, 1), (1, 3), (1, 32)])
+@pytest.mark.parametrize("nch,splits", [(4, 0), (8, 0), (16, 0), (32, 0), (1, 1), (1, 3), (1, 32)])
 def test_gemm_q8b32_k_splits(dev, rng, nch, splits):
-    """Every chunk count of the unrolled kernel (8, 4 and 2 K splits at K =
+    """Every chunk count of the unrolled kernel (8, 4, 2 and 1 K splits at K =
     4096) and the runtime loop (GM_NCH = 1) at 1, 3 and 32 splits; partials
     are added in split order by the second kernel."""
     from gemmagemini4hackathon2026_10_2425_amd import _lib
