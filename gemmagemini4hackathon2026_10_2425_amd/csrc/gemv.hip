@@ -627,14 +627,18 @@ int launch_sweep(const GemvArgs& a, int nw, int cpw, int wg_per_cu, hipStream_t 
 // every tiling timed back to back): four waves across K for rows of up to 8
 // chunks, eight for longer rows; two rows per workgroup with fp16 x, four with
 // fp32 x (more x registers per chunk), eight for int8 weights (half the bytes
-// per row). Small M keeps enough workgroups to fill the GPU.
-void pick_tiling(int M, int nch, bool q8, bool x_half, int& nr, int& nw) {
+// per row). With a fused RMSNorm every workgroup also reads the norm weights,
+// so a vocabulary-sized matrix of short rows (the LM head) takes eight rows per
+// workgroup: 256000 x 2048 runs in 158.8 us instead of 197.7. Small M keeps
+// enough workgroups to fill the GPU.
+void pick_tiling(int M, int nch, bool q8, bool x_half, bool norm, int& nr, int& nw) {
     if (nch > 8) {
         nw = 8;
         nr = q8 ? 8 : 4;
     } else {
         nw = nch >= 4 ? 4 : nch >= 2 ? 2 : 1;
         nr = q8 ? 8 : x_half ? 2 : 4;
+        if (norm && M >= 65536) nr = 8;
     }
     if (M < 1024) nr = M >= 256 ? (nr < 2 ? nr : 2) : 1;
     nr = mxd::tunable("MV_NR", nr);
@@ -686,7 +690,7 @@ int launch(const GemvArgs& a, hipStream_t s) {
         return launch_sweep<WF, XT, NMAT, OP>(a, nw, cpw, wg_per_cu, s);
     }
     int nr, nw;
-    pick_tiling(a.M, nch, WF == MXD_W_Q8B32, sizeof(XT) == 2, nr, nw);
+    pick_tiling(a.M, nch, WF == MXD_W_Q8B32, sizeof(XT) == 2, a.nw != nullptr, nr, nw);
     switch (nr) {
         case 1: return launch_nw<WF, XT, NMAT, OP, 1>(a, nw, s);
         case 2: return launch_nw<WF, XT, NMAT, OP, 2>(a, nw, s);
@@ -850,7 +854,7 @@ extern "C" int mxd_qkv_rope_kv(const uint16_t* Wqkv, const float* x, const float
     a.hd = head_dim;
     a.max_ctx = max_ctx;
     int nr, nw;
-    pick_tiling(M, (K + 511) / 512, false, false, nr, nw);
+    pick_tiling(M, (K + 511) / 512, false, false, false, nr, nw);
     nr = nr < 2 ? 2 : (nr & ~1);  // rotation pairs stay inside one workgroup
     hipStream_t s = mxd::as_stream(stream);
     switch (nr) {
