@@ -96,6 +96,16 @@ class Engine:
             out.append((name.value.decode(), ptr.value, nb.value))
         return out
 
+    def tensor_specs(self) -> list[tuple[str, int, type]]:
+        """(name, bytes, numpy dtype) of every weight tensor, in engine order."""
+        out = []
+        for i in range(self._lib.mxd_engine_num_tensors(self._h)):
+            name, ptr, nb, dt = ctypes.c_char_p(), ctypes.c_void_p(), ctypes.c_size_t(), ctypes.c_int()
+            call("mxd_engine_tensor", self._h, i, ctypes.byref(name), ctypes.byref(ptr), ctypes.byref(nb),
+                 ctypes.byref(dt))
+            out.append((name.value.decode(), nb.value, np.float16 if dt.value == _lib.MXD_F16 else np.float32))
+        return out
+
     def init_random(self, seed: int, std: float = 0.02) -> None:
         call("mxd_engine_init_random", self._h, seed, std)
 
