@@ -101,6 +101,7 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_rope_kv": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),
     "mxd_attention_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "mxd_attention": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, P, c_size_t, P]),
+    "mxd_attention_prefill": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P]),
     "mxd_argmax_workspace_size": (c_size_t, [c_int]),
     "mxd_argmax": (c_int, [P, P, c_int, c_int, P, c_size_t, P]),
     "mxd_rope_kv_paged": (c_int, [P, P, P, c_int, P, c_int, c_int, c_int, P, c_int, P, c_int, P]),
@@ -111,6 +112,10 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_gemm_q8b32": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
     "mxd_gemm_gate_up_q8b32_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "mxd_gemm_gate_up_q8b32": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
+    "mxd_gemm_f16_workspace_size": (c_size_t, [c_int, c_int, c_int]),
+    "mxd_gemm_f16": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
+    "mxd_gemm_gate_up_f16_workspace_size": (c_size_t, [c_int, c_int, c_int]),
+    "mxd_gemm_gate_up_f16": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
 }
 
 _lock = threading.Lock()

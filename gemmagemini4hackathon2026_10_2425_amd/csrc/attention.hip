@@ -404,6 +404,20 @@ __global__ void __launch_bounds__(W * 64) attn_split_kernel(AttnArgs a) {
     attn_split<HD, W, PF>(a, src, n_keys_of(a), a.n_splits, blockIdx.x, kvh, a.q, a.out, a.ws_o, a.ws_ml);
 }
 
+// Prefill: `rows` queries at positions pos0 .. pos0 + rows - 1 over the
+// contiguous cache (their keys and values already appended); query t sees
+// keys [0, pos0 + t] (a.n_keys = pos0 + 1). Grid (rows, n_kv): one workgroup
+// per (query, kv head), one split, so each writes its output rows directly;
+// the kv head's G query heads share every K/V tile as in decode.
+template <int HD, int W, bool PF>
+__global__ void __launch_bounds__(W * 64) attn_prefill_kernel(AttnArgs a) {
+    const int t = blockIdx.x, kvh = blockIdx.y;
+    const ContigKV<HD> src{a.k + (size_t)kvh * a.max_ctx * HD, a.v + (size_t)kvh * a.max_ctx * HD};
+    const int n = min(a.n_keys + t, a.max_ctx);
+    attn_split<HD, W, PF>(a, src, n, 1, 0, kvh, a.q + (size_t)t * a.q_stride, a.out + (size_t)t * a.out_stride,
+                          a.ws_o, a.ws_ml);
+}
+
 // Keys and splits of paged sequence seq (clamped so a bad length can never
 // address past its page-table row).
 __device__ __forceinline__ int paged_keys(const AttnArgs& a, int seq) {
@@ -865,6 +879,53 @@ size_t sk_workspace(int nw, int n_seqs, int n_heads, int n_kv, int hd) {
     return sk_slots(nw, n_seqs, n_kv) * G * (hd + 2) * sizeof(float) + ((size_t)n_seqs + 1) * sizeof(int32_t);
 }
 }  // namespace
+
+extern "C" int mxd_attention_prefill(const float* q, int q_stride, const uint16_t* kcache, const uint16_t* vcache,
+                                     float* out, int out_stride, int n_heads, int n_kv_heads, int head_dim,
+                                     int max_ctx, int pos0, int rows, float scale, mxd_stream_t stream) {
+    MXD_REQUIRE(q && kcache && vcache && out, MXD_ERR_INVALID_ARG, "mxd_attention_prefill: null pointer");
+    MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, MXD_ERR_INVALID_ARG,
+                "mxd_attention_prefill: n_heads=%d must be a positive multiple of n_kv_heads=%d", n_heads, n_kv_heads);
+    const int G = n_heads / n_kv_heads;
+    MXD_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_prefill: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", G);
+    MXD_REQUIRE(head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_prefill: head_dim %d (128 or 256)", head_dim);
+    MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_prefill: max_ctx=%d must be a positive multiple of 32", max_ctx);
+    MXD_REQUIRE(rows >= 1 && pos0 >= 0 && (long long)pos0 + rows <= max_ctx, MXD_ERR_INVALID_ARG,
+                "mxd_attention_prefill: positions [%d, %d + %d) outside [0, max_ctx=%d)", pos0, pos0, rows, max_ctx);
+    MXD_REQUIRE(q_stride >= n_heads * head_dim && out_stride >= n_heads * head_dim && q_stride % 4 == 0,
+                MXD_ERR_INVALID_ARG, "mxd_attention_prefill: q_stride=%d out_stride=%d below n_heads * head_dim = %d "
+                "(q_stride a multiple of 4)", q_stride, out_stride, n_heads * head_dim);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kcache) |
+                         reinterpret_cast<uintptr_t>(vcache);
+    MXD_REQUIRE((al & 15) == 0, MXD_ERR_UNSUPPORTED, "mxd_attention_prefill: q, kcache, vcache must be 16-byte aligned");
+    AttnArgs a;
+    a.q = q;
+    a.k = kcache;
+    a.v = vcache;
+    a.out = out;
+    a.ws_o = nullptr;
+    a.ws_ml = nullptr;
+    a.pos_dev = nullptr;
+    a.q_stride = q_stride;
+    a.out_stride = out_stride;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv_heads;
+    a.G = G;
+    a.max_ctx = max_ctx;
+    a.n_keys = pos0 + 1;
+    a.n_splits = 1;
+    a.qscale = scale * LOG2E;
+    hipStream_t s = mxd::as_stream(stream);
+    const dim3 grid(rows, n_kv_heads);
+    if (head_dim == 128)
+        hipLaunchKernelGGL((attn_prefill_kernel<128, ATT_WAVES, false>), grid, dim3(ATT_WAVES * 64), 0, s, a);
+    else
+        hipLaunchKernelGGL((attn_prefill_kernel<256, ATT_WAVES, false>), grid, dim3(ATT_WAVES * 64), 0, s, a);
+    return mxd::check_launch("mxd_attention_prefill");
+}
 
 extern "C" size_t mxd_attention_paged_workspace_size(int n_heads, int n_kv_heads, int head_dim, int n_seqs,
                                                      int max_keys) {

@@ -12,6 +12,14 @@
 // priority). A decode run replays one captured hipGraph per token; inside it
 // every kernel reads the step position from a device counter that the final
 // argmax advances, so the same graph serves every position.
+//
+// Prefill (prefill(n:useGemm:), KL/main.swift:357-372, 412-446) runs the
+// prompt in chunks of up to PREFILL_ROWS rows through the matrix-core
+// products, the causal multi-query attention and row-batched norm / RoPE /
+// cast kernels, with the reference's fp16 activation points; the last row of
+// the last chunk goes through the decode path's LM head and argmax. The
+// ENG_NO_GEMM tunable (the reference's --no-gemm) steps the decode path
+// instead.
 #include "internal.hpp"
 
 #include <math.h>
@@ -38,6 +46,8 @@ struct LayerPtrs {
 };
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+constexpr int PREFILL_ROWS = 256;  // prompt rows per prefill chunk
 
 #define HIP_OK(expr, what)                                                                         \
     do {                                                                                           \
@@ -69,6 +79,13 @@ struct mxd_engine {
     size_t attn_ws_bytes = 0;
     void* am_ws = nullptr;
     hipGraphExec_t graph = nullptr;
+    // prefill chunk buffers: rows x {dim f32, dim f16, qkv f32, q f32, q f16,
+    // ffn f32, ffn f16}, and the products' split-K workspace
+    int max_rows = 0;
+    float *bx = nullptr, *bqkv = nullptr, *batt = nullptr, *bh = nullptr;
+    uint16_t *bxn = nullptr, *batt16 = nullptr, *bh16 = nullptr;
+    void* gm_ws = nullptr;
+    size_t gm_ws_bytes = 0;
 
     int qkv_dim() const { return (c.n_heads + 2 * c.n_kv_heads) * c.head_dim; }
     int q_dim() const { return c.n_heads * c.head_dim; }
@@ -155,6 +172,58 @@ int encode_step(mxd_engine* e, int pos, int32_t* pos_dev, bool sample) {
     return mxd::argmax_dev(e->logits, e->tokens, V, pos + 1, pos_dev, pos_dev != nullptr, e->am_ws, s);
 }
 
+// The batched prefill of tokens[pos0 .. pos0 + T) (encodePrefillChunk,
+// KL/main.swift:412-446); with sample, tokens[pos0 + T] = argmax of the last
+// row's logits, which stay in e->logits.
+int encode_prefill(mxd_engine* e, int pos0, int T, bool sample) {
+    const mxd_model_config& c = e->c;
+    hipStream_t s = e->stream;
+    mxd_stream_t ms = reinterpret_cast<mxd_stream_t>(s);
+    const int D = c.dim, NH = c.n_heads, NKV = c.n_kv_heads, HD = c.head_dim, F = c.ffn_dim, V = c.vocab;
+    const int QKV = e->qkv_dim(), QD = e->q_dim();
+    const float escale = c.embed_scale_sqrt_dim ? sqrtf((float)D) : 1.0f;
+    const float ascale = 1.0f / sqrtf((float)HD);
+    void* ws = e->gm_ws;
+    const size_t wsb = e->gm_ws_bytes;
+    int rc;
+    if ((rc = mxd::embed_dev(e->embed, e->tokens, pos0, nullptr, T, e->bx, D, escale, V, s))) return rc;
+    for (int l = 0; l < c.n_layers; ++l) {
+        const LayerPtrs& Lp = e->L[l];
+        if ((rc = mxd_rmsnorm(e->bx, Lp.attn_norm, e->bxn, MXD_F16, T, D, c.rms_eps, c.norm_plus_one, ms))) return rc;
+        if ((rc = mxd_gemm_f16(Lp.wqkv, e->bxn, e->bqkv, T, QKV, D, MXD_EPI_STORE, ws, wsb, ms))) return rc;
+        if ((rc = mxd_rope_kv(e->bqkv, Lp.kc, Lp.vc, e->invf, NH, NKV, HD, e->max_ctx, pos0, T, ms))) return rc;
+        if ((rc = mxd_attention_prefill(e->bqkv, QKV, Lp.kc, Lp.vc, e->batt, QD, NH, NKV, HD, e->max_ctx, pos0, T,
+                                        ascale, ms)))
+            return rc;
+        if ((rc = mxd_f32_to_f16(e->batt, e->batt16, (size_t)T * QD, ms))) return rc;
+        if ((rc = mxd_gemm_f16(Lp.wo, e->batt16, e->bx, T, D, QD, MXD_EPI_ADD, ws, wsb, ms))) return rc;
+        if ((rc = mxd_rmsnorm(e->bx, Lp.ffn_norm, e->bxn, MXD_F16, T, D, c.rms_eps, c.norm_plus_one, ms))) return rc;
+        if ((rc = mxd_gemm_gate_up_f16(Lp.wgate, Lp.wup, e->bxn, e->bh, T, F, D, c.act, ws, wsb, ms))) return rc;
+        if ((rc = mxd_f32_to_f16(e->bh, e->bh16, (size_t)T * F, ms))) return rc;
+        if ((rc = mxd_gemm_f16(Lp.wdown, e->bh16, e->bx, T, D, F, MXD_EPI_ADD, ws, wsb, ms))) return rc;
+    }
+    if (!sample) return MXD_OK;
+    // Only the last row needs logits: it takes the decode path's head.
+    HIP_OK(hipMemcpyAsync(e->x, e->bx + (size_t)(T - 1) * D, (size_t)D * 4, hipMemcpyDeviceToDevice, s),
+           "mxd_engine_prefill");
+    if ((rc = mxd_matvec_f16_rmsnorm(e->embed, e->x, e->final_norm, c.rms_eps, c.norm_plus_one, e->logits, V, D,
+                                     MXD_EPI_STORE, nullptr, ms)))
+        return rc;
+    return mxd::argmax_dev(e->logits, e->tokens, V, pos0 + T, nullptr, false, e->am_ws, s);
+}
+
+// Split-K workspace the prefill products may need for any chunk of 1 .. rows rows.
+size_t prefill_ws_bytes(const mxd_model_config& c, int qkv_dim, int q_dim, int rows) {
+    size_t m = 0;
+    for (int T = 1; T <= rows; ++T) {
+        m = max(m, mxd_gemm_f16_workspace_size(T, qkv_dim, c.dim));
+        m = max(m, mxd_gemm_f16_workspace_size(T, c.dim, q_dim));
+        m = max(m, mxd_gemm_gate_up_f16_workspace_size(T, c.ffn_dim, c.dim));
+        m = max(m, mxd_gemm_f16_workspace_size(T, c.dim, c.ffn_dim));
+    }
+    return m;
+}
+
 int check_config(const mxd_model_config* c, int max_ctx) {
     MXD_REQUIRE(c, MXD_ERR_INVALID_ARG, "mxd_engine_create: null config");
     MXD_REQUIRE(c->n_layers > 0 && c->dim > 0 && c->n_heads > 0 && c->n_kv_heads > 0 && c->head_dim > 0 &&
@@ -198,6 +267,11 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
     const size_t o_att = take((size_t)e->q_dim() * 4), o_h = take(F * 4), o_logits = take((size_t)c.vocab * 4);
     const size_t o_invf = take((size_t)c.head_dim / 2 * 4), o_tok = take(((size_t)max_ctx + 1) * 4), o_pos = take(4);
     const size_t o_aws = take(e->attn_ws_bytes), o_am = take(mxd_argmax_workspace_size(c.vocab));
+    const size_t B = (size_t)(e->max_rows = min(PREFILL_ROWS, max_ctx));
+    e->gm_ws_bytes = prefill_ws_bytes(c, e->qkv_dim(), e->q_dim(), e->max_rows);
+    const size_t o_bx = take(B * D * 4), o_bxn = take(B * D * 2), o_bqkv = take(B * e->qkv_dim() * 4);
+    const size_t o_batt = take(B * e->q_dim() * 4), o_batt16 = take(B * e->q_dim() * 2);
+    const size_t o_bh = take(B * F * 4), o_bh16 = take(B * F * 2), o_gws = take(max(e->gm_ws_bytes, (size_t)16));
     std::vector<size_t> o_kc(c.n_layers), o_vc(c.n_layers);
     for (int l = 0; l < c.n_layers; ++l) {
         o_kc[l] = take(kv_bytes);
@@ -224,6 +298,14 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
     e->pos = reinterpret_cast<int32_t*>(a + o_pos);
     e->attn_ws = a + o_aws;
     e->am_ws = a + o_am;
+    e->bx = reinterpret_cast<float*>(a + o_bx);
+    e->bxn = reinterpret_cast<uint16_t*>(a + o_bxn);
+    e->bqkv = reinterpret_cast<float*>(a + o_bqkv);
+    e->batt = reinterpret_cast<float*>(a + o_batt);
+    e->batt16 = reinterpret_cast<uint16_t*>(a + o_batt16);
+    e->bh = reinterpret_cast<float*>(a + o_bh);
+    e->bh16 = reinterpret_cast<uint16_t*>(a + o_bh16);
+    e->gm_ws = a + o_gws;
     e->embed = wptr<uint16_t>(e, "embed");
     e->final_norm = wptr<float>(e, "final_norm");
     e->L.resize(c.n_layers);
@@ -359,6 +441,14 @@ extern "C" int mxd_engine_step(mxd_engine* e, int pos, int sample) {
 
 extern "C" int mxd_engine_prefill(mxd_engine* e, int n) {
     MXD_REQUIRE(e && n >= 1 && n <= e->max_ctx, MXD_ERR_INVALID_ARG, "mxd_engine_prefill: n=%d", n);
+    if (n > 1 && mxd::tunable("ENG_NO_GEMM", 0) != 1) {
+        for (int done = 0; done < n;) {
+            const int rows = min(e->max_rows, n - done);
+            if (int rc = encode_prefill(e, done, rows, done + rows == n)) return rc;
+            done += rows;
+        }
+        return MXD_OK;
+    }
     for (int p = 0; p < n; ++p)
         if (int rc = encode_step(e, p, nullptr, p == n - 1)) return rc;
     return MXD_OK;

@@ -51,13 +51,30 @@ constexpr int GM2_XP = GM2_CK + 8;      // LDS pitch in halfs of the runtime-loo
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 struct GemmArgs {
-    const int8_t* W[2];
+    const int8_t* W[2];  // int8 [M][K], or fp16 [M][K] (MXD_W_F16) through the same pointer
     const uint16_t* S[2];
     const uint16_t* X;  // fp16 [n_rows][K]
     float* Y;           // fp32 [n_rows][M]
     float* part;        // fp32 [splits][n_rows][NMAT][M] when splits > 1
     int n_rows, M, K, splits;
+    int row_tiles, batch_tiles;  // weight-row tiles of GM_ROWS / NMAT, activation tiles of GM_BATCH
 };
+
+// XCD-aware tile order on a 1-D grid. Workgroup L runs on XCD L % 8 (the
+// 8 XCDs take workgroups round-robin); the batch tiles of one (row tile,
+// split) pair take consecutive slots of one XCD, so a weight tile streamed
+// from HBM once is re-read from that XCD's L2 by the pair's other batch
+// tiles, which run at the same time. The grid is rounded up to whole groups
+// of 8 pairs; a workgroup past the last pair returns before any barrier.
+__device__ __forceinline__ bool gemm_tile(const GemmArgs& a, int& split, int& rt, int& bz) {
+    const int L = blockIdx.x, rest = L >> 3;
+    bz = rest % a.batch_tiles;
+    const int pair = (rest / a.batch_tiles) * 8 + (L & 7);
+    if (pair >= a.row_tiles * a.splits) return false;
+    rt = pair / a.splits;
+    split = pair - rt * a.splits;
+    return true;
+}
 
 template <int NMAT, int OP>
 __device__ __forceinline__ float epilogue(float g, float u, float old) {
@@ -90,8 +107,10 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_loop_kernel(GemmArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int mc = lane & 31, h = lane >> 5;
     const int m = wave / WPM;  // which matrix this wave reads
-    const int row0 = blockIdx.y * ROWS + 32 * (wave % WPM);
-    const int split = blockIdx.x, b0 = blockIdx.z * GM_BATCH;
+    int split, rt, bz;
+    if (!gemm_tile(a, split, rt, bz)) return;
+    const int row0 = rt * ROWS + 32 * (wave % WPM);
+    const int b0 = bz * GM_BATCH;
     const int M = a.M, K = a.K;
     const int nck = K / GM2_CK;
     const int c0 = split * nck / a.splits, c1 = (split + 1) * nck / a.splits;  // this split's chunks
@@ -262,9 +281,14 @@ __device__ __forceinline__ void static_for(F&& f) {
     }
 }
 
-// The default kernel: NCH chunks per workgroup, fully unrolled.
-template <int NMAT, int OP, int NCH>
-__global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
+// The default kernel: NCH chunks per workgroup, fully unrolled. WF selects
+// the weights: int8 block-32 (a lane's 16-byte load is half a block, dequantised
+// and scaled per block) or fp16 (a lane's 16 k of a block are 32 contiguous
+// bytes, two 16-byte loads that are the MFMA operands as they stand; products
+// accumulate in the MFMA accumulators). The k order, the activation side and
+// the epilogues are the same for both.
+template <int WF, int NMAT, int OP, int NCH>
+__global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
     constexpr int WAVES = GM_WAVES, NT = GM_THREADS;
     constexpr int WPM = WAVES / NMAT;
     constexpr int ROWS = 32 * WPM;
@@ -274,19 +298,24 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) _Float16 xs[2][GM_BATCH][GM2_CK];
     // the split's scales of each wave's 32 rows: [wave][row][NCH * 4 (+8 pad,
     // keeping every row 16-byte aligned for the 16-byte stores below)]
-    constexpr int SP = NCH * 4 + 8;
+    constexpr bool Q8 = WF == MXD_W_Q8B32;
+    constexpr int SP = Q8 ? NCH * 4 + 8 : 8;
     __shared__ __attribute__((aligned(16))) uint16_t ss[WAVES][32][SP];
+    constexpr int ESZ = Q8 ? 1 : 2;  // bytes per weight
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int mc = lane & 31, h = lane >> 5;
     const int m = wave / WPM;
-    const int row0 = blockIdx.y * ROWS + 32 * (wave % WPM);
-    const int split = blockIdx.x, b0 = blockIdx.z * GM_BATCH;
+    int split, rt, bz;
+    if (!gemm_tile(a, split, rt, bz)) return;
+    const int row0 = rt * ROWS + 32 * (wave % WPM);
+    const int b0 = bz * GM_BATCH;
     const int M = a.M, K = a.K;
     const int c0 = split * NCH;  // a.splits * NCH == K / GM2_CK
 
     const int wrow = min(row0 + mc, M - 1);
-    const int8_t* wp = a.W[m] + (size_t)wrow * K + (size_t)c0 * GM2_CK + 16 * h;
+    const unsigned char* wp =
+        reinterpret_cast<const unsigned char*>(a.W[m]) + ((size_t)wrow * K + (size_t)c0 * GM2_CK + 16 * h) * ESZ;
     const uint16_t* xbase = a.X + (size_t)c0 * GM2_CK;
 
     // Activations of chunk ci: thread t loads pieces t + NT u (row p / 16,
@@ -310,15 +339,19 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
             *reinterpret_cast<u4_t*>(&xs[ci & 1][r][8 * (q ^ (r & 15))]) = xv[ci & 1][u];
         }
     };
-    u4_t wr[2][4];
+    // Block j of chunk ci: ESZ 16-byte pieces per lane.
+    u4_t wr[2][4 * ESZ];
     auto load_w = [&](int ci, int j) {
-        wr[ci & 1][j] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wp + (size_t)ci * GM2_CK + 32 * j));
+#pragma unroll
+        for (int e = 0; e < ESZ; ++e)
+            wr[ci & 1][ESZ * j + e] = __builtin_nontemporal_load(
+                reinterpret_cast<const u4_t*>(wp + ((size_t)ci * GM2_CK + 32 * j) * ESZ + 16 * e));
     };
-    // Scales first: lane l fetches row l / 2's half (l & 1) of the split's
-    // NCH * 4 scales (NCH * 4 bytes) in 16-byte pieces.
-    constexpr int SPL = NCH * 4 / 2 / 8;  // 16-byte pieces per lane
+    // int8: scales first; lane l fetches row l / 2's half (l & 1) of the
+    // split's NCH * 4 scales (NCH * 4 bytes) in 16-byte pieces.
+    constexpr int SPL = Q8 ? NCH * 4 / 2 / 8 : 1;  // 16-byte pieces per lane
     u4_t sv[SPL];
-    {
+    if constexpr (Q8) {
         const uint16_t* srow = a.S[m] + (size_t)min(row0 + (lane >> 1), M - 1) * (K / 32) + (size_t)c0 * 4 +
                                (lane & 1) * (NCH * 2);
 #pragma unroll
@@ -333,9 +366,11 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) load_w(1, j);
     }
+    if constexpr (Q8) {
 #pragma unroll
-    for (int u = 0; u < SPL; ++u)
-        *reinterpret_cast<u4_t*>(&ss[wave][lane >> 1][(lane & 1) * (NCH * 2) + 8 * u]) = sv[u];
+        for (int u = 0; u < SPL; ++u)
+            *reinterpret_cast<u4_t*>(&ss[wave][lane >> 1][(lane & 1) * (NCH * 2) + 8 * u]) = sv[u];
+    }
     store_x(ic<0>{});
     __syncthreads();
     f32x16_t acc[2];
@@ -350,7 +385,7 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
         constexpr int par = ci & 1;
         const _Float16(*xcur)[GM2_CK] = xs[par];
         float sc[4];
-        {
+        if constexpr (Q8) {
             const u2_t sv2 = *reinterpret_cast<const u2_t*>(&ss[wave][mc][4 * ci]);
             sc[0] = mxd::h2f((uint16_t)(sv2.x & 0xFFFFu));
             sc[1] = mxd::h2f((uint16_t)(sv2.x >> 16));
@@ -362,8 +397,15 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const u4_t w = wr[par][j];
-            const h8_t w0 = q8x8_to_h8(w.x, w.y), w1 = q8x8_to_h8(w.z, w.w);
+            h8_t w0, w1;
+            if constexpr (Q8) {
+                const u4_t w = wr[par][j];
+                w0 = q8x8_to_h8(w.x, w.y);
+                w1 = q8x8_to_h8(w.z, w.w);
+            } else {
+                __builtin_memcpy(&w0, &wr[par][2 * j], 16);
+                __builtin_memcpy(&w1, &wr[par][2 * j + 1], 16);
+            }
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (ci + 2 < NCH) load_w(ci + 2, j);
             __builtin_amdgcn_sched_barrier(0);
@@ -372,14 +414,21 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_kernel(GemmArgs a) {
             const h8_t x01 = *reinterpret_cast<const h8_t*>(&xcur[mc][8 * ((p0 + 1) ^ sw)]);
             const h8_t x10 = *reinterpret_cast<const h8_t*>(&xcur[32 + mc][8 * (p0 ^ sw)]);
             const h8_t x11 = *reinterpret_cast<const h8_t*>(&xcur[32 + mc][8 * ((p0 + 1) ^ sw)]);
-            f32x16_t t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x00, w0, zero, 0, 0, 0);
-            f32x16_t t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, zero, 0, 0, 0);
-            t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, t0, 0, 0, 0);
-            t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, t1, 0, 0, 0);
+            if constexpr (Q8) {
+                f32x16_t t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x00, w0, zero, 0, 0, 0);
+                f32x16_t t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, zero, 0, 0, 0);
+                t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, t0, 0, 0, 0);
+                t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, t1, 0, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                acc[0][r] = fmaf(sc[j], t0[r], acc[0][r]);
-                acc[1][r] = fmaf(sc[j], t1[r], acc[1][r]);
+                for (int r = 0; r < 16; ++r) {
+                    acc[0][r] = fmaf(sc[j], t0[r], acc[0][r]);
+                    acc[1][r] = fmaf(sc[j], t1[r], acc[1][r]);
+                }
+            } else {
+                acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x00, w0, acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, acc[1], 0, 0, 0);
+                acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, acc[1], 0, 0, 0);
             }
             asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
         }
@@ -454,8 +503,11 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a) {
     }
 }
 
-bool use_mfma(int n_rows, int K) {
-    return n_rows >= mxd::tunable("GM_MIN_ROWS", 16) && K % GM2_CK == 0;
+// int8 weights need whole 128-k chunks (the runtime loop takes any count);
+// fp16 weights run only the unrolled kernel, so K must split into chunks of
+// at least 4 (K % 512 == 0).
+bool use_mfma(int wf, int n_rows, int K) {
+    return n_rows >= mxd::tunable("GM_MIN_ROWS", 16) && K % (wf == MXD_W_F16 ? 4 * GM2_CK : GM2_CK) == 0;
 }
 
 // Chunks per workgroup of the unrolled kernel: the largest of 32, 16, 8, 4
@@ -464,12 +516,14 @@ bool use_mfma(int n_rows, int K) {
 // loop; 0 (the runtime loop) when none divides. Fewer, longer splits also save
 // the partials and their reduction (gate/up at 64 rows: 62.2 us with one split
 // of 32 chunks against 65.1 us with two of 16).
-int pick_nch(int n_rows, int M, int K, int nmat) {
+int pick_nch(int wf, int n_rows, int M, int K, int nmat) {
     const int nck = K / GM2_CK;
     const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + GM_BATCH - 1) / GM_BATCH);
     const int forced = mxd::tunable("GM_NCH", 0);
-    if (forced == 1) return 0;
-    if (forced == 4 || forced == 8 || forced == 16 || forced == 32) return nck % forced == 0 ? forced : 0;
+    const bool loop_ok = wf == MXD_W_Q8B32;  // the runtime-loop kernel is int8 only
+    if (forced == 1 && loop_ok) return 0;
+    if ((forced == 4 || forced == 8 || forced == 16 || forced == 32) && (nck % forced == 0 || loop_ok))
+        return nck % forced == 0 ? forced : 0;
     int best = 0;
     for (int nch : {32, 16, 8, 4}) {
         if (nck % nch) continue;
@@ -483,34 +537,44 @@ int pick_nch(int n_rows, int M, int K, int nmat) {
 // K splits: nck / NCH for the unrolled kernel; for the runtime loop about two
 // workgroups per CU, at most one split per chunk. GM_SPLITS overrides the
 // latter.
-int pick_splits(int n_rows, int M, int K, int nmat) {
-    const int nch = pick_nch(n_rows, M, K, nmat);
+int pick_splits(int wf, int n_rows, int M, int K, int nmat) {
+    const int nch = pick_nch(wf, n_rows, M, K, nmat);
     if (nch) return (K / GM2_CK) / nch;
     const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + GM_BATCH - 1) / GM_BATCH);
     const int s = mxd::tunable("GM_SPLITS", (512 + tiles - 1) / tiles);
     return max(1, min(s, K / GM2_CK));
 }
 
-size_t ws_bytes_for(int n_rows, int M, int K, int nmat) {
-    if (n_rows <= 0 || M <= 0 || K <= 0 || !use_mfma(n_rows, K)) return 0;
-    const int s = pick_splits(n_rows, M, K, nmat);
+size_t ws_bytes_for(int wf, int n_rows, int M, int K, int nmat) {
+    if (n_rows <= 0 || M <= 0 || K <= 0 || !use_mfma(wf, n_rows, K)) return 0;
+    const int s = pick_splits(wf, n_rows, M, K, nmat);
     return s > 1 ? (size_t)s * n_rows * nmat * M * sizeof(float) : 0;
 }
 
-template <int NMAT, int OP>
+template <int WF, int NMAT, int OP>
 int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char* fn) {
-    a.splits = pick_splits(a.n_rows, a.M, a.K, NMAT);
+    a.splits = pick_splits(WF, a.n_rows, a.M, a.K, NMAT);
     const size_t need = a.splits > 1 ? (size_t)a.splits * a.n_rows * NMAT * a.M * sizeof(float) : 0;
     MXD_REQUIRE(need == 0 || (ws && ws_bytes >= need), MXD_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)",
                 fn, need, ws_bytes);
     a.part = static_cast<float*>(ws);
-    const dim3 grid(a.splits, (a.M + GM_ROWS / NMAT - 1) / (GM_ROWS / NMAT), (a.n_rows + GM_BATCH - 1) / GM_BATCH);
-    switch (pick_nch(a.n_rows, a.M, a.K, NMAT)) {
-        case 4: hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP, 4>), grid, dim3(GM_THREADS), 0, s, a); break;
-        case 8: hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP, 8>), grid, dim3(GM_THREADS), 0, s, a); break;
-        case 16: hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP, 16>), grid, dim3(GM_THREADS), 0, s, a); break;
-        case 32: hipLaunchKernelGGL((gemm_q8_kernel<NMAT, OP, 32>), grid, dim3(GM_THREADS), 0, s, a); break;
-        default: hipLaunchKernelGGL((gemm_q8_loop_kernel<NMAT, OP>), grid, dim3(GM_THREADS), 0, s, a); break;
+    a.row_tiles = (a.M + GM_ROWS / NMAT - 1) / (GM_ROWS / NMAT);
+    a.batch_tiles = (a.n_rows + GM_BATCH - 1) / GM_BATCH;
+    const int pairs = a.row_tiles * a.splits;
+    const dim3 grid((unsigned)((pairs + 7) / 8 * 8 * a.batch_tiles));  // see gemm_tile
+    const int nch = pick_nch(WF, a.n_rows, a.M, a.K, NMAT);
+    switch (nch) {
+        case 4: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 4>), grid, dim3(GM_THREADS), 0, s, a); break;
+        case 8: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 8>), grid, dim3(GM_THREADS), 0, s, a); break;
+        case 16: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 16>), grid, dim3(GM_THREADS), 0, s, a); break;
+        case 32: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 32>), grid, dim3(GM_THREADS), 0, s, a); break;
+        default:
+            if constexpr (WF == MXD_W_Q8B32) {
+                hipLaunchKernelGGL((gemm_q8_loop_kernel<NMAT, OP>), grid, dim3(GM_THREADS), 0, s, a);
+            } else {
+                return mxd::fail(MXD_ERR_UNSUPPORTED, "%s: K=%d has no chunk count for fp16 weights", fn, a.K);
+            }
+            break;
     }
     if (a.splits > 1) {
         const size_t n = (size_t)a.n_rows * a.M;
@@ -534,10 +598,20 @@ int check_common(const void* W, const void* S, const void* X, const void* Y, int
 
 }  // namespace
 
-extern "C" size_t mxd_gemm_q8b32_workspace_size(int n_rows, int M, int K) { return ws_bytes_for(n_rows, M, K, 1); }
+extern "C" size_t mxd_gemm_q8b32_workspace_size(int n_rows, int M, int K) {
+    return ws_bytes_for(MXD_W_Q8B32, n_rows, M, K, 1);
+}
 
 extern "C" size_t mxd_gemm_gate_up_q8b32_workspace_size(int n_rows, int F, int K) {
-    return ws_bytes_for(n_rows, F, K, 2);
+    return ws_bytes_for(MXD_W_Q8B32, n_rows, F, K, 2);
+}
+
+extern "C" size_t mxd_gemm_f16_workspace_size(int n_rows, int M, int K) {
+    return ws_bytes_for(MXD_W_F16, n_rows, M, K, 1);
+}
+
+extern "C" size_t mxd_gemm_gate_up_f16_workspace_size(int n_rows, int F, int K) {
+    return ws_bytes_for(MXD_W_F16, n_rows, F, K, 2);
 }
 
 extern "C" int mxd_gemm_q8b32(const int8_t* Wq, const uint16_t* scales, const uint16_t* X, float* Y, int n_rows, int M,
@@ -545,7 +619,7 @@ extern "C" int mxd_gemm_q8b32(const int8_t* Wq, const uint16_t* scales, const ui
     if (int rc = check_common(Wq, scales, X, Y, n_rows, M, K, "mxd_gemm_q8b32")) return rc;
     MXD_REQUIRE(epilogue == MXD_EPI_STORE || epilogue == MXD_EPI_ADD, MXD_ERR_INVALID_ARG,
                 "mxd_gemm_q8b32: epilogue %d (store or add)", epilogue);
-    if (!use_mfma(n_rows, K)) {  // few rows: one matvec per row
+    if (!use_mfma(MXD_W_Q8B32, n_rows, K)) {  // few rows: one matvec per row
         for (int b = 0; b < n_rows; ++b) {
             if (int rc = mxd_matvec_q8b32(Wq, scales, X + (size_t)b * K, MXD_F16, Y + (size_t)b * M, M, K, epilogue,
                                           nullptr, stream))
@@ -562,8 +636,9 @@ extern "C" int mxd_gemm_q8b32(const int8_t* Wq, const uint16_t* scales, const ui
     a.M = M;
     a.K = K;
     hipStream_t s = mxd::as_stream(stream);
-    if (epilogue == MXD_EPI_ADD) return launch_gemm<1, MXD_EPI_ADD>(a, workspace, ws_bytes, s, "mxd_gemm_q8b32");
-    return launch_gemm<1, MXD_EPI_STORE>(a, workspace, ws_bytes, s, "mxd_gemm_q8b32");
+    if (epilogue == MXD_EPI_ADD)
+        return launch_gemm<MXD_W_Q8B32, 1, MXD_EPI_ADD>(a, workspace, ws_bytes, s, "mxd_gemm_q8b32");
+    return launch_gemm<MXD_W_Q8B32, 1, MXD_EPI_STORE>(a, workspace, ws_bytes, s, "mxd_gemm_q8b32");
 }
 
 extern "C" int mxd_gemm_gate_up_q8b32(const int8_t* Wg, const uint16_t* sg, const int8_t* Wu, const uint16_t* su,
@@ -573,7 +648,7 @@ extern "C" int mxd_gemm_gate_up_q8b32(const int8_t* Wg, const uint16_t* sg, cons
     if (int rc = check_common(Wu, su, X, H, n_rows, F, K, "mxd_gemm_gate_up_q8b32")) return rc;
     MXD_REQUIRE(act == MXD_ACT_GELU_TANH || act == MXD_ACT_SILU, MXD_ERR_INVALID_ARG,
                 "mxd_gemm_gate_up_q8b32: unknown activation %d", act);
-    if (!use_mfma(n_rows, K)) {
+    if (!use_mfma(MXD_W_Q8B32, n_rows, K)) {
         for (int b = 0; b < n_rows; ++b) {
             if (int rc = mxd_matvec_gate_up(MXD_W_Q8B32, Wg, sg, Wu, su, X + (size_t)b * K, MXD_F16, H + (size_t)b * F,
                                             F, K, act, stream))
@@ -593,6 +668,73 @@ extern "C" int mxd_gemm_gate_up_q8b32(const int8_t* Wg, const uint16_t* sg, cons
     a.K = K;
     hipStream_t s = mxd::as_stream(stream);
     if (act == MXD_ACT_SILU)
-        return launch_gemm<2, MXD_ACT_SILU>(a, workspace, ws_bytes, s, "mxd_gemm_gate_up_q8b32");
-    return launch_gemm<2, MXD_ACT_GELU_TANH>(a, workspace, ws_bytes, s, "mxd_gemm_gate_up_q8b32");
+        return launch_gemm<MXD_W_Q8B32, 2, MXD_ACT_SILU>(a, workspace, ws_bytes, s, "mxd_gemm_gate_up_q8b32");
+    return launch_gemm<MXD_W_Q8B32, 2, MXD_ACT_GELU_TANH>(a, workspace, ws_bytes, s, "mxd_gemm_gate_up_q8b32");
+}
+
+namespace {
+
+int check_f16(const void* W, const void* X, const void* Y, int n_rows, int M, int K, const char* fn) {
+    MXD_REQUIRE(W && X && Y, MXD_ERR_INVALID_ARG, "%s: null pointer", fn);
+    MXD_REQUIRE(n_rows > 0 && M > 0 && K > 0, MXD_ERR_INVALID_ARG, "%s: n_rows=%d M=%d K=%d must be positive", fn,
+                n_rows, M, K);
+    MXD_REQUIRE(K % 8 == 0, MXD_ERR_INVALID_ARG, "%s: K=%d must be a multiple of 8", fn, K);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(X);
+    MXD_REQUIRE((al & 15) == 0, MXD_ERR_UNSUPPORTED, "%s: W and X must be 16-byte aligned", fn);
+    return MXD_OK;
+}
+
+}  // namespace
+
+extern "C" int mxd_gemm_f16(const uint16_t* W, const uint16_t* X, float* Y, int n_rows, int M, int K, int epilogue,
+                            void* workspace, size_t ws_bytes, mxd_stream_t stream) {
+    if (int rc = check_f16(W, X, Y, n_rows, M, K, "mxd_gemm_f16")) return rc;
+    MXD_REQUIRE(epilogue == MXD_EPI_STORE || epilogue == MXD_EPI_ADD, MXD_ERR_INVALID_ARG,
+                "mxd_gemm_f16: epilogue %d (store or add)", epilogue);
+    if (!use_mfma(MXD_W_F16, n_rows, K)) {  // few rows or K % 512: one matvec per row
+        for (int b = 0; b < n_rows; ++b) {
+            if (int rc = mxd_matvec_f16(W, X + (size_t)b * K, MXD_F16, Y + (size_t)b * M, M, K, epilogue, nullptr,
+                                        stream))
+                return rc;
+        }
+        return MXD_OK;
+    }
+    GemmArgs a{};
+    a.W[0] = a.W[1] = reinterpret_cast<const int8_t*>(W);
+    a.X = X;
+    a.Y = Y;
+    a.n_rows = n_rows;
+    a.M = M;
+    a.K = K;
+    hipStream_t s = mxd::as_stream(stream);
+    if (epilogue == MXD_EPI_ADD) return launch_gemm<MXD_W_F16, 1, MXD_EPI_ADD>(a, workspace, ws_bytes, s, "mxd_gemm_f16");
+    return launch_gemm<MXD_W_F16, 1, MXD_EPI_STORE>(a, workspace, ws_bytes, s, "mxd_gemm_f16");
+}
+
+extern "C" int mxd_gemm_gate_up_f16(const uint16_t* Wg, const uint16_t* Wu, const uint16_t* X, float* H, int n_rows,
+                                    int F, int K, int act, void* workspace, size_t ws_bytes, mxd_stream_t stream) {
+    if (int rc = check_f16(Wg, X, H, n_rows, F, K, "mxd_gemm_gate_up_f16")) return rc;
+    if (int rc = check_f16(Wu, X, H, n_rows, F, K, "mxd_gemm_gate_up_f16")) return rc;
+    MXD_REQUIRE(act == MXD_ACT_GELU_TANH || act == MXD_ACT_SILU, MXD_ERR_INVALID_ARG,
+                "mxd_gemm_gate_up_f16: unknown activation %d", act);
+    if (!use_mfma(MXD_W_F16, n_rows, K)) {
+        for (int b = 0; b < n_rows; ++b) {
+            if (int rc = mxd_matvec_gate_up(MXD_W_F16, Wg, nullptr, Wu, nullptr, X + (size_t)b * K, MXD_F16,
+                                            H + (size_t)b * F, F, K, act, stream))
+                return rc;
+        }
+        return MXD_OK;
+    }
+    GemmArgs a{};
+    a.W[0] = reinterpret_cast<const int8_t*>(Wg);
+    a.W[1] = reinterpret_cast<const int8_t*>(Wu);
+    a.X = X;
+    a.Y = H;
+    a.n_rows = n_rows;
+    a.M = F;
+    a.K = K;
+    hipStream_t s = mxd::as_stream(stream);
+    if (act == MXD_ACT_SILU)
+        return launch_gemm<MXD_W_F16, 2, MXD_ACT_SILU>(a, workspace, ws_bytes, s, "mxd_gemm_gate_up_f16");
+    return launch_gemm<MXD_W_F16, 2, MXD_ACT_GELU_TANH>(a, workspace, ws_bytes, s, "mxd_gemm_gate_up_f16");
 }

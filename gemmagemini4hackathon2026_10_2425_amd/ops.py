@@ -291,6 +291,75 @@ def attention(q, kcache, vcache, n_keys: int, n_heads: int, scale: float | None 
     return out
 
 
+def attention_prefill(q, kcache, vcache, pos0: int, n_heads: int, scale: float | None = None, out=None,
+                      q_stride: int | None = None, rows: int | None = None) -> torch.Tensor:
+    """Causal attention of a prefill chunk: row t of q (rows q_stride floats
+    apart; the q part of a qkv row [rows, qkv_dim] works in place) is the query
+    at position pos0 + t over keys [0, pos0 + t] of the tiled caches. Returns
+    out [rows, n_heads * hd]."""
+    _on_gpu(q, kcache, vcache)
+    n_kv, max_ctx, hd = _check_caches(kcache, vcache, "attention_prefill")
+    _need(q.dtype == torch.float32 and q.is_contiguous() and q.dim() == 2, "attention_prefill: q float32 [rows, stride]")
+    rows = q.shape[0] if rows is None else rows
+    q_stride = q.shape[1] if q_stride is None else q_stride
+    _need(q.numel() >= (rows - 1) * q_stride + n_heads * hd, "attention_prefill: q too small for rows x stride")
+    scale = 1.0 / math.sqrt(hd) if scale is None else scale
+    out = torch.empty((rows, n_heads * hd), dtype=torch.float32, device=q.device) if out is None else out
+    _need(out.dtype == torch.float32 and out.is_contiguous() and out.numel() == rows * n_heads * hd,
+          "attention_prefill: out float32 [rows, n_heads * hd]")
+    call("mxd_attention_prefill", _ptr(q), q_stride, _ptr(kcache), _ptr(vcache), _ptr(out), n_heads * hd, n_heads,
+         n_kv, hd, max_ctx, int(pos0), int(rows), float(scale), _stream())
+    return out
+
+
+def gemm_workspace(n_rows: int, M: int, K: int, glu: bool = False, device="cuda") -> torch.Tensor:
+    name = "mxd_gemm_gate_up_f16_workspace_size" if glu else "mxd_gemm_f16_workspace_size"
+    return torch.empty(max(query(name, n_rows, M, K), 16), dtype=torch.uint8, device=device)
+
+
+def gemm_f16(W, X, Y=None, epilogue: str = "store", workspace=None) -> torch.Tensor:
+    """Y[b] (op)= W . X[b]: fp16 W [M, K], X fp16 [B, K], Y fp32 [B, M]
+    (gemm_f16 / gemm_f16_add of the reference's prefill)."""
+    _on_gpu(W, X)
+    M, K = W.shape
+    _need(W.dtype == torch.float16 and W.is_contiguous(), "gemm_f16: W float16 [M, K]")
+    _need(X.dtype == torch.float16 and X.dim() == 2 and X.shape[1] == K and X.is_contiguous(),
+          "gemm_f16: X float16 [B, K]")
+    B = X.shape[0]
+    if Y is None:
+        _need(epilogue == "store", "gemm_f16: epilogue 'add' needs Y")
+        Y = torch.empty((B, M), dtype=torch.float32, device=X.device)
+    _need(Y.is_contiguous() and Y.dtype == torch.float32 and Y.numel() == B * M, "gemm_f16: Y float32 [B, M]")
+    if workspace is None:
+        workspace = gemm_workspace(B, M, K, False, X.device)
+    call("mxd_gemm_f16", _ptr(W), _ptr(X), _ptr(Y), B, M, K, _EPI[epilogue], _ptr(workspace), workspace.numel(),
+         _stream())
+    return Y
+
+
+def gemm_f16_add(W, X, Y, workspace=None) -> torch.Tensor:
+    return gemm_f16(W, X, Y, "add", workspace)
+
+
+def gemm_gate_up(Wg, Wu, X, act: str = "gelu_tanh", H=None, workspace=None) -> torch.Tensor:
+    """H[b] = act(Wg . X[b]) * (Wu . X[b]): fp16 Wg, Wu [F, K], X fp16 [B, K],
+    H fp32 [B, F] (gemm_gate_up_silu of the reference's prefill, and GeGLU)."""
+    _on_gpu(Wg, Wu, X)
+    F, K = Wg.shape
+    _need(Wg.dtype == torch.float16 and Wu.dtype == torch.float16 and tuple(Wu.shape) == (F, K),
+          "gemm_gate_up: Wg, Wu float16 [F, K]")
+    _need(X.dtype == torch.float16 and X.dim() == 2 and X.shape[1] == K and X.is_contiguous(),
+          "gemm_gate_up: X float16 [B, K]")
+    B = X.shape[0]
+    H = torch.empty((B, F), dtype=torch.float32, device=X.device) if H is None else H
+    _need(H.is_contiguous() and H.dtype == torch.float32 and H.numel() == B * F, "gemm_gate_up: H float32 [B, F]")
+    if workspace is None:
+        workspace = gemm_workspace(B, F, K, True, X.device)
+    call("mxd_gemm_gate_up_f16", _ptr(Wg), _ptr(Wu), _ptr(X), _ptr(H), B, F, K, _ACT[act], _ptr(workspace),
+         workspace.numel(), _stream())
+    return H
+
+
 def argmax_workspace(device="cuda") -> torch.Tensor:
     """Zeroed once here; the kernel leaves it zeroed after every call."""
     return torch.zeros(max(query("mxd_argmax_workspace_size", 0), 16), dtype=torch.uint8, device=device)

@@ -17,8 +17,9 @@ JSON-lines protocol, with the reference binary's flags and output formats
 Requests are sequential and each starts from position 0. EOF on stdin exits.
 
 --define NAME=VALUE sets a kernel tunable (mxd_set_tunable), the counterpart
-of the reference's Metal #defines. --no-gemm is accepted: prefill always runs
-token by token through the decode path here.
+of the reference's Metal #defines. Prefill runs the prompt in chunks through
+the matrix-core products; --no-gemm steps it token by token through the
+decode path instead (the ENG_NO_GEMM tunable).
 """
 
 from __future__ import annotations
@@ -197,6 +198,8 @@ def main(argv=None) -> int:
 
     for name, val in a.tunables.items():
         _lib.set_tunable(name, val)
+    if a.no_gemm:
+        _lib.set_tunable("ENG_NO_GEMM", 1)
     try:
         import torch
 
@@ -205,7 +208,8 @@ def main(argv=None) -> int:
         device = "HIP device"
     with load_engine(a.weights, a.max_ctx) as e:
         s = e.shape
-        sys.stderr.write(f"device: {device}, dim {s.dim}, layers {s.n_layers}, vocab {s.vocab}, gemm false\n")
+        sys.stderr.write(f"device: {device}, dim {s.dim}, layers {s.n_layers}, vocab {s.vocab}, "
+                         f"gemm {'false' if a.no_gemm else 'true'}\n")
         sys.stderr.flush()
         if a.ids:
             print(json.dumps(generate(e, a.ids, a.gen, a.max_ctx, a.dump_logits)), flush=True)

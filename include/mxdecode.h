@@ -181,6 +181,17 @@ int mxd_attention(const float* q, const uint16_t* kcache, const uint16_t* vcache
                   const int32_t* n_keys_dev, float scale, void* workspace, size_t ws_bytes,
                   mxd_stream_t stream);
 
+/* Causal attention of a prefill chunk: `rows` queries at positions pos0 ..
+ * pos0 + rows - 1 (their keys and values already in the caches), query t over
+ * keys [0, pos0 + t]. q rows are q_stride floats apart (a multiple of 4; the
+ * q part of a qkv row works in place), out rows out_stride. Same head dims,
+ * group sizes and cache layout as mxd_attention. Replaces attention with
+ * T > 1 (KL/kernels.metal:245-305: n = pos0 + t + 1, q_row_stride; host
+ * attention(enc, layer:, pos0:, rows:) in KL/main.swift:412-446). */
+int mxd_attention_prefill(const float* q, int q_stride, const uint16_t* kcache, const uint16_t* vcache,
+                          float* out, int out_stride, int n_heads, int n_kv_heads, int head_dim, int max_ctx,
+                          int pos0, int rows, float scale, mxd_stream_t stream);
+
 /* ---- greedy sample -------------------------------------------------------- */
 
 /* Workspace bytes mxd_argmax needs for N logits. */
@@ -258,6 +269,27 @@ size_t mxd_gemm_gate_up_q8b32_workspace_size(int n_rows, int F, int K);
 int mxd_gemm_gate_up_q8b32(const int8_t* Wg, const uint16_t* sg, const int8_t* Wu, const uint16_t* su,
                            const uint16_t* X, float* H, int n_rows, int F, int K, int act, void* workspace,
                            size_t ws_bytes, mxd_stream_t stream);
+
+/* Workspace bytes mxd_gemm_f16 needs (0 when it does not split K). */
+size_t mxd_gemm_f16_workspace_size(int n_rows, int M, int K);
+
+/* Y[b] (op)= W · X[b] for fp16 W [M][K] and the n_rows fp16 rows of X
+ * [n_rows][K]; Y fp32 [n_rows][M]; epilogue MXD_EPI_STORE or MXD_EPI_ADD; fp32
+ * accumulation. From 16 rows on (and K % 512 == 0) this runs on the matrix
+ * cores; below, one matvec per row. Replaces gemm_f16 / gemm_f16_add
+ * (KL/kernels.metal:376-441; host gemm KL/main.swift:397-410), the prefill
+ * products. */
+int mxd_gemm_f16(const uint16_t* W, const uint16_t* X, float* Y, int n_rows, int M, int K, int epilogue,
+                 void* workspace, size_t ws_bytes, mxd_stream_t stream);
+
+/* Workspace bytes mxd_gemm_gate_up_f16 needs (0 when it does not split K). */
+size_t mxd_gemm_gate_up_f16_workspace_size(int n_rows, int F, int K);
+
+/* H[b] = act(Wg · X[b]) ⊙ (Wu · X[b]) for fp16 Wg, Wu [F][K]; H fp32
+ * [n_rows][F]. Replaces gemm_gate_up_silu (KL/kernels.metal:445-510; host
+ * gemmGateUp KL/main.swift:412-446), with GeGLU as well. */
+int mxd_gemm_gate_up_f16(const uint16_t* Wg, const uint16_t* Wu, const uint16_t* X, float* H, int n_rows, int F,
+                         int K, int act, void* workspace, size_t ws_bytes, mxd_stream_t stream);
 
 /* ---- decode engine ---------------------------------------------------------- */
 

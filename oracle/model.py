@@ -120,6 +120,37 @@ class OracleDecoder:
         xn = ops.rmsnorm(x, w["final_norm"], c.eps, c.plus_one).astype(F32)
         return ops.matvec(w["embed"], xn).astype(F32)
 
+    def prefill_chunk(self, pos0: int, rows: int, sample: bool = True, half_acts: bool = True) -> np.ndarray | None:
+        """The batched prefill of tokens[pos0 .. pos0 + rows) (encodePrefillChunk,
+        KL/main.swift:412-446): per layer rmsnorm -> fp16 rows (xnHalf) -> qkv
+        product, RoPE + append per position, causal attention (query t over keys
+        [0, pos0 + t]), fp16(att) -> wo product added to x, rmsnorm -> fp16 ->
+        gate/up, fp16(h) -> down product added to x. With sample, the last row's
+        logits (final norm + tied head) are returned and their argmax written to
+        tokens[pos0 + rows]. half_acts=False skips the three fp16 roundings (then
+        every row equals forward() at its position)."""
+        c, w = self.cfg, self.w
+        F16 = np.float16 if half_acts else F32
+        scale = F32(math.sqrt(c.dim)) if c.gemma_embed_scale else F32(1.0)
+        X = np.stack([ops.embed(w["embed"], int(self.tokens[pos0 + t]), float(scale)) for t in range(rows)]).astype(F32)
+        att_scale = float(F32(1.0) / F32(math.sqrt(c.head_dim)))
+        for l in range(c.n_layers):
+            XN = ops.rmsnorm(X, w[f"l{l}.attn_norm"], c.eps, c.plus_one).astype(F32).astype(F16)
+            QKV = ops.matvec(w[f"l{l}.wqkv"], XN.T).T.astype(F32)
+            Q = np.stack([self._rope_kv(l, QKV[t], pos0 + t) for t in range(rows)]).astype(F32)
+            ATT = np.stack([ops.attention(Q[t], self.k[l], self.v[l], pos0 + t + 1, c.n_heads, att_scale)
+                            for t in range(rows)]).astype(F32)
+            X = (X + ops.matvec(w[f"l{l}.wo"], ATT.astype(F16).T).T.astype(F32)).astype(F32)
+            XN = ops.rmsnorm(X, w[f"l{l}.ffn_norm"], c.eps, c.plus_one).astype(F32).astype(F16)
+            H = ops.gate_up(w[f"l{l}.wgate"], w[f"l{l}.wup"], XN.T, c.act).T.astype(F32)
+            X = (X + ops.matvec(w[f"l{l}.wdown"], H.astype(F16).T).T.astype(F32)).astype(F32)
+        if not sample:
+            return None
+        xn = ops.rmsnorm(X[rows - 1], w["final_norm"], c.eps, c.plus_one).astype(F32)
+        logits = ops.matvec(w["embed"], xn).astype(F32)
+        self.tokens[pos0 + rows] = ops.argmax(logits)
+        return logits
+
     def step(self, pos: int, sample: bool = True) -> tuple[int, float]:
         """One decode step; with sample, tokens[pos + 1] = argmax. Returns (token,
         top-1 minus top-2 logit margin)."""
@@ -130,14 +161,26 @@ class OracleDecoder:
         top2 = np.partition(logits, -2)[-2:]
         return tok, float(top2[1] - top2[0])
 
-    def generate(self, prompt: list[int], n_new: int) -> tuple[list[int], list[float]]:
-        """Prefill token by token through the decode path (the reference's
-        --no-gemm prefill, KL/main.swift:367-368), then n_new - 1 more steps:
-        returns the n_new greedy tokens tokens[P .. P + n_new) and margins."""
+    def generate(self, prompt: list[int], n_new: int, prefill_rows: int | None = None) -> tuple[list[int], list[float]]:
+        """Prefill, then n_new - 1 more steps: returns the n_new greedy tokens
+        tokens[P .. P + n_new) and their top-2 margins. Prefill is token by token
+        through the decode path (the reference's --no-gemm prefill,
+        KL/main.swift:367-368) or, with prefill_rows and P > 1, batched in chunks
+        of that many rows (prefill(n:useGemm:), KL/main.swift:357-365)."""
         P = len(prompt)
         self.tokens[:P] = prompt
         margins = []
-        for pos in range(P + n_new - 1):
+        start = 0
+        if prefill_rows and P > 1:
+            done = 0
+            while done < P:
+                rows = min(prefill_rows, P - done)
+                lg = self.prefill_chunk(done, rows, sample=done + rows == P)
+                done += rows
+            top2 = np.partition(lg, -2)[-2:]
+            margins.append(float(top2[1] - top2[0]))
+            start = P
+        for pos in range(start, P + n_new - 1):
             _, m = self.step(pos, sample=pos >= P - 1)
             if pos >= P - 1:
                 margins.append(m)

@@ -74,13 +74,56 @@ def test_engine_steps_match_oracle(dev, cfg):
         assert e.tokens(0, n) == [int(t) for t in ref.tokens[:n]]
 
 
-@pytest.mark.parametrize("cfg", [SMALL, SMALL_GQA], ids=["gemma-mqa128", "llama-gqa"])
-def test_engine_generate_matches_oracle(dev, cfg):
-    seed, max_ctx = 9, 128
-    prompt = [int(t) for t in np.random.default_rng(4).integers(0, cfg.vocab, 33)]
-    toks_ref, margins = om.OracleDecoder(cfg, om.make_weights(cfg, seed), max_ctx).generate(prompt, 60)
+PREFILL_ROWS = 256  # the engine's prefill chunk
+
+
+@pytest.fixture(params=["batched", "tokenwise"])
+def prefill_mode(request):
+    """Batched prefill (default: matrix-core products, fp16 activation rows) or
+    token by token through the decode path (ENG_NO_GEMM, the reference's
+    --no-gemm); the oracle runs the same mode."""
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
+    _lib.set_tunable("ENG_NO_GEMM", 1 if request.param == "tokenwise" else 0)
+    try:
+        yield request.param
+    finally:
+        _lib.set_tunable("ENG_NO_GEMM", 0)
+
+
+@pytest.mark.parametrize("cfg,P", [(SMALL, 33), (SMALL_GQA, 33), (SMALL_MQA256, 20), (SMALL, 300)],
+                         ids=["gemma-mqa128", "llama-gqa", "gemma-mqa256", "two-chunks"])
+def test_engine_generate_matches_oracle(dev, cfg, P, prefill_mode):
+    seed, max_ctx = 9, 384
+    prompt = [int(t) for t in np.random.default_rng(4).integers(0, cfg.vocab, P)]
+    rows = PREFILL_ROWS if prefill_mode == "batched" else None
+    toks_ref, margins = om.OracleDecoder(cfg, om.make_weights(cfg, seed), max_ctx).generate(prompt, 40, rows)
     with _engine(cfg, max_ctx, seed) as e:
-        assert e.generate(prompt, 60) == toks_ref, f"min margin {min(margins):.3g}"
+        assert e.generate(prompt, 40) == toks_ref, f"min margin {min(margins):.3g}"
+
+
+@pytest.mark.parametrize("cfg", [SMALL, SMALL_GQA, SMALL_MQA256], ids=["gemma-mqa128", "llama-gqa", "gemma-mqa256"])
+def test_engine_batched_prefill_logits(dev, cfg):
+    """The last prompt row's logits after a batched prefill equal the oracle's
+    batched prefill (same fp16 activation points), for one chunk and for a
+    prompt split over two chunks, and the K/V it appended serve the next step."""
+    seed, max_ctx = 13, 320
+    for P in (17, 270):
+        prompt = [int(t) for t in np.random.default_rng(P).integers(0, cfg.vocab, P)]
+        ref = om.OracleDecoder(cfg, om.make_weights(cfg, seed), max_ctx)
+        ref.tokens[:P] = prompt
+        done = 0
+        while done < P:
+            rows = min(PREFILL_ROWS, P - done)
+            want = ref.prefill_chunk(done, rows, sample=done + rows == P)
+            done += rows
+        with _engine(cfg, max_ctx, seed) as e:
+            e.set_tokens(prompt)
+            e.prefill(P)
+            assert rel_err(e.logits(), want) <= 1e-3, f"P {P}"
+            assert e.token(P) == int(ref.tokens[P])
+            e.step(P)
+            assert rel_err(e.logits(), ref.forward(P)) <= 1e-3, f"step after prefill, P {P}"
 
 
 def test_graph_decode_equals_eager_steps(dev):
@@ -122,7 +165,9 @@ def test_engine_argument_errors(dev):
 @pytest.mark.skipif(not GOLDEN.exists(), reason="fixture not generated")
 def test_gemma2b_greedy_run_matches_oracle_fixture(dev):
     """Gemma-2B shape, N(0, 0.02^2) weights, 128 random prompt ids, 256 greedy
-    tokens: identical to the C oracle's tokens, logits within 1e-3."""
+    tokens: identical to the C oracle's tokens, logits within 1e-3. The fixture
+    prefills token by token, so the engine does too (ENG_NO_GEMM)."""
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
     from gemmagemini4hackathon2026_10_2425_amd.engine import GEMMA_2B, Engine
 
     g = json.loads(GOLDEN.read_text())
@@ -132,7 +177,11 @@ def test_gemma2b_greedy_run_matches_oracle_fixture(dev):
     with Engine(GEMMA_2B, g["max_ctx"]) as e:
         e.init_random(g["seed"], g["std"])
         e.set_tokens(prompt)
-        e.prefill(P)
+        _lib.set_tunable("ENG_NO_GEMM", 1)
+        try:
+            e.prefill(P)
+        finally:
+            _lib.set_tunable("ENG_NO_GEMM", 0)
 
         def check_probe(pos):
             lg = e.logits()
@@ -153,3 +202,28 @@ def test_gemma2b_greedy_run_matches_oracle_fixture(dev):
             e.decode(pos, P + N - 1 - pos)
         got = e.tokens(P, N)
     assert got == want
+
+
+@pytest.mark.skipif(not GOLDEN.exists(), reason="fixture not generated")
+def test_gemma2b_batched_prefill_matches_fixture_probe(dev):
+    """Gemma-2B shape: the batched prefill's last-row logits stay within the
+    1e-2 contract of the fixture's (token-by-token) logits at the last prompt
+    position, and pick the fixture's first token, whose top-2 margin is far
+    above that difference."""
+    from gemmagemini4hackathon2026_10_2425_amd.engine import GEMMA_2B, Engine
+
+    g = json.loads(GOLDEN.read_text())
+    prompt = g["prompt"]
+    P = len(prompt)
+    pr = g["probes"][str(P - 1)]
+    top = np.asarray(pr["top_ids"])
+    with Engine(GEMMA_2B, g["max_ctx"]) as e:
+        e.init_random(g["seed"], g["std"])
+        e.set_tokens(prompt)
+        e.prefill(P)
+        lg = e.logits()
+        scale = max(abs(v) for v in pr["top_logits"])
+        assert np.max(np.abs(lg[top] - np.asarray(pr["top_logits"]))) / scale <= 1e-2
+        margin = (pr["top_logits"][0] - pr["top_logits"][1]) / scale
+        if margin > 2e-2:
+            assert e.token(P) == g["tokens"][0]

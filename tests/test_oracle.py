@@ -294,6 +294,38 @@ def test_decode_matches_hf_gemma():
     assert toks == [int(t) for t in z["greedy"]]
 
 
+def test_prefill_chunk_pins():
+    """The batched prefill restatement: without its fp16 activation roundings
+    every row's logits equal the token-by-token path's (pinned to HF above);
+    chunking the prompt changes nothing; with the roundings the last row stays
+    within the 1e-2 contract of HF's logits and gives HF's first greedy token."""
+    z = np.load(__file__.rsplit("/", 1)[0] + "/golden/hf_gemma_tiny.npz")
+    cfg = om.TINY
+    w = om.make_weights(cfg, int(z["seed"]))
+    prompt = [int(t) for t in z["prompt"]]
+    P = len(prompt)
+    for rows in range(1, P + 1):
+        a = om.OracleDecoder(cfg, w, 64)
+        a.tokens[:P] = prompt
+        lg = a.prefill_chunk(0, rows, half_acts=False)
+        b = om.OracleDecoder(cfg, w, 64)
+        b.tokens[:P] = prompt
+        for pos in range(rows):
+            want = b.forward(pos)
+        assert np.abs(lg - want).max() / np.abs(want).max() < 1e-5, rows
+        assert np.array_equal(a.k, b.k) and np.array_equal(a.v, b.v), rows
+    whole = om.OracleDecoder(cfg, w, 64)
+    whole.tokens[:P] = prompt
+    lg_whole = whole.prefill_chunk(0, P)
+    parts = om.OracleDecoder(cfg, w, 64)
+    parts.tokens[:P] = prompt
+    parts.prefill_chunk(0, 3, sample=False)
+    lg_parts = parts.prefill_chunk(3, P - 3)
+    assert np.array_equal(lg_whole, lg_parts) and np.array_equal(whole.k, parts.k)
+    assert np.abs(lg_whole - z["logits"][P - 1]).max() / np.abs(z["logits"][P - 1]).max() < 1e-2
+    assert int(whole.tokens[P]) == int(z["greedy"][0])
+
+
 def test_decode_numpy_and_c_restatements_agree():
     cfg = om.DecodeConfig(n_layers=2, dim=256, n_heads=8, n_kv_heads=1, head_dim=256, ffn_dim=512, vocab=2000)
     seed = 21
