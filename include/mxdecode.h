@@ -340,8 +340,14 @@ int mxd_engine_get_logits(mxd_engine* e, float* host);
  * sample, writes argmax to tokens[pos + 1]. Asynchronous. Replaces
  * encodeDecode (KL/main.swift:321-347). */
 int mxd_engine_step(mxd_engine* e, int pos, int sample);
-/* Steps 0..n-1 through the decode path, sampling tokens[n] (the reference's
- * token-by-token prefill, KL/main.swift:367-368). Asynchronous. */
+/* Positions 0..n-1 of tokens[], sampling tokens[n] (prefill(n:useGemm:),
+ * KL/main.swift:357-372). From n = 2 the prompt runs in chunks of up to 256
+ * rows through mxd_gemm_f16 / mxd_gemm_gate_up_f16, mxd_attention_prefill and
+ * row-batched norm / RoPE / casts, with activations rounded to fp16 before each
+ * product as the reference's chunk does (encodePrefillChunk,
+ * KL/main.swift:412-446); the last row takes the decode path's LM head. With
+ * the ENG_NO_GEMM tunable set to 1 (the reference's --no-gemm) it steps the
+ * decode path token by token (KL/main.swift:367-368). Asynchronous. */
 int mxd_engine_prefill(mxd_engine* e, int n);
 /* count greedy steps from pos (tokens[pos] must be set) with no host round trip:
  * one captured graph replayed per step, the position kept on the device.
