@@ -259,6 +259,34 @@ def decode_leg(n_new: int = 256, prompt_len: int = 128, reps: int = 3) -> dict:
             "prompt": prompt_len, "generated": n_new}
 
 
+def prefill_leg(prompt_len: int = 512, reps: int = 3) -> dict:
+    """Gemma-2B-shaped batched prefill of a prompt of random ids (the
+    reference's --bench-pp, KL/main.swift:590-603): wall clock over
+    Engine.prefill, which ends with a sync. Flops: 2 per weight per prompt row
+    in the products (the tied head runs for the last row only)."""
+    import numpy as np
+
+    from gemmagemini4hackathon2026_10_2425_amd.engine import GEMMA_2B, Engine
+
+    shape = GEMMA_2B
+    max_ctx = (prompt_len + 32 + 31) // 32 * 32
+    with Engine(shape, max_ctx) as e:
+        e.init_random(1234)
+        e.set_tokens(np.random.default_rng(1234).integers(0, shape.vocab, prompt_len).tolist())
+        e.prefill(prompt_len)  # warm-up
+        rates = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            e.prefill(prompt_len)
+            rates.append(prompt_len / (time.perf_counter() - t0))
+    rate = float(np.median(rates))
+    D, F, qkv = shape.dim, shape.ffn_dim, (shape.n_heads + 2 * shape.n_kv_heads) * shape.head_dim
+    layer_params = shape.n_layers * (qkv * D + D * shape.n_heads * shape.head_dim + 3 * F * D)
+    flops = 2 * layer_params * prompt_len
+    return {"prompt": prompt_len, "tok_s": rate, "ms": prompt_len / rate * 1e3,
+            "product_tflops": flops / (prompt_len / rate) / 1e12}
+
+
 def cpu_baseline(seconds: float = 12.0) -> dict:
     """The C oracle's fp16 GEMV (fp64 sums, OpenMP) on the 14336x4096 matrix."""
     import numpy as np
@@ -292,7 +320,7 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemv_f16",
-                    choices=["gemv_f16", "gemv_q8", "attention", "decode", "ragged_layer", "copy"])
+                    choices=["gemv_f16", "gemv_q8", "attention", "decode", "prefill", "ragged_layer", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-detail", action="store_true", help="skip the int8 / attention detail legs")
     args = ap.parse_args(argv)
@@ -316,6 +344,7 @@ def main(argv=None) -> int:
         legs = {"gemv_q8": lambda: gemv_q8_leg(args.steps, args.warmup, dev),
                 "attention": lambda: attention_leg(args.steps, args.warmup, dev),
                 "decode": decode_leg,
+                "prefill": prefill_leg,
                 "ragged_layer": lambda: ragged_layer_leg(args.steps, args.warmup, dev),
                 "copy": lambda: copy_leg(args.steps, args.warmup, dev)}
         print(json.dumps({"workload": args.workload, **legs[args.workload]()}))
