@@ -92,6 +92,7 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_matvec_q8b32": (c_int, [P, P, P, c_int, P, c_int, c_int, c_int, P, P]),
     "mxd_matvec_gate_up": (c_int, [c_int, P, P, P, P, P, c_int, P, c_int, c_int, c_int, P]),
     "mxd_matvec_f16_rmsnorm": (c_int, [P, P, P, c_float, c_int, P, c_int, c_int, c_int, P, P]),
+    "mxd_matvec_f16_attn_merge": (c_int, [P, P, c_int, c_int, c_int, c_int, c_int, P, P, c_int, c_int, P, P]),
     "mxd_gate_up_rmsnorm": (c_int, [P, P, P, P, c_float, c_int, P, c_int, c_int, c_int, P]),
     "mxd_qkv_rope_kv": (c_int, [P, P, P, c_float, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P,
                                 P]),
@@ -101,6 +102,7 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_rope_kv": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),
     "mxd_attention_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "mxd_attention": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, P, c_size_t, P]),
+    "mxd_attention_split": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, c_int, P, c_size_t, P]),
     "mxd_attention_prefill": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P]),
     "mxd_argmax_workspace_size": (c_size_t, [c_int]),
     "mxd_argmax": (c_int, [P, P, c_int, c_int, P, c_size_t, P]),

@@ -74,6 +74,9 @@ struct AttnArgs {
     int32_t* sk_pre = nullptr;
     int n_heads, n_kv, G, max_ctx, n_keys, n_splits;
     float qscale;  // scale * log2(e): scores live in the log2 domain
+    // Every active split leaves a partial, also a single one (the consumer
+    // merges them): mxd_attention_split.
+    bool partials_only = false;
 };
 
 // Keys visible to the query: n_keys, or *pos_dev + 1 read on the device (clamped
@@ -386,14 +389,21 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a, const KV& src, int
     const int nblocks = (n + BLK - 1) / BLK;
     const size_t g0 = (size_t)kvh * a.G;
     if (nblocks == 0) {
-        if (split == 0)
+        if (split == 0 && a.partials_only) {  // a zero output as a partial: O = 0, (max, sum) = (0, 1)
+            for (int idx = threadIdx.x; idx < a.G * HD; idx += W * 64) ws_o[g0 * HD + idx] = 0.0f;
+            for (int idx = threadIdx.x; idx < a.G; idx += W * 64) {
+                ws_ml[(g0 + idx) * 2] = 0.0f;
+                ws_ml[(g0 + idx) * 2 + 1] = 1.0f;
+            }
+        } else if (split == 0) {
             for (int idx = threadIdx.x; idx < a.G * HD; idx += W * 64) orow[g0 * HD + idx] = 0.0f;
+        }
         return;
     }
     const int n_active = min(S, nblocks);
     if (split >= n_active) return;  // an empty split
     const size_t prow = (size_t)split * a.n_heads + g0;
-    const CoreOut out{orow + g0 * HD, ws_o + prow * HD, ws_ml + prow * 2, n_active == 1};
+    const CoreOut out{orow + g0 * HD, ws_o + prow * HD, ws_ml + prow * 2, n_active == 1 && !a.partials_only};
     attn_core<HD, W, PF>(a, src, n, split, S, nblocks, qrow + g0 * HD, out);
 }
 
@@ -822,6 +832,56 @@ extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint1
         if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(n_heads * 256 / MG_D), dim3(MG_T), 0, s, a);
     }
     return mxd::check_launch("mxd_attention");
+}
+
+extern "C" int mxd_attention_split(const float* q, const uint16_t* kcache, const uint16_t* vcache, int n_heads,
+                                   int n_kv_heads, int head_dim, int max_ctx, int n_keys, const int32_t* pos_dev,
+                                   float scale, int n_splits, float* partials, size_t partial_bytes,
+                                   mxd_stream_t stream) {
+    MXD_REQUIRE(q && kcache && vcache && partials, MXD_ERR_INVALID_ARG, "mxd_attention_split: null pointer");
+    MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, MXD_ERR_INVALID_ARG,
+                "mxd_attention_split: n_heads=%d must be a positive multiple of n_kv_heads=%d", n_heads, n_kv_heads);
+    const int G = n_heads / n_kv_heads;
+    MXD_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_split: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", G);
+    MXD_REQUIRE(head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED, "mxd_attention_split: head_dim %d (128 or 256)",
+                head_dim);
+    MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_split: max_ctx=%d must be a positive multiple of 32", max_ctx);
+    MXD_REQUIRE(pos_dev || (n_keys >= 1 && n_keys <= max_ctx), MXD_ERR_INVALID_ARG,
+                "mxd_attention_split: n_keys=%d outside [1, max_ctx=%d]", n_keys, max_ctx);
+    MXD_REQUIRE(n_splits >= 1 && n_splits <= MAX_SPLITS, MXD_ERR_INVALID_ARG,
+                "mxd_attention_split: n_splits=%d outside [1, %d]", n_splits, MAX_SPLITS);
+    const size_t need = (size_t)n_splits * n_heads * (head_dim + 2) * sizeof(float);
+    MXD_REQUIRE(partial_bytes >= need, MXD_ERR_WORKSPACE, "mxd_attention_split: %zu partial bytes needed (got %zu)",
+                need, partial_bytes);
+    const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kcache) |
+                         reinterpret_cast<uintptr_t>(vcache) | reinterpret_cast<uintptr_t>(partials);
+    MXD_REQUIRE((al & 15) == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_split: q, kcache, vcache, partials must be 16-byte aligned");
+    AttnArgs a;
+    a.q = q;
+    a.k = kcache;
+    a.v = vcache;
+    a.out = nullptr;
+    a.ws_o = partials;
+    a.ws_ml = partials + (size_t)n_splits * n_heads * head_dim;
+    a.pos_dev = pos_dev;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv_heads;
+    a.G = G;
+    a.max_ctx = max_ctx;
+    a.n_keys = n_keys;
+    a.n_splits = n_splits;
+    a.qscale = scale * LOG2E;
+    a.partials_only = true;
+    hipStream_t s = mxd::as_stream(stream);
+    const dim3 grid(n_splits, n_kv_heads);
+    if (head_dim == 128)
+        launch_split<128>(grid, s, a);
+    else
+        launch_split<256>(grid, s, a);
+    return mxd::check_launch("mxd_attention_split");
 }
 
 namespace {

@@ -77,6 +77,10 @@ struct mxd_engine {
     int32_t *tokens = nullptr, *pos = nullptr;
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
+    // Splits of the decode attention when its merge is folded into the o
+    // projection (one 32-key block per wave at max_ctx); 0 = the separate
+    // attention with its own merge.
+    int att_splits = 0;
     void* am_ws = nullptr;
     hipGraphExec_t graph = nullptr;
     // prefill chunk buffers: rows x {dim f32, dim f16, qkv f32, q f32, q f16,
@@ -156,10 +160,23 @@ int encode_step(mxd_engine* e, int pos, int32_t* pos_dev, bool sample) {
         if ((rc = mxd_qkv_rope_kv(Lp.wqkv, e->x, Lp.attn_norm, c.rms_eps, c.norm_plus_one, e->qkv, Lp.kc, Lp.vc,
                                   e->invf, NH, NKV, HD, D, e->max_ctx, pos, pos_dev, ms)))
             return rc;
-        if ((rc = mxd_attention(e->qkv, Lp.kc, Lp.vc, e->att, NH, NKV, HD, e->max_ctx, pos + 1, pos_dev, ascale,
-                                e->attn_ws, e->attn_ws_bytes, ms)))
-            return rc;
-        if ((rc = mxd_matvec_f16(Lp.wo, e->att, MXD_F32, e->x, D, e->q_dim(), MXD_EPI_ADD, nullptr, ms))) return rc;
+        if (e->att_splits) {
+            // The attention leaves its splits' partials; the o projection
+            // merges them as it loads its input (no merge launch).
+            float* part = static_cast<float*>(e->attn_ws);
+            if ((rc = mxd_attention_split(e->qkv, Lp.kc, Lp.vc, NH, NKV, HD, e->max_ctx, pos + 1, pos_dev, ascale,
+                                          e->att_splits, part, e->attn_ws_bytes, ms)))
+                return rc;
+            if ((rc = mxd_matvec_f16_attn_merge(Lp.wo, part, e->att_splits, NH, HD, e->max_ctx, pos + 1, pos_dev,
+                                                e->x, D, MXD_EPI_ADD, nullptr, ms)))
+                return rc;
+        } else {
+            if ((rc = mxd_attention(e->qkv, Lp.kc, Lp.vc, e->att, NH, NKV, HD, e->max_ctx, pos + 1, pos_dev, ascale,
+                                    e->attn_ws, e->attn_ws_bytes, ms)))
+                return rc;
+            if ((rc = mxd_matvec_f16(Lp.wo, e->att, MXD_F32, e->x, D, e->q_dim(), MXD_EPI_ADD, nullptr, ms)))
+                return rc;
+        }
         if ((rc = mxd_gate_up_rmsnorm(Lp.wgate, Lp.wup, e->x, Lp.ffn_norm, c.rms_eps, c.norm_plus_one, e->h, F, D,
                                       c.act, ms)))
             return rc;
@@ -257,6 +274,15 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
     const size_t D = c.dim, F = c.ffn_dim;
     const size_t kv_bytes = (size_t)c.n_kv_heads * max_ctx * c.head_dim * 2;
     e->attn_ws_bytes = mxd_attention_workspace_size(c.n_heads, c.n_kv_heads, c.head_dim, max_ctx);
+    {
+        // One 32-key block per wave (4 waves per split) over the whole
+        // context; folded into the o projection while that is at most 8
+        // splits (contexts of up to 1024 keys) and more than one.
+        const int splits = ((max_ctx + 31) / 32 + 3) / 4;
+        e->att_splits = splits >= 2 && splits <= 8 && mxd::tunable("ENG_ATT_FOLD", 1) != 2 ? splits : 0;
+        const size_t need = (size_t)splits * c.n_heads * (c.head_dim + 2) * sizeof(float);
+        if (e->att_splits && e->attn_ws_bytes < need) e->attn_ws_bytes = need;
+    }
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;

@@ -12,6 +12,8 @@
 //
 // Reference semantics: matvec_f16 / matvec_gate_up_* (KG/kernels.metal:159-234,
 // KL/kernels.metal:106-173): fp32 accumulation of float(w) * x.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace {
@@ -41,7 +43,24 @@ struct GemvArgs {
     uint16_t* vcache = nullptr;
     const int32_t* pos_dev = nullptr;
     int pos = 0, n_heads = 0, n_kv = 0, hd = 0, max_ctx = 0;
+    // x as the log-sum-exp merge of single-query attention partials
+    // (mxd_attention_split: O [splits][n_heads][hd], (max, sum) [splits][n_heads][2],
+    // log2 domain); the active splits follow from the key count n_keys, or
+    // *pos_dev + 1, as in the producer.
+    const float* mpo = nullptr;
+    const float* mpml = nullptr;
+    int msplits = 0, n_keys = 0;
 };
+
+constexpr int MERGE_MAX_SPLITS = 8;
+
+// Splits of a key count that hold a partial (one per 32-key block, at most
+// msplits, at least one: an empty context leaves one zero partial).
+__device__ __forceinline__ int merge_active(const GemvArgs& a) {
+    int n = a.pos_dev ? a.pos_dev[0] + 1 : a.n_keys;
+    n = max(0, min(n, a.max_ctx));
+    return max(1, min(a.msplits, (n + 31) / 32));
+}
 
 // Internal epilogue: rows are rotated in (i, i + hd/2) pairs and q goes back
 // to y while k and v are appended to the tiled caches.
@@ -75,11 +94,53 @@ template <int EPL> struct XFrag<float, EPL> {
             for (int j = 0; j < 4; ++j) v[4 * i + j] = v[4 * i + j] * scale * (plus_one ? 1.0f + wv[j] : wv[j]);
         }
     }
+    // x[c .. c + EPL) merged from the attention partials: the EPL values lie in
+    // one head h (hd % EPL == 0); x = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+    // Every split's loads go out before any math.
+    __device__ __forceinline__ void load_merge(const GemvArgs& a, int c) {
+        const int h = c / a.hd, na = merge_active(a);
+        const size_t ostride = (size_t)a.n_heads * a.hd, mlstride = (size_t)a.n_heads * 2;
+        float m[MERGE_MAX_SPLITS], l[MERGE_MAX_SPLITS];
+        f4_t o[MERGE_MAX_SPLITS][EPL / 4];
+#pragma unroll
+        for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp) {
+            if (sp >= na) break;
+            m[sp] = a.mpml[sp * mlstride + 2 * h];
+            l[sp] = a.mpml[sp * mlstride + 2 * h + 1];
+#pragma unroll
+            for (int i = 0; i < EPL / 4; ++i) o[sp][i] = *reinterpret_cast<const f4_t*>(a.mpo + sp * ostride + c + 4 * i);
+        }
+        float M = m[0];
+#pragma unroll
+        for (int sp = 1; sp < MERGE_MAX_SPLITS; ++sp)
+            if (sp < na) M = fmaxf(M, m[sp]);
+        float L = 0.0f;
+        f4_t acc[EPL / 4];
+#pragma unroll
+        for (int i = 0; i < EPL / 4; ++i) acc[i] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int sp = 0; sp < MERGE_MAX_SPLITS; ++sp) {
+            if (sp >= na) break;
+            const float f = __builtin_amdgcn_exp2f(m[sp] - M);
+            L += f * l[sp];
+#pragma unroll
+            for (int i = 0; i < EPL / 4; ++i) acc[i] += f * o[sp][i];
+        }
+        const float inv = 1.0f / L;
+#pragma unroll
+        for (int i = 0; i < EPL / 4; ++i) {
+            v[4 * i + 0] = acc[i].x * inv;
+            v[4 * i + 1] = acc[i].y * inv;
+            v[4 * i + 2] = acc[i].z * inv;
+            v[4 * i + 3] = acc[i].w * inv;
+        }
+    }
 };
 
 template <int EPL> struct XFrag<_Float16, EPL> {
     h2_t v[EPL / 2];
     __device__ __forceinline__ void load_norm(const void*, const float*, int, float, int) {}  // host rejects
+    __device__ __forceinline__ void load_merge(const GemvArgs&, int) {}                      // host rejects
     __device__ __forceinline__ void load(const void* x, int c) {
         const _Float16* p = static_cast<const _Float16*>(x) + c;
 #pragma unroll
@@ -230,7 +291,9 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
             const int col = c * CH + lane * EPL;
             ok[u] = (c < nch) && (col < K);
             if (ok[u]) {
-                if (a.nw)
+                if (a.mpo)
+                    xf[u].load_merge(a, col);
+                else if (a.nw)
                     xf[u].load_norm(a.x, a.nw, col, 1.0f, a.plus_one);
                 else
                     xf[u].load(a.x, col);
@@ -873,4 +936,46 @@ extern "C" int mxd_qkv_rope_kv(const uint16_t* Wqkv, const float* x, const float
         case 4: return launch_nw<MXD_W_F16, float, 1, EPI_ROPE_KV, 4>(a, nw, s);
         default: return launch_nw<MXD_W_F16, float, 1, EPI_ROPE_KV, 8>(a, nw, s);
     }
+}
+
+extern "C" int mxd_matvec_f16_attn_merge(const uint16_t* W, const float* partials, int n_splits, int n_heads,
+                                         int head_dim, int max_ctx, int n_keys, const int32_t* pos_dev, float* y,
+                                         int M, int epilogue, const float* aux, mxd_stream_t stream) {
+    const int K = n_heads * head_dim;
+    if (int rc = check_common("mxd_matvec_f16_attn_merge", W, partials, y, M, K)) return rc;
+    MXD_REQUIRE(n_splits >= 1 && n_splits <= MERGE_MAX_SPLITS, MXD_ERR_UNSUPPORTED,
+                "mxd_matvec_f16_attn_merge: n_splits=%d outside [1, %d]", n_splits, MERGE_MAX_SPLITS);
+    MXD_REQUIRE(head_dim > 0 && head_dim % 8 == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_matvec_f16_attn_merge: head_dim=%d must be a multiple of 8", head_dim);
+    MXD_REQUIRE(max_ctx > 0, MXD_ERR_INVALID_ARG, "mxd_matvec_f16_attn_merge: max_ctx=%d", max_ctx);
+    MXD_REQUIRE(pos_dev || (n_keys >= 0 && n_keys <= max_ctx), MXD_ERR_INVALID_ARG,
+                "mxd_matvec_f16_attn_merge: n_keys=%d outside [0, max_ctx=%d]", n_keys, max_ctx);
+    MXD_REQUIRE(epilogue != MXD_EPI_GELU_MUL || aux, MXD_ERR_INVALID_ARG,
+                "mxd_matvec_f16_attn_merge: GELU_MUL needs aux");
+    GemvArgs a{{W, nullptr}, {nullptr, nullptr}, partials, y, aux, M, K};
+    a.mpo = partials;
+    a.mpml = partials + (size_t)n_splits * K;
+    a.msplits = n_splits;
+    a.n_heads = n_heads;
+    a.hd = head_dim;
+    a.max_ctx = max_ctx;
+    a.n_keys = n_keys;
+    a.pos_dev = pos_dev;
+    // Row tiles (every workgroup merges the x it reads, so fewer, taller
+    // tiles read fewer partials): 8 rows from 2048 rows on.
+    int nr, nw;
+    pick_tiling(M, (K + 511) / 512, false, false, false, nr, nw);
+    hipStream_t s = mxd::as_stream(stream);
+    auto go = [&](auto nrc) -> int {
+        constexpr int NR = decltype(nrc)::value;
+        switch (epilogue) {
+            case MXD_EPI_STORE: return launch_nw<MXD_W_F16, float, 1, MXD_EPI_STORE, NR>(a, nw, s);
+            case MXD_EPI_ADD: return launch_nw<MXD_W_F16, float, 1, MXD_EPI_ADD, NR>(a, nw, s);
+            case MXD_EPI_GELU_MUL: return launch_nw<MXD_W_F16, float, 1, MXD_EPI_GELU_MUL, NR>(a, nw, s);
+            default: return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_matvec_f16_attn_merge: unknown epilogue %d", epilogue);
+        }
+    };
+    if (M >= 2048) return go(std::integral_constant<int, 8>{});
+    if (M >= 256) return go(std::integral_constant<int, 2>{});
+    return go(std::integral_constant<int, 1>{});
 }

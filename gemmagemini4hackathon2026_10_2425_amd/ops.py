@@ -291,6 +291,42 @@ def attention(q, kcache, vcache, n_keys: int, n_heads: int, scale: float | None 
     return out
 
 
+def attention_split(q, kcache, vcache, n_keys: int, n_heads: int, n_splits: int, scale: float | None = None,
+                    partials=None, pos_dev=None) -> torch.Tensor:
+    """The split half of attention without its merge: a float32 buffer of
+    n_splits unnormalised partials, O [n_splits, n_heads, hd] then (max, sum)
+    [n_splits, n_heads, 2] (log2-domain scores), for matvec_f16_attn_merge."""
+    _on_gpu(q, kcache, vcache)
+    n_kv, max_ctx, hd = _check_caches(kcache, vcache, "attention_split")
+    _need(q.numel() == n_heads * hd and q.dtype == torch.float32, "attention_split: q float32 [n_heads*hd]")
+    scale = 1.0 / math.sqrt(hd) if scale is None else scale
+    n = n_splits * n_heads * (hd + 2)
+    partials = torch.empty(n, dtype=torch.float32, device=q.device) if partials is None else partials
+    _need(partials.dtype == torch.float32 and partials.numel() >= n, f"attention_split: partials float32 [{n}]")
+    call(
+        "mxd_attention_split", _ptr(q), _ptr(kcache), _ptr(vcache), n_heads, n_kv, hd, max_ctx, int(n_keys),
+        _ptr(pos_dev), float(scale), int(n_splits), _ptr(partials), partials.numel() * 4, _stream(),
+    )
+    return partials
+
+
+def matvec_f16_attn_merge(W, partials, n_splits: int, n_heads: int, head_dim: int, max_ctx: int, n_keys: int,
+                          y=None, epilogue: str = "store", pos_dev=None) -> torch.Tensor:
+    """y (op)= W . x with x the log-sum-exp merge of attention_split's partials."""
+    _on_gpu(W, partials)
+    M, K = W.shape
+    _need(W.dtype == torch.float16 and K == n_heads * head_dim, "matvec_f16_attn_merge: W fp16 [M, n_heads*hd]")
+    _need(partials.dtype == torch.float32, "matvec_f16_attn_merge: partials float32")
+    if y is None:
+        _need(epilogue == "store", "matvec_f16_attn_merge: epilogue 'add' needs y")
+        y = torch.empty(M, dtype=torch.float32, device=W.device)
+    call(
+        "mxd_matvec_f16_attn_merge", _ptr(W), _ptr(partials), int(n_splits), n_heads, head_dim, max_ctx,
+        int(n_keys), _ptr(pos_dev), _ptr(y), M, _EPI[epilogue], None, _stream(),
+    )
+    return y
+
+
 def attention_prefill(q, kcache, vcache, pos0: int, n_heads: int, scale: float | None = None, out=None,
                       q_stride: int | None = None, rows: int | None = None) -> torch.Tensor:
     """Causal attention of a prefill chunk: row t of q (rows q_stride floats

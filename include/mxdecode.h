@@ -130,6 +130,17 @@ int mxd_qkv_rope_kv(const uint16_t* Wqkv, const float* x, const float* norm_w, f
                     uint16_t* kcache, uint16_t* vcache, const float* inv_freq, int n_heads, int n_kv_heads,
                     int head_dim, int K, int max_ctx, int pos, const int32_t* pos_dev, mxd_stream_t stream);
 
+/* y (op)= W · x where x is the single-query attention output given as the
+ * unmerged partials of mxd_attention_split (n_splits <= 8): every workgroup
+ * merges the x values it reads with the log-sum-exp rule, so the attention
+ * needs no merge launch. W fp16 [M][n_heads*head_dim]; the active splits
+ * follow from n_keys, or *n_keys_dev + 1, as in the producer. Fuses the
+ * attention output into the output projection (KL/main.swift:336-337:
+ * attention then matvec_add(wo)). */
+int mxd_matvec_f16_attn_merge(const uint16_t* W, const float* partials, int n_splits, int n_heads,
+                              int head_dim, int max_ctx, int n_keys, const int32_t* n_keys_dev, float* y,
+                              int M, int epilogue, const float* aux, mxd_stream_t stream);
+
 /* ---- normalisation, embedding, casts ------------------------------------ */
 
 /* y[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * (plus_one ? 1 + w : w), rows x D,
@@ -180,6 +191,21 @@ int mxd_attention(const float* q, const uint16_t* kcache, const uint16_t* vcache
                   int n_heads, int n_kv_heads, int head_dim, int max_ctx, int n_keys,
                   const int32_t* n_keys_dev, float scale, void* workspace, size_t ws_bytes,
                   mxd_stream_t stream);
+
+/* The split half of mxd_attention without its merge: split s of n_splits
+ * (1 .. 512) takes the 32-key blocks s, s + n_splits, ... and writes its
+ * unnormalised partial, O to partials[s][h][0..hd) and (max, sum) of its
+ * log2-domain scores to partials[n_splits*n_heads*hd + (s*n_heads + h)*2 ..],
+ * for the splits that hold a block (min(n_splits, ceil(n_keys / 32))); with
+ * no keys, split 0 holds a zero partial (O = 0, max 0, sum 1). partial_bytes
+ * >= n_splits*n_heads*(hd + 2)*4. The merge belongs to the consumer
+ * (mxd_matvec_f16_attn_merge). Same shapes and caches as mxd_attention;
+ * replaces the reference attention's per-head loop over keys
+ * (KL/kernels.metal:258-304) for T = 1. */
+int mxd_attention_split(const float* q, const uint16_t* kcache, const uint16_t* vcache, int n_heads,
+                        int n_kv_heads, int head_dim, int max_ctx, int n_keys, const int32_t* n_keys_dev,
+                        float scale, int n_splits, float* partials, size_t partial_bytes,
+                        mxd_stream_t stream);
 
 /* Causal attention of a prefill chunk: `rows` queries at positions pos0 ..
  * pos0 + rows - 1 (their keys and values already in the caches), query t over

@@ -142,3 +142,45 @@ def test_every_matvec_variant(dev, rng, algo):
         assert rel_err(yn.cpu().numpy(), ref.matvec(W, xn)) <= 1e-4
     finally:
         L.set_tunable("MV_ALGO", 0)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,M", [(8, 1, 256, 2048), (32, 8, 128, 4096), (4, 2, 128, 300)])
+@pytest.mark.parametrize("L,n_splits", [(1, 3), (45, 3), (384, 3), (129, 8), (1000, 8), (700, 2)])
+@pytest.mark.parametrize("device_pos", [False, True])
+def test_attention_split_merged_by_matvec(dev, rng, nh, nkv, hd, M, L, n_splits, device_pos):
+    """Attention left as unmerged split partials, merged by the o projection
+    as it loads its input, equals the oracle's attention then matvec + residual;
+    cache rows past the key count hold NaN/inf and must not leak."""
+    from gemmagemini4hackathon2026_10_2425_amd import ops
+
+    max_ctx = 1024
+    q = rng.standard_normal(nh * hd, dtype=np.float32)
+    kc = np.full((nkv, max_ctx, hd), np.nan, np.float16)
+    vc = np.full((nkv, max_ctx, hd), np.inf, np.float16)
+    kc[:, :L] = rng.standard_normal((nkv, L, hd), dtype=np.float32).astype(np.float16)
+    vc[:, :L] = rng.standard_normal((nkv, L, hd), dtype=np.float32).astype(np.float16)
+    W = (rng.standard_normal((M, nh * hd), dtype=np.float32) * 0.02).astype(np.float16)
+    base = rng.standard_normal(M, dtype=np.float32)
+    qd, kd, vd = _d(q, dev), _d(ops.to_tiles(kc, "k"), dev), _d(ops.to_tiles(vc, "v"), dev)
+    Wd, yd = _d(W, dev), _d(base, dev)
+    pos = torch.tensor([L - 1], dtype=torch.int32, device=dev) if device_pos else None
+    n_keys = 0 if device_pos else L
+    part = ops.attention_split(qd, kd, vd, n_keys, nh, n_splits, pos_dev=pos)
+    ops.matvec_f16_attn_merge(Wd, part, n_splits, nh, hd, max_ctx, n_keys, y=yd, epilogue="add", pos_dev=pos)
+    att = ref.attention(q, kc[:, :L], vc[:, :L], L, nh, 1 / math.sqrt(hd)).astype(np.float32)
+    want = base + ref.matvec(W, att)
+    assert rel_err(yd.cpu().numpy(), want) <= 1e-3
+
+
+def test_attention_split_rejects_bad_args(dev):
+    from gemmagemini4hackathon2026_10_2425_amd import _lib as L
+    from gemmagemini4hackathon2026_10_2425_amd import ops
+
+    q = torch.zeros(8 * 256, dtype=torch.float32, device=dev)
+    kc = torch.zeros((1, 64, 256), dtype=torch.float16, device=dev)
+    with pytest.raises(L.MxdValueError):
+        ops.attention_split(q, kc, kc, 10, 8, 600)  # more splits than supported
+    part = ops.attention_split(q, kc, kc, 10, 8, 2)
+    W = torch.zeros((16, 8 * 256), dtype=torch.float16, device=dev)
+    with pytest.raises(L.MxdValueError):
+        ops.matvec_f16_attn_merge(W, part, 9, 8, 256, 64, 10)  # the merge takes at most 8 splits
