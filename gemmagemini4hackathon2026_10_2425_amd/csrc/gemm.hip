@@ -379,6 +379,8 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
     const f32x16_t zero = acc[0];
+    f32x16_t tp[2] = {zero, zero};  // int8: the previous block's unscaled products
+    float sp = 0.0f;                // and its scale
 
     static_for<0, NCH>([&](auto cic) {
         constexpr int ci = decltype(cic)::value;
@@ -419,24 +421,39 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
                 f32x16_t t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, zero, 0, 0, 0);
                 t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, t0, 0, 0, 0);
                 t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, t1, 0, 0, 0);
+                // Software pipeline: the previous block's products are scaled
+                // while this block's MFMAs run (they do not depend on each
+                // other), so the matrix core and the VALU overlap in one wave.
+                if (ci > 0 || j > 0) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    acc[0][r] = fmaf(sc[j], t0[r], acc[0][r]);
-                    acc[1][r] = fmaf(sc[j], t1[r], acc[1][r]);
+                    for (int r = 0; r < 16; ++r) {
+                        acc[0][r] = fmaf(sp, tp[0][r], acc[0][r]);
+                        acc[1][r] = fmaf(sp, tp[1][r], acc[1][r]);
+                    }
                 }
+                tp[0] = t0;
+                tp[1] = t1;
+                sp = sc[j];
             } else {
                 acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x00, w0, acc[0], 0, 0, 0);
                 acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, acc[1], 0, 0, 0);
                 acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, acc[0], 0, 0, 0);
                 acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, acc[1], 0, 0, 0);
             }
-            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
+            if constexpr (!Q8) asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
         }
         if constexpr (ci + 1 < NCH) {
             store_x(ic<ci + 1>{});
             __syncthreads();
         }
     });
+    if constexpr (Q8) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            acc[0][r] = fmaf(sp, tp[0][r], acc[0][r]);
+            acc[1][r] = fmaf(sp, tp[1][r], acc[1][r]);
+        }
+    }
 
     const int wr_out = row0 + mc;
     auto brow = [&](int t, int r) { return b0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3); };
