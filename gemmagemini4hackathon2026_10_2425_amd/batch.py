@@ -175,12 +175,14 @@ def gemm_workspace(n_rows: int, M: int, K: int, glu: bool = False, device="cuda"
 
 
 def gemm_q8b32(Wq, scales, X, Y=None, epilogue: str = "store", workspace=None) -> torch.Tensor:
-    """Y[b] (op)= dequant(Wq, scales) . X[b]; X fp16 [B, K], Y fp32 [B, M]."""
+    """Y[b] (op)= dequant(Wq, scales) . X[b]; X fp16 or fp32 [B, K] (fp32 is
+    rounded to fp16 as it is loaded), Y fp32 [B, M]."""
     ops._on_gpu(Wq, scales, X)
     M, K = Wq.shape
     _need(Wq.dtype == torch.int8 and scales.dtype == torch.float16 and tuple(scales.shape) == (M, K // 32),
           "gemm_q8b32: int8 Wq [M, K] and fp16 scales [M, K/32]")
-    _need(X.dtype == torch.float16 and X.dim() == 2 and X.shape[1] == K, "gemm_q8b32: X fp16 [B, K]")
+    _need(X.dtype in (torch.float16, torch.float32) and X.dim() == 2 and X.shape[1] == K and X.is_contiguous(),
+          "gemm_q8b32: X fp16 or fp32 [B, K]")
     B = X.shape[0]
     if Y is None:
         _need(epilogue == "store", "gemm_q8b32: epilogue 'add' needs Y")
@@ -188,7 +190,7 @@ def gemm_q8b32(Wq, scales, X, Y=None, epilogue: str = "store", workspace=None) -
     _need(Y.is_contiguous() and Y.dtype == torch.float32 and Y.numel() == B * M, "gemm_q8b32: Y fp32 [B, M]")
     if workspace is None:
         workspace = gemm_workspace(B, M, K, False, X.device)
-    call("mxd_gemm_q8b32", Wq.data_ptr(), scales.data_ptr(), X.data_ptr(), Y.data_ptr(), B, M, K,
+    call("mxd_gemm_q8b32", Wq.data_ptr(), scales.data_ptr(), X.data_ptr(), ops._xdtype(X), Y.data_ptr(), B, M, K,
          ops._EPI[epilogue], workspace.data_ptr(), workspace.numel(), ops._stream())
     return Y
 
@@ -264,9 +266,7 @@ class RaggedLayerQ8:
         self.xn = torch.empty((B, D), dtype=torch.float16, device=self.dev)
         self.qkv = torch.empty((B, s.qkv_dim), dtype=torch.float32, device=self.dev)
         self.att = torch.empty((B, QD), dtype=torch.float32, device=self.dev)
-        self.att16 = torch.empty((B, QD), dtype=torch.float16, device=self.dev)
         self.h = torch.empty((B, F), dtype=torch.float32, device=self.dev)
-        self.h16 = torch.empty((B, F), dtype=torch.float16, device=self.dev)
         self.ws = {
             "wqkv": gemm_workspace(B, s.qkv_dim, D, False, self.dev),
             "wo": gemm_workspace(B, D, QD, False, self.dev),
@@ -280,19 +280,18 @@ class RaggedLayerQ8:
         layer's pools; seq_lens int32 [B] after the append."""
         s, B = self.s, X.shape[0]
         D, F, QD = s.dim, s.ffn_dim, s.n_heads * s.head_dim
-        xn, qkv, att, att16 = self.xn[:B], self.qkv[:B], self.att[:B], self.att16[:B]
-        h, h16 = self.h[:B], self.h16[:B]
+        xn, qkv, att, h = self.xn[:B], self.qkv[:B], self.att[:B], self.h[:B]
         ops.rmsnorm(X, self.attn_norm, s.eps, s.plus_one, y=xn, out_dtype=torch.float16)
         gemm_q8b32(*self.W["wqkv"], xn, qkv, workspace=self.ws["wqkv"])
         rope_kv_paged(qkv, kpool, vpool, self.invf, s.n_heads, s.n_kv_heads, page_table, seq_lens)
         attention_paged(qkv, kpool, vpool, page_table, seq_lens, s.n_heads, self.max_keys, q_stride=s.qkv_dim,
                         out=att, workspace=self.ws["attn"])
-        ops.f32_to_f16(att, att16)
-        gemm_q8b32(*self.W["wo"], att16, X, "add", workspace=self.ws["wo"])
+        # the fp32 attention output and hidden rows are rounded to fp16 as the
+        # products load them (the reference's attHalf / hidHalf casts)
+        gemm_q8b32(*self.W["wo"], att, X, "add", workspace=self.ws["wo"])
         ops.rmsnorm(X, self.ffn_norm, s.eps, s.plus_one, y=xn, out_dtype=torch.float16)
         gemm_gate_up_q8b32(*self.W["wgate"], *self.W["wup"], xn, s.act, h, workspace=self.ws["glu"])
-        ops.f32_to_f16(h, h16)
-        gemm_q8b32(*self.W["wdown"], h16, X, "add", workspace=self.ws["wdown"])
+        gemm_q8b32(*self.W["wdown"], h, X, "add", workspace=self.ws["wdown"])
 
 
 def random_layer_weights(shape: LayerShape, seed: int, std: float = 0.02) -> dict:

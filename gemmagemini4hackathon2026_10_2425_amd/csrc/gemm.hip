@@ -38,7 +38,7 @@
 // down 4096x14336 34.8 us; an earlier layout (16x16 MFMAs, a 64 x 1024
 // activation slice resident in LDS, one workgroup per CU) took 29.3 / 19.9 /
 // 67.4 / 36.3 us.
-#include "common.hpp"
+#include "internal.hpp"
 
 namespace {
 
@@ -54,6 +54,7 @@ struct GemmArgs {
     const int8_t* W[2];  // int8 [M][K], or fp16 [M][K] (MXD_W_F16) through the same pointer
     const uint16_t* S[2];
     const uint16_t* X;  // fp16 [n_rows][K]
+    const float* Xf;    // or fp32 [n_rows][K], rounded to fp16 as it is staged (XF32 kernels)
     float* Y;           // fp32 [n_rows][M]
     float* part;        // fp32 [splits][n_rows][NMAT][M] when splits > 1
     int n_rows, M, K, splits;
@@ -87,6 +88,31 @@ __device__ __forceinline__ float epilogue(float g, float u, float old) {
     }
 }
 
+// One 16-byte activation piece (8 k of one row) on its way to LDS: fp16 as
+// loaded, or fp32 (two 16-byte loads) rounded to nearest-even fp16 when it is
+// written (the rounding of mxd_f32_to_f16), so an fp32 producer needs no cast
+// launch. e is the element offset of the piece in X.
+template <bool XF32>
+struct XPiece {
+    u4_t v;
+    __device__ __forceinline__ void load(const GemmArgs& a, size_t e) { v = *reinterpret_cast<const u4_t*>(a.X + e); }
+    __device__ __forceinline__ u4_t h8() const { return v; }
+};
+template <>
+struct XPiece<true> {
+    f4_t lo, hi;
+    __device__ __forceinline__ void load(const GemmArgs& a, size_t e) {
+        lo = *reinterpret_cast<const f4_t*>(a.Xf + e);
+        hi = *reinterpret_cast<const f4_t*>(a.Xf + e + 4);
+    }
+    static __device__ __forceinline__ uint32_t pack(float x, float y) {
+        return (uint32_t)mxd::f2h_bits(x) | ((uint32_t)mxd::f2h_bits(y) << 16);
+    }
+    __device__ __forceinline__ u4_t h8() const {
+        return u4_t{pack(lo.x, lo.y), pack(lo.z, lo.w), pack(hi.x, hi.y), pack(hi.z, hi.w)};
+    }
+};
+
 __device__ __forceinline__ h8_t q8x8_to_h8(uint32_t lo, uint32_t hi) {
     h2_t a[4];
     mxd::i8x4_to_h2x2(lo, a[0], a[1]);
@@ -96,7 +122,7 @@ __device__ __forceinline__ h8_t q8x8_to_h8(uint32_t lo, uint32_t hi) {
 
 // The runtime-loop form (any chunk count): activations in registers two
 // chunks ahead, a register ring of two chunks of weights and scales.
-template <int NMAT, int OP>
+template <int NMAT, int OP, bool XF32>
 __global__ void __launch_bounds__(GM_THREADS) gemm_q8_loop_kernel(GemmArgs a) {
     constexpr int WAVES = GM_WAVES, NT = GM_THREADS;
     constexpr int WPM = WAVES / NMAT;  // waves per matrix
@@ -135,26 +161,26 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_loop_kernel(GemmArgs a) {
     // Activation chunk c: 64 rows x 128 halfs as 1024 pieces of 16 bytes;
     // thread t takes pieces t + NT u (row p / 16, piece p % 16). Rows past
     // n_rows are stored as zeros (loaded from a clamped, valid row).
-    const uint16_t* xbase = a.X + (size_t)c0 * GM2_CK;
-    auto load_x = [&](u4_t (&v)[XPT], int ci) {
+    const size_t xoff = (size_t)c0 * GM2_CK;
+    auto load_x = [&](XPiece<XF32> (&v)[XPT], int ci) {
 #pragma unroll
         for (int u = 0; u < XPT; ++u) {
             const int p = threadIdx.x + NT * u, r = p >> 4, q = p & 15;
-            v[u] = *reinterpret_cast<const u4_t*>(xbase + (size_t)min(b0 + r, a.n_rows - 1) * K + (size_t)ci * GM2_CK + 8 * q);
+            v[u].load(a, xoff + (size_t)min(b0 + r, a.n_rows - 1) * K + (size_t)ci * GM2_CK + 8 * q);
         }
     };
-    auto store_x = [&](const u4_t (&v)[XPT], int buf) {
+    auto store_x = [&](const XPiece<XF32> (&v)[XPT], int buf) {
 #pragma unroll
         for (int u = 0; u < XPT; ++u) {
             const int p = threadIdx.x + NT * u, r = p >> 4, q = p & 15;
             const u4_t z = {0u, 0u, 0u, 0u};
-            *reinterpret_cast<u4_t*>(&xs[buf][r][8 * q]) = b0 + r < a.n_rows ? v[u] : z;
+            *reinterpret_cast<u4_t*>(&xs[buf][r][8 * q]) = b0 + r < a.n_rows ? v[u].h8() : z;
         }
     };
     // Register ring of two chunks: set p holds chunk ci (ci & 1 == p) from its
     // load, issued two chunks ahead, until it is stored to LDS buffer p at the
     // end of chunk ci - 1.
-    u4_t xv[2][XPT];
+    XPiece<XF32> xv[2][XPT];
     load_x(xv[0], 0);
     if (c0 + 1 < c1) load_x(xv[1], 1);
     store_x(xv[0], 0);
@@ -287,7 +313,7 @@ __device__ __forceinline__ void static_for(F&& f) {
 // bytes, two 16-byte loads that are the MFMA operands as they stand; products
 // accumulate in the MFMA accumulators). The k order, the activation side and
 // the epilogues are the same for both.
-template <int WF, int NMAT, int OP, int NCH>
+template <int WF, int NMAT, int OP, int NCH, bool XF32>
 __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
     constexpr int WAVES = GM_WAVES, NT = GM_THREADS;
     constexpr int WPM = WAVES / NMAT;
@@ -316,19 +342,18 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
     const int wrow = min(row0 + mc, M - 1);
     const unsigned char* wp =
         reinterpret_cast<const unsigned char*>(a.W[m]) + ((size_t)wrow * K + (size_t)c0 * GM2_CK + 16 * h) * ESZ;
-    const uint16_t* xbase = a.X + (size_t)c0 * GM2_CK;
+    const size_t xoff = (size_t)c0 * GM2_CK;
 
     // Activations of chunk ci: thread t loads pieces t + NT u (row p / 16,
     // piece p % 16) into register set ci & 1, two chunks ahead; the set is
     // written to LDS buffer ci & 1 at the end of chunk ci - 1.
-    u4_t xv[2][XPT];
+    XPiece<XF32> xv[2][XPT];
     auto load_x = [&](auto cic) {
         constexpr int ci = decltype(cic)::value;
 #pragma unroll
         for (int u = 0; u < XPT; ++u) {
             const int p = threadIdx.x + NT * u, r = p >> 4, q = p & 15;
-            xv[ci & 1][u] = *reinterpret_cast<const u4_t*>(xbase + (size_t)min(b0 + r, a.n_rows - 1) * K +
-                                                          (size_t)ci * GM2_CK + 8 * q);
+            xv[ci & 1][u].load(a, xoff + (size_t)min(b0 + r, a.n_rows - 1) * K + (size_t)ci * GM2_CK + 8 * q);
         }
     };
     auto store_x = [&](auto cic) {
@@ -336,7 +361,7 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
         for (int u = 0; u < XPT; ++u) {
             const int p = threadIdx.x + NT * u, r = p >> 4, q = p & 15;
-            *reinterpret_cast<u4_t*>(&xs[ci & 1][r][8 * (q ^ (r & 15))]) = xv[ci & 1][u];
+            *reinterpret_cast<u4_t*>(&xs[ci & 1][r][8 * (q ^ (r & 15))]) = xv[ci & 1][u].h8();
         }
     };
     // Block j of chunk ci: ESZ 16-byte pieces per lane. Ordinary (temporal)
@@ -573,7 +598,7 @@ size_t ws_bytes_for(int wf, int n_rows, int M, int K, int nmat) {
     return s > 1 ? (size_t)s * n_rows * nmat * M * sizeof(float) : 0;
 }
 
-template <int WF, int NMAT, int OP>
+template <int WF, int NMAT, int OP, bool XF32 = false>
 int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char* fn) {
     a.splits = pick_splits(WF, a.n_rows, a.M, a.K, NMAT);
     const size_t need = a.splits > 1 ? (size_t)a.splits * a.n_rows * NMAT * a.M * sizeof(float) : 0;
@@ -586,13 +611,13 @@ int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char
     const dim3 grid((unsigned)((pairs + 7) / 8 * 8 * a.batch_tiles));  // see gemm_tile
     const int nch = pick_nch(WF, a.n_rows, a.M, a.K, NMAT);
     switch (nch) {
-        case 4: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 4>), grid, dim3(GM_THREADS), 0, s, a); break;
-        case 8: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 8>), grid, dim3(GM_THREADS), 0, s, a); break;
-        case 16: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 16>), grid, dim3(GM_THREADS), 0, s, a); break;
-        case 32: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 32>), grid, dim3(GM_THREADS), 0, s, a); break;
+        case 4: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 4, XF32>), grid, dim3(GM_THREADS), 0, s, a); break;
+        case 8: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 8, XF32>), grid, dim3(GM_THREADS), 0, s, a); break;
+        case 16: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 16, XF32>), grid, dim3(GM_THREADS), 0, s, a); break;
+        case 32: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 32, XF32>), grid, dim3(GM_THREADS), 0, s, a); break;
         default:
             if constexpr (WF == MXD_W_Q8B32) {
-                hipLaunchKernelGGL((gemm_q8_loop_kernel<NMAT, OP>), grid, dim3(GM_THREADS), 0, s, a);
+                hipLaunchKernelGGL((gemm_q8_loop_kernel<NMAT, OP, XF32>), grid, dim3(GM_THREADS), 0, s, a);
             } else {
                 return mxd::fail(MXD_ERR_UNSUPPORTED, "%s: K=%d has no chunk count for fp16 weights", fn, a.K);
             }
@@ -636,28 +661,42 @@ extern "C" size_t mxd_gemm_gate_up_f16_workspace_size(int n_rows, int F, int K) 
     return ws_bytes_for(MXD_W_F16, n_rows, F, K, 2);
 }
 
-extern "C" int mxd_gemm_q8b32(const int8_t* Wq, const uint16_t* scales, const uint16_t* X, float* Y, int n_rows, int M,
-                              int K, int epilogue, void* workspace, size_t ws_bytes, mxd_stream_t stream) {
+extern "C" int mxd_gemm_q8b32(const int8_t* Wq, const uint16_t* scales, const void* X, int x_dtype, float* Y,
+                              int n_rows, int M, int K, int epilogue, void* workspace, size_t ws_bytes,
+                              mxd_stream_t stream) {
     if (int rc = check_common(Wq, scales, X, Y, n_rows, M, K, "mxd_gemm_q8b32")) return rc;
     MXD_REQUIRE(epilogue == MXD_EPI_STORE || epilogue == MXD_EPI_ADD, MXD_ERR_INVALID_ARG,
                 "mxd_gemm_q8b32: epilogue %d (store or add)", epilogue);
-    if (!use_mfma(MXD_W_Q8B32, n_rows, K)) {  // few rows: one matvec per row
+    MXD_REQUIRE(x_dtype == MXD_F16 || x_dtype == MXD_F32, MXD_ERR_INVALID_ARG, "mxd_gemm_q8b32: x_dtype %d",
+                x_dtype);
+    const size_t xesz = x_dtype == MXD_F32 ? 4 : 2;
+    if (!use_mfma(MXD_W_Q8B32, n_rows, K)) {  // few rows: one matvec per row (fp32 X rounded the same way)
         for (int b = 0; b < n_rows; ++b) {
-            if (int rc = mxd_matvec_q8b32(Wq, scales, X + (size_t)b * K, MXD_F16, Y + (size_t)b * M, M, K, epilogue,
-                                          nullptr, stream))
-                return rc;
+            const void* xb = static_cast<const char*>(X) + (size_t)b * K * xesz;
+            const int rc = x_dtype == MXD_F32
+                               ? mxd::matvec_q8b32_xr16(Wq, scales, static_cast<const float*>(xb), Y + (size_t)b * M,
+                                                        M, K, epilogue, mxd::as_stream(stream))
+                               : mxd_matvec_q8b32(Wq, scales, xb, MXD_F16, Y + (size_t)b * M, M, K, epilogue, nullptr,
+                                                  stream);
+            if (rc) return rc;
         }
         return MXD_OK;
     }
     GemmArgs a{};
     a.W[0] = a.W[1] = Wq;
     a.S[0] = a.S[1] = scales;
-    a.X = X;
+    a.X = static_cast<const uint16_t*>(X);
+    a.Xf = static_cast<const float*>(X);
     a.Y = Y;
     a.n_rows = n_rows;
     a.M = M;
     a.K = K;
     hipStream_t s = mxd::as_stream(stream);
+    if (x_dtype == MXD_F32) {
+        if (epilogue == MXD_EPI_ADD)
+            return launch_gemm<MXD_W_Q8B32, 1, MXD_EPI_ADD, true>(a, workspace, ws_bytes, s, "mxd_gemm_q8b32");
+        return launch_gemm<MXD_W_Q8B32, 1, MXD_EPI_STORE, true>(a, workspace, ws_bytes, s, "mxd_gemm_q8b32");
+    }
     if (epilogue == MXD_EPI_ADD)
         return launch_gemm<MXD_W_Q8B32, 1, MXD_EPI_ADD>(a, workspace, ws_bytes, s, "mxd_gemm_q8b32");
     return launch_gemm<MXD_W_Q8B32, 1, MXD_EPI_STORE>(a, workspace, ws_bytes, s, "mxd_gemm_q8b32");

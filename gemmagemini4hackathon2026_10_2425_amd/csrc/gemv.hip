@@ -14,7 +14,7 @@
 // KL/kernels.metal:106-173): fp32 accumulation of float(w) * x.
 #include <type_traits>
 
-#include "common.hpp"
+#include "internal.hpp"
 
 namespace {
 
@@ -50,6 +50,9 @@ struct GemvArgs {
     const float* mpo = nullptr;
     const float* mpml = nullptr;
     int msplits = 0, n_keys = 0;
+    // fp32 x rounded to nearest-even fp16 on load (the batched products'
+    // fp32-activation mode, below their matrix-core threshold)
+    int xr16 = 0;
 };
 
 constexpr int MERGE_MAX_SPLITS = 8;
@@ -71,7 +74,7 @@ template <typename XT, int EPL> struct XFrag;
 
 template <int EPL> struct XFrag<float, EPL> {
     float v[EPL];
-    __device__ __forceinline__ void load(const void* x, int c) {
+    __device__ __forceinline__ void load(const void* x, int c, int round16 = 0) {
         const float* p = static_cast<const float*>(x) + c;
 #pragma unroll
         for (int i = 0; i < EPL / 4; ++i) {
@@ -80,6 +83,10 @@ template <int EPL> struct XFrag<float, EPL> {
             v[4 * i + 1] = t.y;
             v[4 * i + 2] = t.z;
             v[4 * i + 3] = t.w;
+        }
+        if (round16) {
+#pragma unroll
+            for (int i = 0; i < EPL; ++i) v[i] = (float)(_Float16)v[i];
         }
     }
     // x_k * scale * w_k (or * (1 + w_k)): the fused RMSNorm, same operation
@@ -141,7 +148,7 @@ template <int EPL> struct XFrag<_Float16, EPL> {
     h2_t v[EPL / 2];
     __device__ __forceinline__ void load_norm(const void*, const float*, int, float, int) {}  // host rejects
     __device__ __forceinline__ void load_merge(const GemvArgs&, int) {}                      // host rejects
-    __device__ __forceinline__ void load(const void* x, int c) {
+    __device__ __forceinline__ void load(const void* x, int c, int = 0) {
         const _Float16* p = static_cast<const _Float16*>(x) + c;
 #pragma unroll
         for (int i = 0; i < EPL / 8; ++i) {
@@ -296,7 +303,7 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
                 else if (a.nw)
                     xf[u].load_norm(a.x, a.nw, col, 1.0f, a.plus_one);
                 else
-                    xf[u].load(a.x, col);
+                    xf[u].load(a.x, col, a.xr16);
 #pragma unroll
                 for (int m = 0; m < NMAT; ++m)
 #pragma unroll
@@ -452,7 +459,7 @@ __global__ void __launch_bounds__(NW * 64) gemv_rows_kernel(GemvArgs a) {
             if (a.nw)
                 xf[j].load_norm(a.x, a.nw, col[j], nscale, a.plus_one);
             else
-                xf[j].load(a.x, col[j]);
+                xf[j].load(a.x, col[j], a.xr16);
         }
     }
 
@@ -586,7 +593,7 @@ __global__ void __launch_bounds__(NW * 64) gemv_sweep_kernel(GemvArgs a) {
             if (a.nw)
                 xf[j].load_norm(a.x, a.nw, col[j], 1.0f, a.plus_one);
             else
-                xf[j].load(a.x, col[j]);
+                xf[j].load(a.x, col[j], a.xr16);
         }
     }
 
@@ -829,6 +836,20 @@ extern "C" int mxd_matvec_f16(const uint16_t* W, const void* x, int x_dtype, flo
     if (x_dtype == MXD_F16) return launch_epi<MXD_W_F16, _Float16>(a, epilogue, s);
     return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_matvec_f16: x_dtype %d", x_dtype);
 }
+
+namespace mxd {
+
+// int8 matvec with fp32 x rounded to fp16 as it is loaded (the per-row path
+// of the batched product with fp32 activations).
+int matvec_q8b32_xr16(const int8_t* Wq, const uint16_t* scales, const float* x, float* y, int M, int K, int epilogue,
+                      hipStream_t s) {
+    if (int rc = check_common("mxd_gemm_q8b32", Wq, x, y, M, K)) return rc;
+    GemvArgs a{{Wq, nullptr}, {scales, nullptr}, x, y, nullptr, M, K};
+    a.xr16 = 1;
+    return launch_epi<MXD_W_Q8B32, float>(a, epilogue, s);
+}
+
+}  // namespace mxd
 
 extern "C" int mxd_matvec_q8b32(const int8_t* Wq, const uint16_t* scales, const void* x, int x_dtype, float* y, int M,
                                 int K, int epilogue, const float* aux, mxd_stream_t stream) {

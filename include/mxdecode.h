@@ -279,13 +279,17 @@ int mxd_attention_paged(const float* q, int q_stride, const uint16_t* kpool, con
 /* Workspace bytes mxd_gemm_q8b32 needs (0 when it does not split K). */
 size_t mxd_gemm_q8b32_workspace_size(int n_rows, int M, int K);
 
-/* Y[b] (op)= dequant(Wq, scales) · X[b] for the n_rows rows of X (fp16
- * [n_rows][K]); Y fp32 [n_rows][M]; epilogue MXD_EPI_STORE or MXD_EPI_ADD.
- * From 16 rows on (and K % 128 == 0) this runs on the matrix cores; below, one
- * matvec per row. The batched-matrix counterpart of gemm_f16 / gemm_f16_add
- * (KL/kernels.metal:376-441), with int8 block-32 weights. */
-int mxd_gemm_q8b32(const int8_t* Wq, const uint16_t* scales, const uint16_t* X, float* Y, int n_rows, int M,
-                   int K, int epilogue, void* workspace, size_t ws_bytes, mxd_stream_t stream);
+/* Y[b] (op)= dequant(Wq, scales) · X[b] for the n_rows rows of X ([n_rows][K],
+ * x_dtype MXD_F16, or MXD_F32 rounded to nearest-even fp16 as it is loaded,
+ * the rounding of mxd_f32_to_f16); Y fp32 [n_rows][M]; epilogue
+ * MXD_EPI_STORE or MXD_EPI_ADD. From 16 rows on (and K % 128 == 0) this runs
+ * on the matrix cores; below, one matvec per row. The batched-matrix
+ * counterpart of gemm_f16 / gemm_f16_add (KL/kernels.metal:376-441), with
+ * int8 block-32 weights; fp32 X folds the reference's f32_to_f16 cast
+ * (KL/main.swift:448-454) into the product. */
+int mxd_gemm_q8b32(const int8_t* Wq, const uint16_t* scales, const void* X, int x_dtype, float* Y,
+                   int n_rows, int M, int K, int epilogue, void* workspace, size_t ws_bytes,
+                   mxd_stream_t stream);
 
 /* Workspace bytes mxd_gemm_gate_up_q8b32 needs (0 when it does not split K). */
 size_t mxd_gemm_gate_up_q8b32_workspace_size(int n_rows, int F, int K);

@@ -187,6 +187,27 @@ def test_gemm_q8b32(dev, rng, rows, M, K):
     assert rel_err(Yd.cpu().numpy(), Y0 + want) <= 1e-4
 
 
+@pytest.mark.parametrize("rows,K", [(5, 4096), (64, 4096), (64, 14336), (37, 640)])
+def test_gemm_q8b32_fp32_activations(dev, rng, rows, K):
+    """fp32 X is rounded to fp16 as the product loads it: on the matrix cores
+    (the unrolled kernel, the runtime loop) the result equals the product of the
+    fp16-cast X bit for bit; the per-row matvecs below 16 rows sum the same
+    fp16 values in another instruction order (fp32 FMAs, not packed dot
+    products); both match the oracle on fp16(X)."""
+    B = _bm()
+    M = 512
+    q, s = _qweights(rng, M, K)
+    X = rng.standard_normal((rows, K), dtype=F32) * 3
+    qd, sd = _d(q, dev), _d(s, dev)
+    got = B.gemm_q8b32(qd, sd, _d(X, dev)).cpu().numpy()
+    cast = B.gemm_q8b32(qd, sd, _d(X.astype(F16), dev)).cpu().numpy()
+    if rows >= 16:
+        assert np.array_equal(got, cast)
+    else:
+        assert rel_err(got, cast) <= 1e-6
+    assert rel_err(got, obatch.gemm_q8b32(q, s, X.astype(F16))) <= 1e-4
+
+
 @pytest.mark.parametrize("nch,splits", [(4, 0), (8, 0), (16, 0), (32, 0), (1, 1), (1, 3), (1, 32)])
 def test_gemm_q8b32_k_splits(dev, rng, nch, splits):
     """Every chunk count of the unrolled kernel (8, 4, 2 and 1 K splits at K =
