@@ -558,8 +558,10 @@ bool use_mfma(int wf, int n_rows, int K) {
 }
 
 // Chunks per workgroup of the unrolled kernel: the largest of 32, 16, 8, 4
-// that divides K's chunk count and still gives at least 192 workgroups (3/4 of
-// the CUs); the GM_NCH tunable (4, 8, 16, 32) forces one, GM_NCH = 1 the runtime
+// that divides K's chunk count and still gives at least 128 workgroups (half
+// the CUs: fewer, longer splits write fewer partials; the 4096 x 4096 product
+// at 64 rows ran 15.7 us as 4 splits of 8 chunks against 16.6 us as 8 of 4);
+// the GM_NCH tunable (4, 8, 16, 32) forces one, GM_NCH = 1 the runtime
 // loop; 0 (the runtime loop) when none divides. Fewer, longer splits also save
 // the partials and their reduction (gate/up at 64 rows: 62.2 us with one split
 // of 32 chunks against 65.1 us with two of 16).
@@ -575,7 +577,7 @@ int pick_nch(int wf, int n_rows, int M, int K, int nmat) {
     for (int nch : {32, 16, 8, 4}) {
         if (nck % nch) continue;
         if (!best) best = nch;
-        if (tiles * (nck / nch) >= 192) return nch;
+        if (tiles * (nck / nch) >= 128) return nch;
         best = nch;
     }
     return best;
