@@ -115,7 +115,7 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_gemm_gate_up_q8b32_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "mxd_gemm_gate_up_q8b32": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
     "mxd_gemm_f16_workspace_size": (c_size_t, [c_int, c_int, c_int]),
-    "mxd_gemm_f16": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
+    "mxd_gemm_f16": (c_int, [P, P, c_int, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
     "mxd_gemm_gate_up_f16_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "mxd_gemm_gate_up_f16": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
 }

@@ -83,11 +83,12 @@ struct mxd_engine {
     int att_splits = 0;
     void* am_ws = nullptr;
     hipGraphExec_t graph = nullptr;
-    // prefill chunk buffers: rows x {dim f32, dim f16, qkv f32, q f32, q f16,
-    // ffn f32, ffn f16}, and the products' split-K workspace
+    // prefill chunk buffers: rows x {dim f32, dim f16, qkv f32, q f32, ffn f32}
+    // (the products round fp32 rows to fp16 as they load them), and the
+    // products' split-K workspace
     int max_rows = 0;
     float *bx = nullptr, *bqkv = nullptr, *batt = nullptr, *bh = nullptr;
-    uint16_t *bxn = nullptr, *batt16 = nullptr, *bh16 = nullptr;
+    uint16_t* bxn = nullptr;
     void* gm_ws = nullptr;
     size_t gm_ws_bytes = 0;
 
@@ -207,17 +208,17 @@ int encode_prefill(mxd_engine* e, int pos0, int T, bool sample) {
     for (int l = 0; l < c.n_layers; ++l) {
         const LayerPtrs& Lp = e->L[l];
         if ((rc = mxd_rmsnorm(e->bx, Lp.attn_norm, e->bxn, MXD_F16, T, D, c.rms_eps, c.norm_plus_one, ms))) return rc;
-        if ((rc = mxd_gemm_f16(Lp.wqkv, e->bxn, e->bqkv, T, QKV, D, MXD_EPI_STORE, ws, wsb, ms))) return rc;
+        if ((rc = mxd_gemm_f16(Lp.wqkv, e->bxn, MXD_F16, e->bqkv, T, QKV, D, MXD_EPI_STORE, ws, wsb, ms))) return rc;
         if ((rc = mxd_rope_kv(e->bqkv, Lp.kc, Lp.vc, e->invf, NH, NKV, HD, e->max_ctx, pos0, T, ms))) return rc;
         if ((rc = mxd_attention_prefill(e->bqkv, QKV, Lp.kc, Lp.vc, e->batt, QD, NH, NKV, HD, e->max_ctx, pos0, T,
                                         ascale, ms)))
             return rc;
-        if ((rc = mxd_f32_to_f16(e->batt, e->batt16, (size_t)T * QD, ms))) return rc;
-        if ((rc = mxd_gemm_f16(Lp.wo, e->batt16, e->bx, T, D, QD, MXD_EPI_ADD, ws, wsb, ms))) return rc;
+        // the fp32 attention rows and hidden rows are rounded to fp16 as the
+        // products load them (the reference's attHalf / hidHalf casts)
+        if ((rc = mxd_gemm_f16(Lp.wo, e->batt, MXD_F32, e->bx, T, D, QD, MXD_EPI_ADD, ws, wsb, ms))) return rc;
         if ((rc = mxd_rmsnorm(e->bx, Lp.ffn_norm, e->bxn, MXD_F16, T, D, c.rms_eps, c.norm_plus_one, ms))) return rc;
         if ((rc = mxd_gemm_gate_up_f16(Lp.wgate, Lp.wup, e->bxn, e->bh, T, F, D, c.act, ws, wsb, ms))) return rc;
-        if ((rc = mxd_f32_to_f16(e->bh, e->bh16, (size_t)T * F, ms))) return rc;
-        if ((rc = mxd_gemm_f16(Lp.wdown, e->bh16, e->bx, T, D, F, MXD_EPI_ADD, ws, wsb, ms))) return rc;
+        if ((rc = mxd_gemm_f16(Lp.wdown, e->bh, MXD_F32, e->bx, T, D, F, MXD_EPI_ADD, ws, wsb, ms))) return rc;
     }
     if (!sample) return MXD_OK;
     // Only the last row needs logits: it takes the decode path's head.
@@ -296,8 +297,8 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
     const size_t B = (size_t)(e->max_rows = min(PREFILL_ROWS, max_ctx));
     e->gm_ws_bytes = prefill_ws_bytes(c, e->qkv_dim(), e->q_dim(), e->max_rows);
     const size_t o_bx = take(B * D * 4), o_bxn = take(B * D * 2), o_bqkv = take(B * e->qkv_dim() * 4);
-    const size_t o_batt = take(B * e->q_dim() * 4), o_batt16 = take(B * e->q_dim() * 2);
-    const size_t o_bh = take(B * F * 4), o_bh16 = take(B * F * 2), o_gws = take(max(e->gm_ws_bytes, (size_t)16));
+    const size_t o_batt = take(B * e->q_dim() * 4);
+    const size_t o_bh = take(B * F * 4), o_gws = take(max(e->gm_ws_bytes, (size_t)16));
     std::vector<size_t> o_kc(c.n_layers), o_vc(c.n_layers);
     for (int l = 0; l < c.n_layers; ++l) {
         o_kc[l] = take(kv_bytes);
@@ -328,9 +329,7 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
     e->bxn = reinterpret_cast<uint16_t*>(a + o_bxn);
     e->bqkv = reinterpret_cast<float*>(a + o_bqkv);
     e->batt = reinterpret_cast<float*>(a + o_batt);
-    e->batt16 = reinterpret_cast<uint16_t*>(a + o_batt16);
     e->bh = reinterpret_cast<float*>(a + o_bh);
-    e->bh16 = reinterpret_cast<uint16_t*>(a + o_bh16);
     e->gm_ws = a + o_gws;
     e->embed = wptr<uint16_t>(e, "embed");
     e->final_norm = wptr<float>(e, "final_norm");

@@ -676,8 +676,8 @@ extern "C" int mxd_gemm_q8b32(const int8_t* Wq, const uint16_t* scales, const vo
         for (int b = 0; b < n_rows; ++b) {
             const void* xb = static_cast<const char*>(X) + (size_t)b * K * xesz;
             const int rc = x_dtype == MXD_F32
-                               ? mxd::matvec_q8b32_xr16(Wq, scales, static_cast<const float*>(xb), Y + (size_t)b * M,
-                                                        M, K, epilogue, mxd::as_stream(stream))
+                               ? mxd::matvec_xr16(MXD_W_Q8B32, Wq, scales, static_cast<const float*>(xb),
+                                                  Y + (size_t)b * M, M, K, epilogue, mxd::as_stream(stream))
                                : mxd_matvec_q8b32(Wq, scales, xb, MXD_F16, Y + (size_t)b * M, M, K, epilogue, nullptr,
                                                   stream);
             if (rc) return rc;
@@ -749,27 +749,38 @@ int check_f16(const void* W, const void* X, const void* Y, int n_rows, int M, in
 
 }  // namespace
 
-extern "C" int mxd_gemm_f16(const uint16_t* W, const uint16_t* X, float* Y, int n_rows, int M, int K, int epilogue,
-                            void* workspace, size_t ws_bytes, mxd_stream_t stream) {
+extern "C" int mxd_gemm_f16(const uint16_t* W, const void* X, int x_dtype, float* Y, int n_rows, int M, int K,
+                            int epilogue, void* workspace, size_t ws_bytes, mxd_stream_t stream) {
     if (int rc = check_f16(W, X, Y, n_rows, M, K, "mxd_gemm_f16")) return rc;
     MXD_REQUIRE(epilogue == MXD_EPI_STORE || epilogue == MXD_EPI_ADD, MXD_ERR_INVALID_ARG,
                 "mxd_gemm_f16: epilogue %d (store or add)", epilogue);
-    if (!use_mfma(MXD_W_F16, n_rows, K)) {  // few rows or K % 512: one matvec per row
+    MXD_REQUIRE(x_dtype == MXD_F16 || x_dtype == MXD_F32, MXD_ERR_INVALID_ARG, "mxd_gemm_f16: x_dtype %d", x_dtype);
+    const size_t xesz = x_dtype == MXD_F32 ? 4 : 2;
+    if (!use_mfma(MXD_W_F16, n_rows, K)) {  // few rows or K % 512: one matvec per row (fp32 X rounded the same way)
         for (int b = 0; b < n_rows; ++b) {
-            if (int rc = mxd_matvec_f16(W, X + (size_t)b * K, MXD_F16, Y + (size_t)b * M, M, K, epilogue, nullptr,
-                                        stream))
-                return rc;
+            const void* xb = static_cast<const char*>(X) + (size_t)b * K * xesz;
+            const int rc = x_dtype == MXD_F32
+                               ? mxd::matvec_xr16(MXD_W_F16, W, nullptr, static_cast<const float*>(xb),
+                                                  Y + (size_t)b * M, M, K, epilogue, mxd::as_stream(stream))
+                               : mxd_matvec_f16(W, xb, MXD_F16, Y + (size_t)b * M, M, K, epilogue, nullptr, stream);
+            if (rc) return rc;
         }
         return MXD_OK;
     }
     GemmArgs a{};
     a.W[0] = a.W[1] = reinterpret_cast<const int8_t*>(W);
-    a.X = X;
+    a.X = static_cast<const uint16_t*>(X);
+    a.Xf = static_cast<const float*>(X);
     a.Y = Y;
     a.n_rows = n_rows;
     a.M = M;
     a.K = K;
     hipStream_t s = mxd::as_stream(stream);
+    if (x_dtype == MXD_F32) {
+        if (epilogue == MXD_EPI_ADD)
+            return launch_gemm<MXD_W_F16, 1, MXD_EPI_ADD, true>(a, workspace, ws_bytes, s, "mxd_gemm_f16");
+        return launch_gemm<MXD_W_F16, 1, MXD_EPI_STORE, true>(a, workspace, ws_bytes, s, "mxd_gemm_f16");
+    }
     if (epilogue == MXD_EPI_ADD) return launch_gemm<MXD_W_F16, 1, MXD_EPI_ADD>(a, workspace, ws_bytes, s, "mxd_gemm_f16");
     return launch_gemm<MXD_W_F16, 1, MXD_EPI_STORE>(a, workspace, ws_bytes, s, "mxd_gemm_f16");
 }

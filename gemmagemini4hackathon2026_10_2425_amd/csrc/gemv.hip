@@ -839,14 +839,15 @@ extern "C" int mxd_matvec_f16(const uint16_t* W, const void* x, int x_dtype, flo
 
 namespace mxd {
 
-// int8 matvec with fp32 x rounded to fp16 as it is loaded (the per-row path
-// of the batched product with fp32 activations).
-int matvec_q8b32_xr16(const int8_t* Wq, const uint16_t* scales, const float* x, float* y, int M, int K, int epilogue,
-                      hipStream_t s) {
-    if (int rc = check_common("mxd_gemm_q8b32", Wq, x, y, M, K)) return rc;
-    GemvArgs a{{Wq, nullptr}, {scales, nullptr}, x, y, nullptr, M, K};
+// fp16 or int8 matvec with fp32 x rounded to fp16 as it is loaded (the
+// per-row path of the batched products with fp32 activations).
+int matvec_xr16(int w_format, const void* W, const uint16_t* scales, const float* x, float* y, int M, int K,
+                int epilogue, hipStream_t s) {
+    if (int rc = check_common("matvec (fp32 x rounded to fp16)", W, x, y, M, K)) return rc;
+    GemvArgs a{{W, nullptr}, {scales, nullptr}, x, y, nullptr, M, K};
     a.xr16 = 1;
-    return launch_epi<MXD_W_Q8B32, float>(a, epilogue, s);
+    if (w_format == MXD_W_Q8B32) return launch_epi<MXD_W_Q8B32, float>(a, epilogue, s);
+    return launch_epi<MXD_W_F16, float>(a, epilogue, s);
 }
 
 }  // namespace mxd

@@ -19,8 +19,9 @@ int rope_kv_dev(float* qkv, uint16_t* kcache, uint16_t* vcache, const float* inv
 int argmax_dev(const float* logits, int32_t* tokens, int N, int out_idx, int32_t* pos_dev, bool advance,
                void* workspace, hipStream_t s);
 
-// int8 block-32 matvec whose fp32 x is rounded to fp16 as it is loaded.
-int matvec_q8b32_xr16(const int8_t* Wq, const uint16_t* scales, const float* x, float* y, int M, int K, int epilogue,
-                      hipStream_t s);
+// fp16 (MXD_W_F16) or int8 block-32 (MXD_W_Q8B32) matvec whose fp32 x is
+// rounded to fp16 as it is loaded.
+int matvec_xr16(int w_format, const void* W, const uint16_t* scales, const float* x, float* y, int M, int K,
+                int epilogue, hipStream_t s);
 
 }  // namespace mxd

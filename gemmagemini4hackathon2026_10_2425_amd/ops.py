@@ -354,13 +354,14 @@ def gemm_workspace(n_rows: int, M: int, K: int, glu: bool = False, device="cuda"
 
 
 def gemm_f16(W, X, Y=None, epilogue: str = "store", workspace=None) -> torch.Tensor:
-    """Y[b] (op)= W . X[b]: fp16 W [M, K], X fp16 [B, K], Y fp32 [B, M]
-    (gemm_f16 / gemm_f16_add of the reference's prefill)."""
+    """Y[b] (op)= W . X[b]: fp16 W [M, K], X fp16 or fp32 [B, K] (fp32 is
+    rounded to fp16 as it is loaded), Y fp32 [B, M] (gemm_f16 / gemm_f16_add
+    of the reference's prefill)."""
     _on_gpu(W, X)
     M, K = W.shape
     _need(W.dtype == torch.float16 and W.is_contiguous(), "gemm_f16: W float16 [M, K]")
-    _need(X.dtype == torch.float16 and X.dim() == 2 and X.shape[1] == K and X.is_contiguous(),
-          "gemm_f16: X float16 [B, K]")
+    _need(X.dtype in (torch.float16, torch.float32) and X.dim() == 2 and X.shape[1] == K and X.is_contiguous(),
+          "gemm_f16: X float16 or float32 [B, K]")
     B = X.shape[0]
     if Y is None:
         _need(epilogue == "store", "gemm_f16: epilogue 'add' needs Y")
@@ -368,8 +369,8 @@ def gemm_f16(W, X, Y=None, epilogue: str = "store", workspace=None) -> torch.Ten
     _need(Y.is_contiguous() and Y.dtype == torch.float32 and Y.numel() == B * M, "gemm_f16: Y float32 [B, M]")
     if workspace is None:
         workspace = gemm_workspace(B, M, K, False, X.device)
-    call("mxd_gemm_f16", _ptr(W), _ptr(X), _ptr(Y), B, M, K, _EPI[epilogue], _ptr(workspace), workspace.numel(),
-         _stream())
+    call("mxd_gemm_f16", _ptr(W), _ptr(X), _xdtype(X), _ptr(Y), B, M, K, _EPI[epilogue], _ptr(workspace),
+         workspace.numel(), _stream())
     return Y
 
 

@@ -303,14 +303,15 @@ int mxd_gemm_gate_up_q8b32(const int8_t* Wg, const uint16_t* sg, const int8_t* W
 /* Workspace bytes mxd_gemm_f16 needs (0 when it does not split K). */
 size_t mxd_gemm_f16_workspace_size(int n_rows, int M, int K);
 
-/* Y[b] (op)= W · X[b] for fp16 W [M][K] and the n_rows fp16 rows of X
- * [n_rows][K]; Y fp32 [n_rows][M]; epilogue MXD_EPI_STORE or MXD_EPI_ADD; fp32
+/* Y[b] (op)= W · X[b] for fp16 W [M][K] and the n_rows rows of X [n_rows][K]
+ * (x_dtype MXD_F16, or MXD_F32 rounded to nearest-even fp16 as it is loaded);
+ * Y fp32 [n_rows][M]; epilogue MXD_EPI_STORE or MXD_EPI_ADD; fp32
  * accumulation. From 16 rows on (and K % 512 == 0) this runs on the matrix
  * cores; below, one matvec per row. Replaces gemm_f16 / gemm_f16_add
  * (KL/kernels.metal:376-441; host gemm KL/main.swift:397-410), the prefill
- * products. */
-int mxd_gemm_f16(const uint16_t* W, const uint16_t* X, float* Y, int n_rows, int M, int K, int epilogue,
-                 void* workspace, size_t ws_bytes, mxd_stream_t stream);
+ * products; fp32 X folds the f32_to_f16 cast before them (KL/main.swift:448-454). */
+int mxd_gemm_f16(const uint16_t* W, const void* X, int x_dtype, float* Y, int n_rows, int M, int K,
+                 int epilogue, void* workspace, size_t ws_bytes, mxd_stream_t stream);
 
 /* Workspace bytes mxd_gemm_gate_up_f16 needs (0 when it does not split K). */
 size_t mxd_gemm_gate_up_f16_workspace_size(int n_rows, int F, int K);

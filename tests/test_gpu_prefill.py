@@ -60,6 +60,26 @@ def test_gemm_f16(dev, rng, B, M, K, epi):
     _close(Y.cpu().numpy(), want)
 
 
+@pytest.mark.parametrize("B,K", [(7, 2048), (64, 2048), (256, 16384), (40, 520)])
+def test_gemm_f16_fp32_activations(dev, rng, B, K):
+    """fp32 X is rounded to fp16 as the product loads it: on the matrix cores
+    the result equals the product of the fp16-cast X bit for bit; the per-row
+    matvecs (below 16 rows, or K % 512 != 0) sum the same fp16 values in
+    another instruction order; both match the oracle on fp16(X)."""
+    ops = _ops()
+    M = 384
+    W = (rng.standard_normal((M, K), dtype=np.float32) * 0.02).astype(np.float16)
+    X = rng.standard_normal((B, K), dtype=np.float32) * 3
+    Wd = torch.from_numpy(W).to(dev)
+    got = ops.gemm_f16(Wd, torch.from_numpy(X).to(dev)).cpu().numpy()
+    cast = ops.gemm_f16(Wd, torch.from_numpy(X.astype(np.float16)).to(dev)).cpu().numpy()
+    if B >= 16 and K % 512 == 0:
+        assert np.array_equal(got, cast)
+    else:
+        assert np.abs(got - cast).max() <= 1e-6 * np.abs(cast).max()
+    _close(got, ref.matvec(W, X.astype(np.float16).T).T)
+
+
 @pytest.mark.parametrize("nch", [4, 8, 16, 32])
 def test_gemm_f16_k_splits(dev, rng, nch):
     """Every chunk count per workgroup, so K splits into 8..1 pieces whose
