@@ -746,11 +746,19 @@ int launch(const GemvArgs& a, hipStream_t s) {
     // waves, 4 workgroups per CU) and small single matrices without a RoPE
     // epilogue (the 2048 x 2048 o projection: 3.95 vs 4.63 us, 4 waves, 8 per
     // CU).
+    //
+    // A vocabulary-sized matrix of short fp16 rows with the fused norm (the
+    // LM head, 256000 x 2048) takes the grid sweep: each wave forms its
+    // x * w_norm fragment once for the whole kernel, and each workgroup the
+    // rsqrt scale once, instead of once per tile of rows.
+    // Back-to-back on MI355X: 157.4 us against 171.7 (row tiles, 8 rows x 4
+    // waves) and 161.0 (row streaming).
     const bool short_f16 = WF == MXD_W_F16 && nch <= 4 && OP != EPI_ROPE_KV;
     const bool rows_glu = short_f16 && NMAT == 2;
     const bool rows_small = short_f16 && NMAT == 1 && a.M <= 4096;
-    const int algo =
-        mxd::tunable("MV_ALGO", (nch > 8 && nch <= RS_MAX_CHUNKS) || rows_glu || rows_small ? 1 : 0);
+    const bool sweep_vocab = short_f16 && NMAT == 1 && a.nw != nullptr && a.M >= 65536;
+    const int algo = mxd::tunable(
+        "MV_ALGO", sweep_vocab ? 2 : (nch > 8 && nch <= RS_MAX_CHUNKS) || rows_glu || rows_small ? 1 : 0);
     if (algo == 1) {
         MXD_REQUIRE(nch <= RS_MAX_CHUNKS, MXD_ERR_UNSUPPORTED, "matvec: row streaming needs K <= %d",
                     RS_MAX_CHUNKS * CH);
