@@ -123,6 +123,41 @@ def gemv_f16_leg(steps: int, warmup: int, dev) -> dict:
     }
 
 
+def gemv_size_fit_leg(steps: int, warmup: int, dev) -> dict:
+    """The fp16 GEMV (fp16 x, K = 4096) at 7168, 14336 and 28672 rows (58.7,
+    117.4 and 234.9 MB of weights, rotated copies as in the headline leg) and a
+    least-squares fit of time = t0 + bytes / marginal bandwidth. The marginal
+    bandwidth is the rate at which the kernel streams once it runs; t0 is the
+    fixed cost of one launch (dispatch, the first HBM round trip, the drain),
+    which caps the fraction of peak any single call of a given size can reach."""
+    import torch
+
+    from gemmagemini4hackathon2026_10_2425_amd import ops
+
+    K = 4096
+    pts = []
+    for M in (7168, 14336, 28672):
+        nb = M * K * 2 + K * 2 + M * 4
+        R = _copies(M * K * 2)
+        mats = [ops.fill_normal((M, K), torch.float16, 7, 200 + i, 0.02, dev) for i in range(R)]
+        x = ops.fill_normal((K,), torch.float16, 7, 90, 1.0, dev)
+        y = torch.empty(M, dtype=torch.float32, device=dev)
+        st = _stream()
+        calls = [_bound("mxd_matvec_f16", W.data_ptr(), x.data_ptr(), 1, y.data_ptr(), M, K, 0, None, st)
+                 for W in mats]
+        ms = _events_time(lambda i: calls[i % R](), steps, warmup)
+        pts.append((nb, ms * 1e3))
+        del mats
+    n = len(pts)
+    mb, mt = sum(b for b, _ in pts) / n, sum(t for _, t in pts) / n
+    slope = sum((b - mb) * (t - mt) for b, t in pts) / sum((b - mb) ** 2 for b, _ in pts)  # us per byte
+    return {
+        "points": [{"bytes": b, "us": t, "gbs": b / t / 1e3} for b, t in pts],
+        "t0_us": mt - slope * mb,
+        "marginal_gbs": 1e-3 / slope,
+    }
+
+
 def gemv_q8_leg(steps: int, warmup: int, dev) -> dict:
     import numpy as np
     import torch
@@ -320,7 +355,8 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemv_f16",
-                    choices=["gemv_f16", "gemv_q8", "attention", "decode", "prefill", "ragged_layer", "copy"])
+                    choices=["gemv_f16", "gemv_q8", "gemv_size_fit", "attention", "decode", "prefill", "ragged_layer",
+                             "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-detail", action="store_true", help="skip the int8 / attention detail legs")
     args = ap.parse_args(argv)
@@ -342,6 +378,7 @@ def main(argv=None) -> int:
     detail = {}
     if args.workload != "gemv_f16":
         legs = {"gemv_q8": lambda: gemv_q8_leg(args.steps, args.warmup, dev),
+                "gemv_size_fit": lambda: gemv_size_fit_leg(args.steps, args.warmup, dev),
                 "attention": lambda: attention_leg(args.steps, args.warmup, dev),
                 "decode": decode_leg,
                 "prefill": prefill_leg,
@@ -353,6 +390,9 @@ def main(argv=None) -> int:
     log("fp16 GEMV leg")
     g = gemv_f16_leg(args.steps, args.warmup, dev)
     if not args.no_detail:
+        log("fp16 GEMV size fit leg")
+        detail["gemv_f16_size_fit"] = gemv_size_fit_leg(args.steps, args.warmup, dev)
+        torch.cuda.empty_cache()
         log("int8 GEMV leg")
         detail["gemv_q8b32"] = gemv_q8_leg(args.steps, args.warmup, dev)
         log("attention leg")
