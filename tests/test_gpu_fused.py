@@ -41,8 +41,11 @@ def _f16_close(got, want):
 
 
 @pytest.mark.parametrize("plus_one", [True, False])
-@pytest.mark.parametrize("M,K", [(2048, 2048), (256000, 2048), (37, 4096)])
+@pytest.mark.parametrize("M,K", [(2048, 2048), (256000, 2048), (70001, 2048), (65536, 1024), (37, 4096)])
 def test_matvec_rmsnorm(dev, rng, M, K, plus_one):
+    """Tiled rows (small M) and, from 65536 rows of up to 4 KiB, the grid
+    sweep: rows left over past the last full round of workgroups (70001) and
+    rows shorter than the workgroup's waves (K = 1024: two chunks, four waves)."""
     L = _lib()
     W = (rng.standard_normal((M, K), dtype=np.float32) * 0.02).astype(np.float16)
     x = rng.standard_normal(K, dtype=np.float32) * 4
