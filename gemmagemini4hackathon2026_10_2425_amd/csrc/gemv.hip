@@ -757,8 +757,15 @@ int launch(const GemvArgs& a, hipStream_t s) {
     const bool rows_glu = short_f16 && NMAT == 2;
     const bool rows_small = short_f16 && NMAT == 1 && a.M <= 4096;
     const bool sweep_vocab = short_f16 && NMAT == 1 && a.nw != nullptr && a.M >= 65536;
-    const int algo = mxd::tunable(
-        "MV_ALGO", sweep_vocab ? 2 : (nch > 8 && nch <= RS_MAX_CHUNKS) || rows_glu || rows_small ? 1 : 0);
+    // int8 rows of up to 4 chunks against fp16 x (the 14336 x 4096 FFN matrix)
+    // stream by rows, 4 waves and 8 workgroups per CU: graph-replayed, three
+    // alternating rounds, 12.04-12.07 us against 12.58-12.76 (8-row tiles).
+    const bool rows_q8 = WF == MXD_W_Q8B32 && std::is_same<XT, _Float16>::value && NMAT == 1 &&
+                         OP != EPI_ROPE_KV && nch <= 4 && a.M >= 8192;
+    const int algo = mxd::tunable("MV_ALGO", sweep_vocab ? 2
+                                             : (nch > 8 && nch <= RS_MAX_CHUNKS) || rows_glu || rows_small || rows_q8
+                                                 ? 1
+                                                 : 0);
     if (algo == 1) {
         MXD_REQUIRE(nch <= RS_MAX_CHUNKS, MXD_ERR_UNSUPPORTED, "matvec: row streaming needs K <= %d",
                     RS_MAX_CHUNKS * CH);
