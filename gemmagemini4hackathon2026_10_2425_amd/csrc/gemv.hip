@@ -762,10 +762,13 @@ int launch(const GemvArgs& a, hipStream_t s) {
     // alternating rounds, 12.04-12.07 us against 12.58-12.76 (8-row tiles).
     const bool rows_q8 = WF == MXD_W_Q8B32 && std::is_same<XT, _Float16>::value && NMAT == 1 &&
                          OP != EPI_ROPE_KV && nch <= 4 && a.M >= 8192;
-    const int algo = mxd::tunable("MV_ALGO", sweep_vocab ? 2
-                                             : (nch > 8 && nch <= RS_MAX_CHUNKS) || rows_glu || rows_small || rows_q8
-                                                 ? 1
-                                                 : 0);
+    const bool rows_long = nch > 8 && nch <= RS_MAX_CHUNKS;
+    int algo_default = 0;
+    if (sweep_vocab)
+        algo_default = 2;
+    else if (rows_long || rows_glu || rows_small || rows_q8)
+        algo_default = 1;
+    const int algo = mxd::tunable("MV_ALGO", algo_default);
     if (algo == 1) {
         MXD_REQUIRE(nch <= RS_MAX_CHUNKS, MXD_ERR_UNSUPPORTED, "matvec: row streaming needs K <= %d",
                     RS_MAX_CHUNKS * CH);
