@@ -11,10 +11,12 @@ Modules:
     hashrng  -- NumPy restatement of the synthetic-weight generator
     ops      -- NumPy restatement of each operator, fp64 inside an op
     model    -- the Gemma-2B-shaped decode step composed from ops (small configs)
+    batch    -- one Llama-shaped int8 layer stepping a ragged batch
     native   -- ctypes binding of the C restatement (liboracle.so) for
                 full-size decode runs and CPU timing
 
 How each function is pinned (closed forms, library routines, brute force,
-HF transformers' Gemma) is listed in tests/test_oracle.py; every oracle
-function has at least one such check.
+HF transformers' Gemma model and Llama decoder layer, the llama3 rope
+initialiser) is in tests/test_oracle.py; every oracle function has at least
+one such check.
 """

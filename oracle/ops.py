@@ -88,6 +88,24 @@ def inv_freq(head_dim: int, theta: float) -> np.ndarray:
     return (1.0 / theta ** (2.0 * i / head_dim)).astype(np.float32)
 
 
+def inv_freq_llama3(head_dim: int, theta: float, factor: float, low_freq_factor: float, high_freq_factor: float,
+                    original_max_positions: int) -> np.ndarray:
+    """Llama-3 frequency scaling of inv_freq, in double, stored as fp32
+    (KL/main.swift:96-107): a frequency whose wavelength 2 pi / f is shorter
+    than original / high_freq_factor is kept, one longer than
+    original / low_freq_factor is divided by factor, and in between the two
+    are blended linearly in original / wavelength."""
+    i = np.arange(head_dim // 2, dtype=F64)
+    f = 1.0 / theta ** (2.0 * i / head_dim)
+    wavelen = 2.0 * math.pi / f
+    lo_wave = original_max_positions / low_freq_factor
+    hi_wave = original_max_positions / high_freq_factor
+    t = (original_max_positions / wavelen - low_freq_factor) / (high_freq_factor - low_freq_factor)
+    blended = (1.0 - t) * f / factor + t * f
+    out = np.where(wavelen < hi_wave, f, np.where(wavelen > lo_wave, f / factor, blended))
+    return out.astype(np.float32)
+
+
 def rope(v: np.ndarray, pos: int, invf: np.ndarray) -> np.ndarray:
     """rotate_half RoPE of one head vector: pairs (i, i + hd/2) rotated by
     ang = fp32(pos) * inv_freq[i] (the angle is an fp32 product, as on the
@@ -103,8 +121,9 @@ def rope(v: np.ndarray, pos: int, invf: np.ndarray) -> np.ndarray:
 def rope_kv(qkv_row: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, invf: np.ndarray, n_heads: int,
             n_kv: int, pos: int) -> np.ndarray:
     """One qkv row [q NH*hd | k NKV*hd | v NKV*hd] at position pos: returns the
-    rotated q (fp64) and appends fp16(rotated k) / fp16(v) to the caches
-    (KL/kernels.metal:189-224). kcache, vcache [n_kv, ctx, hd]."""
+    rotated q (fp64) and appends the rotated k and v to the caches, rounded to
+    the caches' dtype: fp16 as on the device (KL/kernels.metal:189-224), or
+    unrounded into fp64 caches. kcache, vcache [n_kv, ctx, hd]."""
     hd = kcache.shape[2]
     row = np.asarray(qkv_row, dtype=F64)
     q = row[: n_heads * hd].reshape(n_heads, hd)
@@ -112,8 +131,8 @@ def rope_kv(qkv_row: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, invf: n
     v = row[(n_heads + n_kv) * hd :].reshape(n_kv, hd)
     qr = rope(q, pos, invf)
     kr = rope(k, pos, invf)
-    kcache[:, pos, :] = kr.astype(np.float16)
-    vcache[:, pos, :] = v.astype(np.float16)
+    kcache[:, pos, :] = kr.astype(kcache.dtype)
+    vcache[:, pos, :] = v.astype(vcache.dtype)
     return qr.reshape(-1)
 
 

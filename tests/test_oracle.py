@@ -11,12 +11,13 @@ HF transformers' Gemma on a tiny config (tests/golden/hf_gemma_tiny.npz).
 from __future__ import annotations
 
 import math
+from pathlib import Path
 
 import numpy as np
 import pytest
 import torch
 
-from oracle import hashrng, model as om, native, ops
+from oracle import batch as ob, hashrng, model as om, native, ops
 
 # ---------------------------------------------------------------- generator
 
@@ -195,6 +196,27 @@ def test_inv_freq_definition():
     assert f[63] == np.float32(1.0 / 500000.0 ** (126 / 128))
 
 
+def test_inv_freq_llama3_matches_hf():
+    """Llama-3 frequency scaling (Llama-3.2-1B's rope_scaling) against
+    transformers' llama3 rope initialiser (fp32); the Llama-3.2-1B head_dim 64
+    puts frequencies in all three bands (kept, divided, blended)."""
+    from transformers import LlamaConfig
+    from transformers.modeling_rope_utils import ROPE_INIT_FUNCTIONS
+
+    rp = {"rope_type": "llama3", "rope_theta": 500000.0, "factor": 32.0, "low_freq_factor": 1.0,
+          "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}
+    hc = LlamaConfig(hidden_size=2048, num_attention_heads=32, head_dim=64, max_position_embeddings=131072,
+                     rope_parameters=rp)
+    want, _ = ROPE_INIT_FUNCTIONS["llama3"](hc, "cpu")
+    got = ops.inv_freq_llama3(64, 500000.0, 32.0, 1.0, 4.0, 8192)
+    assert got.dtype == np.float32
+    assert np.abs(want.numpy().astype(np.float64) / got - 1).max() < 1e-6
+    base = ops.inv_freq(64, 500000.0)
+    kept, divided = got == base, np.isclose(got, base / 32, rtol=1e-7)
+    assert kept.sum() >= 8 and divided.sum() >= 8 and (~kept & ~divided).sum() >= 2
+    assert np.all(np.diff(got) < 0)  # still strictly decreasing
+
+
 def test_rope_kv_appends_fp16(rng):
     nh, nkv, hd, ctx = 4, 2, 128, 16
     kc = np.zeros((nkv, ctx, hd), np.float16)
@@ -351,3 +373,99 @@ def test_tensor_ids_are_distinct(name):
     ids = {om.tensor_id(n) for n in om.weight_shapes(om.GEMMA_2B)}
     assert len(ids) == len(om.weight_shapes(om.GEMMA_2B))
     assert om.tensor_id(name) in ids
+
+
+# ---------------------------------------------------------------- ragged-batch layer (oracle.batch)
+
+
+def test_batch_dequant_closed_forms():
+    q = np.zeros((2, 64), np.int8)
+    q[0, :32] = np.arange(-16, 16)
+    q[1, 32:] = -127
+    s = np.array([[0.5, 3.0], [2.0, 0.25]], np.float16)
+    d = ob.dequant(q, s)
+    assert np.array_equal(d[0, :32], np.arange(-16, 16) * 0.5) and not d[0, 32:].any()
+    assert not d[1, :32].any() and np.all(d[1, 32:] == -127 * 0.25)
+
+
+def test_batch_gemm_q8b32_rows_equal_matvec(rng):
+    W = rng.standard_normal((23, 320)).astype(np.float32) * 0.02
+    q, s = ops.quantize_q8b32(W)
+    X = rng.standard_normal((5, 320)).astype(np.float16)
+    Y = ob.gemm_q8b32(q, s, X)
+    assert Y.shape == (5, 23)
+    for b in range(5):
+        assert np.allclose(Y[b], ops.matvec_q8b32(q, s, X[b]), rtol=1e-13, atol=1e-15), b
+
+
+def test_batch_gemm_q8b32_brute_force(rng):
+    q = rng.integers(-127, 128, (3, 64)).astype(np.int8)
+    s = (rng.random((3, 2)) * 0.01).astype(np.float16)
+    X = rng.standard_normal((2, 64)).astype(np.float32)
+    want = [[math.fsum(float(q[r, k]) * float(s[r, k // 32]) * float(X[b, k]) for k in range(64)) for r in range(3)]
+            for b in range(2)]
+    assert np.allclose(ob.gemm_q8b32(q, s, X), want, rtol=0, atol=1e-15)
+
+
+def test_batch_gate_up_rows_equal_per_row(rng):
+    qg, sg = ops.quantize_q8b32(rng.standard_normal((16, 96)).astype(np.float32) * 0.05)
+    qu, su = ops.quantize_q8b32(rng.standard_normal((16, 96)).astype(np.float32) * 0.05)
+    X = rng.standard_normal((4, 96)).astype(np.float16)
+    for act in ("silu", "gelu_tanh"):
+        H = ob.gate_up_rows(qg, sg, qu, su, X, act)
+        for b in range(4):
+            want = ops.gate_up_q8b32(qg, sg, qu, su, X[b], act)
+            assert np.allclose(H[b], want, rtol=1e-12, atol=1e-15), (act, b)
+    assert not ob.gate_up_rows(np.zeros_like(qg), sg, qu, su, X, "silu").any()  # act(0) = 0
+
+
+def _hf_layer_fixture():
+    z = np.load(Path(__file__).resolve().parent / "golden" / "hf_llama_layer.npz")
+    D, NH, NKV, HD, F = (int(v) for v in z["dims"])
+    cfg = ob.LayerConfig(D, NH, NKV, HD, F, eps=float(z["eps"]), rope_theta=float(z["rope_theta"]))
+    seed = int(z["seed"])
+    lens, starts = [int(v) for v in z["lens"]], [int(v) for v in z["starts"]]
+    X = [hashrng.normal((n, D), np.float32, seed, 500 + b, 1.0) for b, n in enumerate(lens)]
+    offs = np.concatenate([[0], np.cumsum(lens)])
+    want = [z["out"][offs[b] : offs[b + 1]] for b in range(len(lens))]
+    return cfg, ob.synthetic_layer(cfg, seed), lens, starts, X, want
+
+
+def _stagger(cfg, W, lens, starts, X, half_acts, kv_dtype):
+    """Steps every sequence token by token; sequence b joins the batch at step
+    starts[b], so one batch holds sequences at different positions. Returns
+    each sequence's output rows."""
+    kc = [np.zeros((cfg.n_kv_heads, n, cfg.head_dim), kv_dtype) for n in lens]
+    vc = [np.zeros((cfg.n_kv_heads, n, cfg.head_dim), kv_dtype) for n in lens]
+    out = [np.zeros((n, cfg.dim), np.float32) for n in lens]
+    for t in range(max(s + n for s, n in zip(starts, lens))):
+        act = [b for b in range(len(lens)) if starts[b] <= t < starts[b] + lens[b]]
+        pos = [t - starts[b] for b in act]
+        Y = ob.layer_step(cfg, W, np.stack([X[b][p] for b, p in zip(act, pos)]), [kc[b] for b in act],
+                          [vc[b] for b in act], np.array(pos) + 1, half_acts=half_acts)
+        for i, (b, p) in enumerate(zip(act, pos)):
+            out[b][p] = Y[i]
+    return out
+
+
+def test_batch_layer_step_matches_hf_llama_layer():
+    """Without the fp16 activation roundings and with fp64 caches, every row of
+    a staggered ragged batch equals transformers' LlamaDecoderLayer (float64)
+    on the dequantised weights, up to the fp32 storage of each output."""
+    cfg, W, lens, starts, X, want = _hf_layer_fixture()
+    got = _stagger(cfg, W, lens, starts, X, half_acts=False, kv_dtype=np.float64)
+    for b in range(len(lens)):
+        assert np.abs(got[b] - want[b]).max() / np.abs(want[b]).max() < 1e-6, b
+    # the device's roundings (fp16 activations and K/V) stay inside the 1e-2 contract
+    got16 = _stagger(cfg, W, lens, starts, X, half_acts=True, kv_dtype=np.float16)
+    for b in range(len(lens)):
+        assert np.abs(got16[b] - want[b]).max() / np.abs(want[b]).max() < 3e-3, b
+
+
+def test_batch_layer_step_ragged_equals_single_sequences():
+    """A sequence's rows do not depend on which other sequences share its batch."""
+    cfg, W, lens, starts, X, _ = _hf_layer_fixture()
+    together = _stagger(cfg, W, lens, starts, X, half_acts=True, kv_dtype=np.float16)
+    for b in range(len(lens)):
+        alone = _stagger(cfg, W, [lens[b]], [0], [X[b]], half_acts=True, kv_dtype=np.float16)[0]
+        assert np.allclose(together[b], alone, rtol=1e-6, atol=1e-7), b
