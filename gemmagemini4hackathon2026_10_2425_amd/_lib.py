@@ -58,7 +58,9 @@ class ModelConfig(ctypes.Structure):
     _fields_ = [
         ("n_layers", c_int), ("dim", c_int), ("n_heads", c_int), ("n_kv_heads", c_int), ("head_dim", c_int),
         ("ffn_dim", c_int), ("vocab", c_int), ("rms_eps", c_float), ("rope_theta", c_float), ("act", c_int),
-        ("norm_plus_one", c_int), ("embed_scale_sqrt_dim", c_int),
+        ("norm_plus_one", c_int), ("embed_scale_sqrt_dim", c_int), ("untied_lm_head", c_int),
+        ("rope_factor", c_float), ("rope_low_freq_factor", c_float), ("rope_high_freq_factor", c_float),
+        ("rope_original_max_positions", c_int),
     ]
 
 
@@ -75,6 +77,7 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_engine_upload": (c_int, [E, c_int, P, c_size_t]),
     "mxd_engine_download": (c_int, [E, c_int, P, c_size_t]),
     "mxd_engine_init_random": (c_int, [E, c_uint64, c_float]),
+    "mxd_engine_fill_tensor": (c_int, [E, c_int, c_uint64, c_float]),
     "mxd_engine_weight_bytes": (c_size_t, [E]),
     "mxd_engine_set_tokens": (c_int, [E, P, c_int, c_int]),
     "mxd_engine_get_tokens": (c_int, [E, P, c_int, c_int]),
@@ -83,6 +86,7 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_engine_prefill": (c_int, [E, c_int]),
     "mxd_engine_decode": (c_int, [E, c_int, c_int]),
     "mxd_engine_sync": (c_int, [E]),
+    "mxd_engine_wait_token": (c_int, [E, c_int, P]),
     "mxd_last_error": (c_char_p, []),
     "mxd_abi_version": (c_int, []),
     "mxd_set_tunable": (c_int, [c_char_p, c_int]),

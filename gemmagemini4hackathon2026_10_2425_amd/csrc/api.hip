@@ -49,7 +49,7 @@ int tunable(const char* name, int fallback) {
 
 extern "C" const char* mxd_last_error(void) { return mxd::g_err; }
 
-extern "C" int mxd_abi_version(void) { return 1; }
+extern "C" int mxd_abi_version(void) { return 2; }
 
 extern "C" int mxd_set_tunable(const char* name, int value) {
     if (!name || !*name) return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_set_tunable: empty name");

@@ -1,5 +1,7 @@
 // Greedy sampling: tokens[out_idx] = argmax(logits), ties to the lowest index
-// (KL/kernels.metal:310-345).
+// (KL/kernels.metal:310-345). As in the reference's `v > best` scan from
+// best = -inf, NaN and -inf logits are never selected, and a row with nothing
+// else gives token 0.
 //
 // Many workgroups scan the logits; each folds (value, index) into one 64-bit
 // key, key = orderable(value) << 32 | ~index, so a larger key is a larger
@@ -20,7 +22,10 @@ struct ArgmaxWs {
     unsigned int pad;
 };
 
+// Key 0 (never selected) for NaN and -inf; otherwise the value's bits mapped
+// to an unsigned order above 0, then the inverted index.
 __device__ __forceinline__ unsigned long long pack(float v, int idx) {
+    if (!(v > -INFINITY)) return 0ull;
     uint32_t u = v == 0.0f ? 0u : __float_as_uint(v);  // -0 ties with +0
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)u << 32) | (uint32_t)(~(uint32_t)idx);
@@ -35,7 +40,7 @@ __device__ __forceinline__ unsigned long long shfl_xor64(unsigned long long v, i
 
 __global__ void __launch_bounds__(AM_THREADS)
 argmax_kernel(const float* __restrict__ logits, int32_t* __restrict__ tokens, int N, int out_idx, int32_t* pos_dev,
-              int advance, ArgmaxWs* ws) {
+              int advance, ArgmaxWs* ws, int32_t* host_tokens) {
     __shared__ unsigned long long wbest[AM_THREADS / 64];
     __shared__ bool last;
     unsigned long long best = 0;  // below every real key
@@ -59,7 +64,9 @@ argmax_kernel(const float* __restrict__ logits, int32_t* __restrict__ tokens, in
         // With pos_dev (a replayed decode step) the token goes to tokens[pos + 1]
         // and, with advance, the step position moves on by one.
         if (pos_dev) out_idx = pos_dev[0] + 1;
-        tokens[out_idx] = (int32_t)(~(uint32_t)(b & 0xFFFFFFFFull));
+        const int32_t tok = b == 0ull ? 0 : (int32_t)(~(uint32_t)(b & 0xFFFFFFFFull));
+        tokens[out_idx] = tok;
+        if (host_tokens) host_tokens[out_idx] = tok;
         if (pos_dev && advance) pos_dev[0] = out_idx;
         atomicExch(&ws->best, 0ull);
         atomicExch(&ws->ticket, 0u);
@@ -87,11 +94,11 @@ extern "C" int mxd_argmax(const float* logits, int32_t* tokens, int N, int out_i
 namespace mxd {
 
 int argmax_dev(const float* logits, int32_t* tokens, int N, int out_idx, int32_t* pos_dev, bool advance,
-               void* workspace, hipStream_t s) {
+               void* workspace, hipStream_t s, int32_t* host_tokens) {
     int blocks = (N + AM_THREADS * AM_PER_THREAD - 1) / (AM_THREADS * AM_PER_THREAD);
     if (blocks > 1024) blocks = 1024;
     hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(AM_THREADS), 0, s, logits, tokens, N, out_idx, pos_dev,
-                       advance ? 1 : 0, static_cast<ArgmaxWs*>(workspace));
+                       advance ? 1 : 0, static_cast<ArgmaxWs*>(workspace), host_tokens);
     return check_launch("argmax");
 }
 

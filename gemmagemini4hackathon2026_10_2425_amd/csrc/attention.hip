@@ -44,6 +44,8 @@
 //  * K and V are read with nontemporal loads: they stream through once.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int ATT_WAVES = 4;  // default waves per workgroup
@@ -77,6 +79,12 @@ struct AttnArgs {
     // Every active split leaves a partial, also a single one (the consumer
     // merges them): mxd_attention_split.
     bool partials_only = false;
+    // mxd_attention: the splits that take blocks follow from the key count on
+    // the device (active_splits), so a grid sized for max_ctx under a device
+    // position splits a given context exactly as a launch for that context.
+    bool auto_splits = false;
+    int single_blocks = 0;  // contexts of up to this many blocks take one split
+    int waves = 4;
 };
 
 // Keys visible to the query: n_keys, or *pos_dev + 1 read on the device (clamped
@@ -84,6 +92,15 @@ struct AttnArgs {
 __device__ __forceinline__ int n_keys_of(const AttnArgs& a) {
     const int n = a.pos_dev ? a.pos_dev[0] + 1 : a.n_keys;
     return max(0, min(n, a.max_ctx));
+}
+
+// Splits of a context of nblocks 32-key blocks under auto_splits: one up to
+// single_blocks, else one block per wave, capped by the launched grid. The
+// host's splits_for computes the grid with the same rule.
+__device__ __forceinline__ int active_splits(const AttnArgs& a, int nblocks) {
+    if (!a.auto_splits) return a.n_splits;
+    if (nblocks <= a.single_blocks) return 1;
+    return min(a.n_splits, (nblocks + a.waves - 1) / a.waves);
 }
 
 template <int HD>
@@ -411,7 +428,9 @@ template <int HD, int W, bool PF>
 __global__ void __launch_bounds__(W * 64) attn_split_kernel(AttnArgs a) {
     const int kvh = blockIdx.y;
     const ContigKV<HD> src{a.k + (size_t)kvh * a.max_ctx * HD, a.v + (size_t)kvh * a.max_ctx * HD};
-    attn_split<HD, W, PF>(a, src, n_keys_of(a), a.n_splits, blockIdx.x, kvh, a.q, a.out, a.ws_o, a.ws_ml);
+    const int n = n_keys_of(a);
+    attn_split<HD, W, PF>(a, src, n, active_splits(a, (n + BLK - 1) / BLK), blockIdx.x, kvh, a.q, a.out, a.ws_o,
+                          a.ws_ml);
 }
 
 // Prefill: `rows` queries at positions pos0 .. pos0 + rows - 1 over the
@@ -687,7 +706,8 @@ __device__ __forceinline__ void attn_merge_core(const AttnArgs& a, int n_active,
 // of head x / (HD/MG_D).
 template <int HD>
 __global__ void __launch_bounds__(MG_T) attn_merge_kernel(AttnArgs a) {
-    const int n_active = min(a.n_splits, (n_keys_of(a) + BLK - 1) / BLK);
+    const int nblocks = (n_keys_of(a) + BLK - 1) / BLK;
+    const int n_active = min(active_splits(a, nblocks), nblocks);
     constexpr int NCH = HD / MG_D;
     attn_merge_core<HD>(a, n_active, blockIdx.x / NCH, blockIdx.x % NCH, a.out, a.ws_o, a.ws_ml);
 }
@@ -761,13 +781,25 @@ int target_splits(int n_kv) {
 // Up to 4 blocks per wave take one split, which writes the output without a
 // merge launch (measured: a second launch costs more than the serial blocks
 // it saves). Longer contexts take enough splits that every wave has at most
-// one block, capped by the occupancy target.
+// one block, capped by the occupancy target. active_splits is the same rule
+// on the device.
+int single_blocks() { return mxd::tunable("ATT_SINGLE", 4 * att_waves()); }
 int splits_for(int max_keys, int n_kv) {
     const int nblocks = (max_keys + BLK - 1) / BLK;
     const int w = att_waves();
-    if (nblocks <= mxd::tunable("ATT_SINGLE", 4 * w)) return 1;
+    if (nblocks <= single_blocks()) return 1;
     const int one_per_wave = (nblocks + w - 1) / w;
     return max(1, min(one_per_wave, target_splits(n_kv)));
+}
+
+// Calls f with std::integral_constant<int, HD> for the supported head dims
+// (64: Llama-3.2-1B; 128: Llama-3-8B; 256: Gemma-2B); the callers have
+// checked head_dim.
+template <typename F>
+void with_head_dim(int head_dim, F&& f) {
+    if (head_dim == 64) f(std::integral_constant<int, 64>{});
+    else if (head_dim == 128) f(std::integral_constant<int, 128>{});
+    else f(std::integral_constant<int, 256>{});
 }
 
 }  // namespace
@@ -788,7 +820,7 @@ extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint1
     const int G = n_heads / n_kv_heads;
     MXD_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, MXD_ERR_UNSUPPORTED,
                 "mxd_attention: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", G);
-    MXD_REQUIRE(head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED, "mxd_attention: head_dim %d (128 or 256)",
+    MXD_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED, "mxd_attention: head_dim %d (64, 128 or 256)",
                 head_dim);
     MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED,
                 "mxd_attention: max_ctx=%d must be a positive multiple of 32", max_ctx);
@@ -821,16 +853,17 @@ extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint1
     a.n_keys = n_keys;
     a.n_splits = n_splits;
     a.qscale = scale * LOG2E;
+    a.auto_splits = true;
+    a.single_blocks = single_blocks();
+    a.waves = att_waves();
 
     hipStream_t s = mxd::as_stream(stream);
     const dim3 grid(n_splits, n_kv_heads);
-    if (head_dim == 128) {
-        launch_split<128>(grid, s, a);
-        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(n_heads * 128 / MG_D), dim3(MG_T), 0, s, a);
-    } else {
-        launch_split<256>(grid, s, a);
-        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<256>, dim3(n_heads * 256 / MG_D), dim3(MG_T), 0, s, a);
-    }
+    with_head_dim(head_dim, [&](auto hd) {
+        constexpr int HD = decltype(hd)::value;
+        launch_split<HD>(grid, s, a);
+        if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<HD>, dim3(n_heads * HD / MG_D), dim3(MG_T), 0, s, a);
+    });
     return mxd::check_launch("mxd_attention");
 }
 
@@ -844,7 +877,7 @@ extern "C" int mxd_attention_split(const float* q, const uint16_t* kcache, const
     const int G = n_heads / n_kv_heads;
     MXD_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, MXD_ERR_UNSUPPORTED,
                 "mxd_attention_split: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", G);
-    MXD_REQUIRE(head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED, "mxd_attention_split: head_dim %d (128 or 256)",
+    MXD_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED, "mxd_attention_split: head_dim %d (64, 128 or 256)",
                 head_dim);
     MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED,
                 "mxd_attention_split: max_ctx=%d must be a positive multiple of 32", max_ctx);
@@ -877,10 +910,7 @@ extern "C" int mxd_attention_split(const float* q, const uint16_t* kcache, const
     a.partials_only = true;
     hipStream_t s = mxd::as_stream(stream);
     const dim3 grid(n_splits, n_kv_heads);
-    if (head_dim == 128)
-        launch_split<128>(grid, s, a);
-    else
-        launch_split<256>(grid, s, a);
+    with_head_dim(head_dim, [&](auto hd) { launch_split<decltype(hd)::value>(grid, s, a); });
     return mxd::check_launch("mxd_attention_split");
 }
 
@@ -929,7 +959,7 @@ int sk_wgs_hd() {
     }
     return n;
 }
-int sk_wgs(int hd) { return hd == 128 ? sk_wgs_hd<128>() : sk_wgs_hd<256>(); }
+int sk_wgs(int hd) { return hd == 64 ? sk_wgs_hd<64>() : hd == 128 ? sk_wgs_hd<128>() : sk_wgs_hd<256>(); }
 
 // Workspace of the balanced schedule: partial slots (O rows, then (max, sum)
 // pairs) and the n_seqs + 1 block prefix.
@@ -949,8 +979,8 @@ extern "C" int mxd_attention_prefill(const float* q, int q_stride, const uint16_
     const int G = n_heads / n_kv_heads;
     MXD_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, MXD_ERR_UNSUPPORTED,
                 "mxd_attention_prefill: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", G);
-    MXD_REQUIRE(head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED,
-                "mxd_attention_prefill: head_dim %d (128 or 256)", head_dim);
+    MXD_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_prefill: head_dim %d (64, 128 or 256)", head_dim);
     MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED,
                 "mxd_attention_prefill: max_ctx=%d must be a positive multiple of 32", max_ctx);
     MXD_REQUIRE(rows >= 1 && pos0 >= 0 && (long long)pos0 + rows <= max_ctx, MXD_ERR_INVALID_ARG,
@@ -980,17 +1010,17 @@ extern "C" int mxd_attention_prefill(const float* q, int q_stride, const uint16_
     a.qscale = scale * LOG2E;
     hipStream_t s = mxd::as_stream(stream);
     const dim3 grid(rows, n_kv_heads);
-    if (head_dim == 128)
-        hipLaunchKernelGGL((attn_prefill_kernel<128, ATT_WAVES, false>), grid, dim3(ATT_WAVES * 64), 0, s, a);
-    else
-        hipLaunchKernelGGL((attn_prefill_kernel<256, ATT_WAVES, false>), grid, dim3(ATT_WAVES * 64), 0, s, a);
+    with_head_dim(head_dim, [&](auto hd) {
+        hipLaunchKernelGGL((attn_prefill_kernel<decltype(hd)::value, ATT_WAVES, false>), grid, dim3(ATT_WAVES * 64), 0,
+                           s, a);
+    });
     return mxd::check_launch("mxd_attention_prefill");
 }
 
 extern "C" size_t mxd_attention_paged_workspace_size(int n_heads, int n_kv_heads, int head_dim, int n_seqs,
                                                      int max_keys) {
     if (n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || n_seqs <= 0 || max_keys <= 0) return 0;
-    if (n_heads % n_kv_heads == 0 && (head_dim == 128 || head_dim == 256) &&
+    if (n_heads % n_kv_heads == 0 && (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
         use_balanced(n_seqs, max_keys, n_kv_heads))
         return sk_workspace(sk_wgs(head_dim), n_seqs, n_heads, n_kv_heads, head_dim);
     return (size_t)n_seqs * paged_split_max(max_keys) * n_heads * (head_dim + 2) * sizeof(float);
@@ -1008,8 +1038,8 @@ extern "C" int mxd_attention_paged(const float* q, int q_stride, const uint16_t*
     const int G = n_heads / n_kv_heads;
     MXD_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, MXD_ERR_UNSUPPORTED,
                 "mxd_attention_paged: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", G);
-    MXD_REQUIRE(head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED,
-                "mxd_attention_paged: head_dim %d (128 or 256)", head_dim);
+    MXD_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_paged: head_dim %d (64, 128 or 256)", head_dim);
     MXD_REQUIRE(n_pages > 0 && max_pages > 0 && n_seqs > 0 && n_seqs <= 65535, MXD_ERR_INVALID_ARG,
                 "mxd_attention_paged: n_pages=%d max_pages=%d n_seqs=%d", n_pages, max_pages, n_seqs);
     MXD_REQUIRE(max_keys >= 1 && max_keys <= max_pages * mxd::PAGE_KEYS, MXD_ERR_INVALID_ARG,
@@ -1065,24 +1095,19 @@ extern "C" int mxd_attention_paged(const float* q, int q_stride, const uint16_t*
     hipStream_t s = mxd::as_stream(stream);
     if (balanced) {
         const dim3 mgrid((n_heads * head_dim + SKM_T - 1) / SKM_T, n_seqs);
-        if (head_dim == 128) {
-            launch_paged_sk<128>(nw, s, a);
-            hipLaunchKernelGGL(attn_paged_sk_merge_kernel<128>, mgrid, dim3(SKM_T), 0, s, a);
-        } else {
-            launch_paged_sk<256>(nw, s, a);
-            hipLaunchKernelGGL(attn_paged_sk_merge_kernel<256>, mgrid, dim3(SKM_T), 0, s, a);
-        }
+        with_head_dim(head_dim, [&](auto hd) {
+            constexpr int HD = decltype(hd)::value;
+            launch_paged_sk<HD>(nw, s, a);
+            hipLaunchKernelGGL(attn_paged_sk_merge_kernel<HD>, mgrid, dim3(SKM_T), 0, s, a);
+        });
         return mxd::check_launch("mxd_attention_paged");
     }
     const dim3 grid(s_max, n_kv_heads, n_seqs);
-    if (head_dim == 128) {
-        launch_paged<128>(grid, s, a);
+    with_head_dim(head_dim, [&](auto hd) {
+        constexpr int HD = decltype(hd)::value;
+        launch_paged<HD>(grid, s, a);
         if (s_max > 1)
-            hipLaunchKernelGGL(attn_paged_merge_kernel<128>, dim3(n_heads * 128 / MG_D, n_seqs), dim3(MG_T), 0, s, a);
-    } else {
-        launch_paged<256>(grid, s, a);
-        if (s_max > 1)
-            hipLaunchKernelGGL(attn_paged_merge_kernel<256>, dim3(n_heads * 256 / MG_D, n_seqs), dim3(MG_T), 0, s, a);
-    }
+            hipLaunchKernelGGL(attn_paged_merge_kernel<HD>, dim3(n_heads * HD / MG_D, n_seqs), dim3(MG_T), 0, s, a);
+    });
     return mxd::check_launch("mxd_attention_paged");
 }

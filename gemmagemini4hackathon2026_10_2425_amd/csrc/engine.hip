@@ -4,7 +4,9 @@
 // Reference: Engine (KL/main.swift:152-347, KG/main.swift:394-457). Step order
 // follows encodeDecode (KL/main.swift:321-347) with the Gemma substitutions
 // (sqrt(D) embedding scale KG/main.swift:397, GeGLU, tied LM head
-// KG/main.swift:379-380, (1 + w) RMSNorm weights). The token of step t is
+// KG/main.swift:379-380, (1 + w) RMSNorm weights), or the Llama ones (plain
+// RMSNorm weights, SwiGLU, an untied lm_head KL/main.swift:306, Llama-3 RoPE
+// scaling KL/main.swift:96-107). The token of step t is
 // written by the GPU into tokens[t + 1] and read from there by step t + 1
 // (KL/kernels.metal:343 / :38), so a run of steps needs no host round trip.
 //
@@ -71,6 +73,7 @@ struct mxd_engine {
     size_t abytes = 0;
     std::vector<LayerPtrs> L;
     uint16_t* embed = nullptr;
+    uint16_t* head = nullptr;  // the LM head: embed (tied) or lm_head
     float* final_norm = nullptr;
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
     float* invf = nullptr;
@@ -83,6 +86,17 @@ struct mxd_engine {
     int att_splits = 0;
     void* am_ws = nullptr;
     hipGraphExec_t graph = nullptr;
+    // Streaming decode: the captured step's argmax also writes each token to
+    // pinned host memory (htokens, its device view htokens_dev), and every
+    // replayed step records an event in a ring indexed by its position, so a
+    // caller waits for one step without draining the ones queued after it.
+    int32_t* htokens = nullptr;
+    int32_t* htokens_dev = nullptr;
+    static constexpr int RING = 16;
+    hipEvent_t step_done[RING] = {};
+    // The position the last decode run left in the device counter (-1: not
+    // known), so a run that continues from it needs no counter write.
+    int pos_next = -1;
     // prefill chunk buffers: rows x {dim f32, dim f16, qkv f32, q f32, ffn f32}
     // (the products round fp32 rows to fp16 as they load them), and the
     // products' split-K workspace
@@ -105,15 +119,17 @@ void add_tensor(mxd_engine* e, const std::string& name, size_t elems, int dtype,
     off += align256(bytes);
 }
 
-// Tensor ids of the synthetic-weight generator: embed 1, final_norm 2, and
-// 1000 + 16 * layer + {attn_norm 0, wqkv 1, wo 2, ffn_norm 3, wgate 4, wup 5,
-// wdown 6}; names follow the reference's weight file (KL/convert_weights.py:56-69).
+// Tensor ids of the synthetic-weight generator: embed 1, final_norm 2,
+// lm_head 3 (untied heads only), and 1000 + 16 * layer + {attn_norm 0, wqkv 1,
+// wo 2, ffn_norm 3, wgate 4, wup 5, wdown 6}; names follow the reference's
+// weight file (KL/convert_weights.py:56-69).
 void plan_weights(mxd_engine* e) {
     const mxd_model_config& c = e->c;
     const size_t D = c.dim, F = c.ffn_dim;
     size_t off = 0;
     add_tensor(e, "embed", (size_t)c.vocab * D, MXD_F16, 1, off);
     add_tensor(e, "final_norm", D, MXD_F32, 2, off);
+    if (c.untied_lm_head) add_tensor(e, "lm_head", (size_t)c.vocab * D, MXD_F16, 3, off);
     for (int l = 0; l < c.n_layers; ++l) {
         const std::string p = "l" + std::to_string(l) + ".";
         const uint64_t base = 1000 + 16 * (uint64_t)l;
@@ -136,6 +152,9 @@ T* wptr(mxd_engine* e, const std::string& name) {
 void destroy(mxd_engine* e) {
     if (!e) return;
     if (e->graph) hipGraphExecDestroy(e->graph);
+    for (hipEvent_t& ev : e->step_done)
+        if (ev) hipEventDestroy(ev);
+    if (e->htokens) hipHostFree(e->htokens);
     if (e->wbase) hipFree(e->wbase);
     if (e->abase) hipFree(e->abase);
     if (e->stream) hipStreamDestroy(e->stream);
@@ -184,10 +203,11 @@ int encode_step(mxd_engine* e, int pos, int32_t* pos_dev, bool sample) {
         if ((rc = mxd_matvec_f16(Lp.wdown, e->h, MXD_F32, e->x, D, F, MXD_EPI_ADD, nullptr, ms))) return rc;
     }
     if (!sample) return MXD_OK;
-    if ((rc = mxd_matvec_f16_rmsnorm(e->embed, e->x, e->final_norm, c.rms_eps, c.norm_plus_one, e->logits, V, D,
+    if ((rc = mxd_matvec_f16_rmsnorm(e->head, e->x, e->final_norm, c.rms_eps, c.norm_plus_one, e->logits, V, D,
                                      MXD_EPI_STORE, nullptr, ms)))
         return rc;
-    return mxd::argmax_dev(e->logits, e->tokens, V, pos + 1, pos_dev, pos_dev != nullptr, e->am_ws, s);
+    return mxd::argmax_dev(e->logits, e->tokens, V, pos + 1, pos_dev, pos_dev != nullptr, e->am_ws, s,
+                           pos_dev ? e->htokens_dev : nullptr);
 }
 
 // The batched prefill of tokens[pos0 .. pos0 + T) (encodePrefillChunk,
@@ -224,7 +244,7 @@ int encode_prefill(mxd_engine* e, int pos0, int T, bool sample) {
     // Only the last row needs logits: it takes the decode path's head.
     HIP_OK(hipMemcpyAsync(e->x, e->bx + (size_t)(T - 1) * D, (size_t)D * 4, hipMemcpyDeviceToDevice, s),
            "mxd_engine_prefill");
-    if ((rc = mxd_matvec_f16_rmsnorm(e->embed, e->x, e->final_norm, c.rms_eps, c.norm_plus_one, e->logits, V, D,
+    if ((rc = mxd_matvec_f16_rmsnorm(e->head, e->x, e->final_norm, c.rms_eps, c.norm_plus_one, e->logits, V, D,
                                      MXD_EPI_STORE, nullptr, ms)))
         return rc;
     return mxd::argmax_dev(e->logits, e->tokens, V, pos0 + T, nullptr, false, e->am_ws, s);
@@ -242,14 +262,36 @@ size_t prefill_ws_bytes(const mxd_model_config& c, int qkv_dim, int q_dim, int r
     return m;
 }
 
+// theta^(-2i/hd), and under Llama-3 scaling: kept when its wavelength 2 pi / f
+// is below original / high_freq_factor, divided by factor above
+// original / low_freq_factor, and blended linearly in original / wavelength in
+// between.
+double rope_inv_freq(const mxd_model_config& c, int i) {
+    const double f = 1.0 / pow((double)c.rope_theta, (double)(2 * i) / (double)c.head_dim);
+    if (c.rope_factor <= 0.0f) return f;
+    const double orig = (double)c.rope_original_max_positions, factor = (double)c.rope_factor;
+    const double lo = (double)c.rope_low_freq_factor, hi = (double)c.rope_high_freq_factor;
+    const double wave = 2.0 * M_PI / f;
+    if (wave < orig / hi) return f;
+    if (wave > orig / lo) return f / factor;
+    const double t = (orig / wave - lo) / (hi - lo);
+    return (1.0 - t) * f / factor + t * f;
+}
+
 int check_config(const mxd_model_config* c, int max_ctx) {
     MXD_REQUIRE(c, MXD_ERR_INVALID_ARG, "mxd_engine_create: null config");
     MXD_REQUIRE(c->n_layers > 0 && c->dim > 0 && c->n_heads > 0 && c->n_kv_heads > 0 && c->head_dim > 0 &&
                     c->ffn_dim > 0 && c->vocab > 0,
                 MXD_ERR_INVALID_ARG, "mxd_engine_create: sizes must be positive");
     MXD_REQUIRE(c->n_heads % c->n_kv_heads == 0, MXD_ERR_INVALID_ARG, "mxd_engine_create: n_heads %% n_kv_heads != 0");
-    MXD_REQUIRE(c->head_dim == 128 || c->head_dim == 256, MXD_ERR_UNSUPPORTED, "mxd_engine_create: head_dim %d",
-                c->head_dim);
+    MXD_REQUIRE(c->head_dim == 64 || c->head_dim == 128 || c->head_dim == 256, MXD_ERR_UNSUPPORTED,
+                "mxd_engine_create: head_dim %d (64, 128 or 256)", c->head_dim);
+    MXD_REQUIRE(c->rope_factor <= 0.0f ||
+                    (c->rope_factor >= 1.0f && c->rope_low_freq_factor > 0.0f &&
+                     c->rope_high_freq_factor > c->rope_low_freq_factor && c->rope_original_max_positions > 0),
+                MXD_ERR_INVALID_ARG,
+                "mxd_engine_create: llama3 rope scaling needs factor >= 1, 0 < low_freq_factor < high_freq_factor "
+                "and original_max_positions > 0");
     MXD_REQUIRE(c->dim % 8 == 0 && c->ffn_dim % 8 == 0, MXD_ERR_UNSUPPORTED,
                 "mxd_engine_create: dim and ffn_dim must be multiples of 8");
     MXD_REQUIRE(c->act == MXD_ACT_GELU_TANH || c->act == MXD_ACT_SILU, MXD_ERR_INVALID_ARG,
@@ -308,10 +350,20 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
 
     hipError_t he;
     if ((he = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking)) != hipSuccess ||
-        (he = hipMalloc(&e->wbase, e->wbytes)) != hipSuccess || (he = hipMalloc(&e->abase, e->abytes)) != hipSuccess) {
+        (he = hipMalloc(&e->wbase, e->wbytes)) != hipSuccess || (he = hipMalloc(&e->abase, e->abytes)) != hipSuccess ||
+        (he = hipHostMalloc(reinterpret_cast<void**>(&e->htokens), ((size_t)max_ctx + 1) * 4,
+                                hipHostMallocMapped | hipHostMallocCoherent)) !=
+            hipSuccess ||
+        (he = hipHostGetDevicePointer(reinterpret_cast<void**>(&e->htokens_dev), e->htokens, 0)) != hipSuccess) {
         destroy(e);
         return mxd::fail(MXD_ERR_ALLOC, "mxd_engine_create: %s (weights %zu B, buffers %zu B)", hipGetErrorString(he),
                          e->wbytes, off);
+    }
+    for (hipEvent_t& ev : e->step_done) {
+        if ((he = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) {
+            destroy(e);
+            return mxd::fail(MXD_ERR_HIP, "mxd_engine_create: %s", hipGetErrorString(he));
+        }
     }
     char* a = e->abase;
     e->x = reinterpret_cast<float*>(a + o_x);
@@ -332,6 +384,7 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
     e->bh = reinterpret_cast<float*>(a + o_bh);
     e->gm_ws = a + o_gws;
     e->embed = wptr<uint16_t>(e, "embed");
+    e->head = c.untied_lm_head ? wptr<uint16_t>(e, "lm_head") : e->embed;
     e->final_norm = wptr<float>(e, "final_norm");
     e->L.resize(c.n_layers);
     for (int l = 0; l < c.n_layers; ++l) {
@@ -352,10 +405,10 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
         destroy(e);
         return mxd::fail(MXD_ERR_HIP, "mxd_engine_create: %s", hipGetErrorString(he));
     }
-    // RoPE inverse frequencies in double, stored as float (KL/main.swift:92-94).
+    // RoPE inverse frequencies in double, stored as float (KL/main.swift:92-94),
+    // with the Llama-3 band scaling when configured (KL/main.swift:96-107).
     std::vector<float> invf(c.head_dim / 2);
-    for (int i = 0; i < c.head_dim / 2; ++i)
-        invf[i] = (float)(1.0 / pow((double)c.rope_theta, (double)(2 * i) / (double)c.head_dim));
+    for (int i = 0; i < c.head_dim / 2; ++i) invf[i] = (float)rope_inv_freq(c, i);
     he = hipMemcpyAsync(e->invf, invf.data(), invf.size() * 4, hipMemcpyHostToDevice, e->stream);
     if (he == hipSuccess) he = hipStreamSynchronize(e->stream);
     if (he != hipSuccess) {
@@ -403,6 +456,18 @@ extern "C" int mxd_engine_init_random(mxd_engine* e, uint64_t seed, float stddev
             return rc;
     }
     HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_init_random");
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_fill_tensor(mxd_engine* e, int i, uint64_t seed, float stddev) {
+    MXD_REQUIRE(e && i >= 0 && i < (int)e->tensors.size(), MXD_ERR_INVALID_ARG, "mxd_engine_fill_tensor: index %d",
+                i);
+    const TensorInfo& t = e->tensors[i];
+    const uint64_t n = t.bytes / (t.dtype == MXD_F32 ? 4 : 2);
+    if (int rc = mxd_fill_normal(e->wbase + t.offset, t.dtype, n, seed, t.id, stddev,
+                                 reinterpret_cast<mxd_stream_t>(e->stream)))
+        return rc;
+    HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_fill_tensor");
     return MXD_OK;
 }
 
@@ -498,9 +563,27 @@ extern "C" int mxd_engine_decode(mxd_engine* e, int pos, int count) {
         hipGraphDestroy(g);
         HIP_OK(ie, "mxd_engine_decode: instantiate");
     }
-    hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, e->stream, e->pos, pos);
-    if (int rc = mxd::check_launch("mxd_engine_decode")) return rc;
-    for (int i = 0; i < count; ++i) HIP_OK(hipGraphLaunch(e->graph, e->stream), "mxd_engine_decode: graph launch");
+    if (pos != e->pos_next) {
+        hipLaunchKernelGGL(set_int_kernel, dim3(1), dim3(1), 0, e->stream, e->pos, pos);
+        if (int rc = mxd::check_launch("mxd_engine_decode")) return rc;
+    }
+    e->pos_next = -1;  // until every launch below went out
+    for (int i = 0; i < count; ++i) {
+        HIP_OK(hipGraphLaunch(e->graph, e->stream), "mxd_engine_decode: graph launch");
+        HIP_OK(hipEventRecord(e->step_done[(pos + i) % mxd_engine::RING], e->stream), "mxd_engine_decode: event");
+    }
+    e->pos_next = pos + count;
+    return MXD_OK;
+}
+
+extern "C" int mxd_engine_wait_token(mxd_engine* e, int pos, int32_t* token) {
+    MXD_REQUIRE(e && token, MXD_ERR_INVALID_ARG, "mxd_engine_wait_token: null argument");
+    MXD_REQUIRE(pos >= 0 && pos < e->max_ctx, MXD_ERR_INVALID_ARG, "mxd_engine_wait_token: pos %d outside [0, %d)",
+                pos, e->max_ctx);
+    // The ring slot of pos holds its step's event, or that of a later step
+    // queued since (then the wait is longer, never too short: one stream).
+    HIP_OK(hipEventSynchronize(e->step_done[pos % mxd_engine::RING]), "mxd_engine_wait_token");
+    *token = __atomic_load_n(&e->htokens[pos + 1], __ATOMIC_ACQUIRE);
     return MXD_OK;
 }
 

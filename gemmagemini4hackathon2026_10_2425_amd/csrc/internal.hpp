@@ -15,9 +15,10 @@ int rope_kv_dev(float* qkv, uint16_t* kcache, uint16_t* vcache, const float* inv
                 int max_ctx, int pos0, int rows, const int32_t* pos_dev, hipStream_t s);
 
 // tokens[pos + 1] (or tokens[out_idx] without pos_dev) = argmax; with advance,
-// *pos_dev += 1 afterwards.
+// *pos_dev += 1 afterwards. With host_tokens (device-visible pinned host
+// memory) the token is also written to host_tokens at the same index.
 int argmax_dev(const float* logits, int32_t* tokens, int N, int out_idx, int32_t* pos_dev, bool advance,
-               void* workspace, hipStream_t s);
+               void* workspace, hipStream_t s, int32_t* host_tokens = nullptr);
 
 // fp16 (MXD_W_F16) or int8 block-32 (MXD_W_Q8B32) matvec whose fp32 x is
 // rounded to fp16 as it is loaded.

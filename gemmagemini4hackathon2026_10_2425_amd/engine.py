@@ -34,24 +34,37 @@ class ModelShape:
     act: str = "gelu_tanh"
     norm_plus_one: bool = True
     embed_scale_sqrt_dim: bool = True
+    tie_embeddings: bool = True  # LM head = the embedding; else a separate lm_head tensor
+    # Llama-3 RoPE scaling (factor, low_freq_factor, high_freq_factor,
+    # original_max_position_embeddings), or None for plain RoPE
+    rope_scaling: tuple | None = None
 
     def to_c(self) -> _lib.ModelConfig:
+        rs = self.rope_scaling or (0.0, 0.0, 0.0, 0)
         return _lib.ModelConfig(
             self.n_layers, self.dim, self.n_heads, self.n_kv_heads, self.head_dim, self.ffn_dim, self.vocab,
             self.rms_eps, self.rope_theta, _lib.MXD_ACT_SILU if self.act == "silu" else _lib.MXD_ACT_GELU_TANH,
-            int(self.norm_plus_one), int(self.embed_scale_sqrt_dim),
+            int(self.norm_plus_one), int(self.embed_scale_sqrt_dim), int(not self.tie_embeddings),
+            float(rs[0]), float(rs[1]), float(rs[2]), int(rs[3]),
         )
 
     @property
     def weight_bytes(self) -> int:
         D, F, qkv = self.dim, self.ffn_dim, (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
         per_layer = 2 * (qkv * D + D * self.n_heads * self.head_dim + 3 * F * D) + 2 * 4 * D
-        return self.n_layers * per_layer + 2 * self.vocab * D + 4 * D
+        heads = 1 if self.tie_embeddings else 2
+        return self.n_layers * per_layer + heads * 2 * self.vocab * D + 4 * D
 
 
 # The Gemma-2B-shaped model of the decode benchmark: 18 layers, hidden 2048,
 # 8 query heads / 1 KV head of dim 256, GeGLU FFN 16384, vocab 256000.
 GEMMA_2B = ModelShape(n_layers=18, dim=2048, n_heads=8, n_kv_heads=1, head_dim=256, ffn_dim=16384, vocab=256000)
+# The reference's Llama engine model (Llama-3.2-1B-Instruct): 16 layers, hidden
+# 2048, 32 query / 8 KV heads of dim 64, SwiGLU 8192, vocab 128256, Llama-3
+# RoPE scaling (KL/main.swift:96-107, 172).
+LLAMA32_1B = ModelShape(n_layers=16, dim=2048, n_heads=32, n_kv_heads=8, head_dim=64, ffn_dim=8192, vocab=128256,
+                        rms_eps=1e-5, rope_theta=500000.0, act="silu", norm_plus_one=False,
+                        embed_scale_sqrt_dim=False, tie_embeddings=True, rope_scaling=(32.0, 1.0, 4.0, 8192))
 
 
 class Engine:
@@ -106,8 +119,18 @@ class Engine:
             out.append((name.value.decode(), nb.value, np.float16 if dt.value == _lib.MXD_F16 else np.float32))
         return out
 
-    def init_random(self, seed: int, std: float = 0.02) -> None:
+    def init_random(self, seed: int, std: float = 0.02, embed_std: float | None = None) -> None:
+        """Synthetic weights: every tensor N(0, std^2) from the hash generator,
+        the embedding N(0, embed_std^2) if given."""
         call("mxd_engine_init_random", self._h, seed, std)
+        if embed_std is not None and embed_std != std:
+            self.fill_tensor("embed", seed, embed_std)
+
+    def fill_tensor(self, name: str, seed: int, std: float) -> None:
+        idx = self._lib.mxd_engine_find_tensor(self._h, name.encode())
+        if idx < 0:
+            raise KeyError(name)
+        call("mxd_engine_fill_tensor", self._h, idx, seed, std)
 
     def upload(self, name: str, array: np.ndarray) -> None:
         idx = self._lib.mxd_engine_find_tensor(self._h, name.encode())
@@ -173,18 +196,26 @@ class Engine:
             self.decode(P, n_new - 1)
         return self.tokens(P, n_new)
 
+    def wait_token(self, pos: int) -> int:
+        """Wait for the decode step at pos (only) and return its token."""
+        tok = ctypes.c_int32()
+        call("mxd_engine_wait_token", self._h, pos, ctypes.byref(tok))
+        return tok.value
+
     def decode_streaming(self, pos: int, count: int, emit: Callable[[int], bool], window: int = 3) -> None:
-        """Like the reference's decodeStreaming (KL/main.swift:477-491): steps are
-        queued `window` ahead; emit(token) gets each token as its step finishes
-        and returning False stops generation (queued steps are drained)."""
+        """Like the reference's decodeStreaming (KL/main.swift:477-491): `window`
+        steps stay in flight; the host waits only for the oldest, hands its
+        token to emit(token) and queues the next step. emit returning False
+        stops generation (steps already queued are drained)."""
+        if not 1 <= window <= 16:
+            raise ValueError(f"window {window} outside [1, 16] (the engine's ring of step events)")
         queued = done = 0
         stopped = False
         while done < queued or (not stopped and queued < count):
             while not stopped and queued < count and queued - done < window:
                 call("mxd_engine_decode", self._h, pos + queued, 1)
                 queued += 1
-            self.sync()
-            for t in self.tokens(pos + done + 1, queued - done):
-                done += 1
-                if not stopped and not emit(t):
-                    stopped = True
+            t = self.wait_token(pos + done)
+            done += 1
+            if not stopped and not emit(t):
+                stopped = True

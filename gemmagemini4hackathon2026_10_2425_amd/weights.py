@@ -13,9 +13,10 @@ Tensor names (KL/convert_weights.py:56-69): embed, l<i>.attn_norm, l<i>.wqkv
 final_norm, and lm_head when the head is not tied. Norm weights are fp32,
 everything else fp16.
 
-The engine covers Gemma-1/2B-style and Llama-style decoders with a tied LM
-head, head_dim 128 or 256 and plain RoPE; a file outside that raises
-ValueError naming what is unsupported.
+The engine covers Gemma-1/2B-style and Llama-style decoders (Llama-3.2-1B
+included) with a tied or untied LM head, head_dim 64, 128 or 256, and plain or
+Llama-3-scaled RoPE; a file outside that raises ValueError naming what is
+unsupported.
 """
 
 from __future__ import annotations
@@ -100,19 +101,40 @@ def read_bin(path: str | os.PathLike) -> tuple[dict, dict[str, np.ndarray]]:
 # ---------------------------------------------------------------- config
 
 
+def _rope(c: dict) -> tuple[float, tuple | None]:
+    """(rope_theta, Llama-3 scaling or None) of a config: transformers 4.x
+    writes rope_theta and rope_scaling at the top level, 5.x both inside
+    rope_parameters. rope_type "default" is plain RoPE, "llama3" the band
+    scaling of KL/main.swift:96-107; any other type is rejected."""
+    rp = c.get("rope_parameters") or {}
+    theta = c.get("rope_theta", rp.get("rope_theta", 10000.0))
+    scaling = c.get("rope_scaling") or (rp if rp.get("rope_type", "default") != "default" else None)
+    if not scaling:
+        return float(theta), None
+    rtype = scaling.get("rope_type", scaling.get("type"))
+    if rtype == "default":
+        return float(theta), None
+    if rtype != "llama3":
+        raise ValueError(f"rope scaling {scaling!r} is not supported (default or llama3)")
+    try:
+        return float(theta), (float(scaling["factor"]), float(scaling["low_freq_factor"]),
+                               float(scaling["high_freq_factor"]), int(scaling["original_max_position_embeddings"]))
+    except KeyError as err:
+        raise ValueError(f"llama3 rope scaling lacks {err}") from None
+
+
 def shape_from_config(c: dict) -> ModelShape:
     """ModelShape of an HF-style config (the keys KL/main.swift:75-110 reads).
     model_type "gemma": GeGLU (tanh), (1 + w) RMSNorm, sqrt(D) embedding scale.
-    "llama" (and configs without a model_type): SwiGLU, w RMSNorm, no scale."""
+    "llama" (and configs without a model_type): SwiGLU, w RMSNorm, no scale.
+    tie_word_embeddings false means a separate lm_head tensor (KL/main.swift:306)."""
     mt = c.get("model_type", "llama")
     if mt not in ("gemma", "llama"):
         raise ValueError(f"model_type {mt!r} is not supported (gemma or llama)")
-    if c.get("rope_scaling"):
-        raise ValueError(f"rope_scaling {c['rope_scaling']!r} is not supported (plain RoPE only)")
+    theta, scaling = _rope(c)
     if c.get("attention_bias") or c.get("mlp_bias"):
         raise ValueError("projection biases are not supported")
-    if not c.get("tie_word_embeddings", mt == "gemma"):
-        raise ValueError("an untied LM head is not supported (tie_word_embeddings must be true)")
+    tied = bool(c.get("tie_word_embeddings", mt == "gemma"))
     act = c.get("hidden_activation") or c.get("hidden_act") or ("gelu_pytorch_tanh" if mt == "gemma" else "silu")
     if act in ("gelu_pytorch_tanh", "gelu_tanh") or (mt == "gemma" and act == "gelu"):
         act = "gelu_tanh"  # Gemma's "gelu" is the tanh form (KG/kernels.metal:26-28)
@@ -124,13 +146,14 @@ def shape_from_config(c: dict) -> ModelShape:
         n_layers=int(c["num_hidden_layers"]), dim=dim, n_heads=nh,
         n_kv_heads=int(c.get("num_key_value_heads", nh)), head_dim=int(c.get("head_dim") or dim // nh),
         ffn_dim=int(c["intermediate_size"]), vocab=int(c["vocab_size"]),
-        rms_eps=float(c.get("rms_norm_eps", 1e-6)), rope_theta=float(c.get("rope_theta", 10000.0)), act=act,
-        norm_plus_one=gemma, embed_scale_sqrt_dim=gemma,
+        rms_eps=float(c.get("rms_norm_eps", 1e-6)), rope_theta=theta, act=act,
+        norm_plus_one=gemma, embed_scale_sqrt_dim=gemma, tie_embeddings=tied, rope_scaling=scaling,
     )
 
 
-def tensor_names(n_layers: int) -> list[str]:
-    return ["embed"] + [f"l{i}.{k}" for i in range(n_layers) for k in _LAYER_KINDS] + ["final_norm"]
+def tensor_names(n_layers: int, tied: bool = True) -> list[str]:
+    names = ["embed"] + [f"l{i}.{k}" for i in range(n_layers) for k in _LAYER_KINDS] + ["final_norm"]
+    return names if tied else names + ["lm_head"]
 
 
 # ---------------------------------------------------------------- engine
@@ -141,7 +164,7 @@ def load_engine(path: str | os.PathLike, max_ctx: int = 4096) -> Engine:
     dtype and size before the first upload)."""
     config, tensors = read_bin(path)
     shape = shape_from_config(config)
-    extra = sorted(set(tensors) - set(tensor_names(shape.n_layers)))
+    extra = sorted(set(tensors) - set(tensor_names(shape.n_layers, shape.tie_embeddings)))
     if extra:
         raise ValueError(f"{path}: tensors the engine does not use: {', '.join(extra[:8])}")
     e = Engine(shape, max_ctx)
@@ -183,7 +206,7 @@ def convert_hf(src: str | os.PathLike, out: str | os.PathLike) -> int:
 
     src = Path(src)
     config = json.loads((src / "config.json").read_text())
-    shape_from_config(config)  # reject what the engine cannot run before converting
+    shape = shape_from_config(config)  # reject what the engine cannot run before converting
     files = sorted(src.glob("*.safetensors"))
     if not files:
         raise FileNotFoundError(f"no *.safetensors in {src}")
@@ -217,6 +240,8 @@ def convert_hf(src: str | os.PathLike, out: str | os.PathLike) -> int:
         out_t[f"l{i}.wup"] = f16(f"l{i}.wup", get(p + "mlp.up_proj.weight"))
         out_t[f"l{i}.wdown"] = f16(f"l{i}.wdown", get(p + "mlp.down_proj.weight"))
     out_t["final_norm"] = get("model.norm.weight").astype(np.float32)
+    if not shape.tie_embeddings:
+        out_t["lm_head"] = f16("lm_head", get("lm_head.weight"))
     return write_bin(out, config, out_t)
 
 

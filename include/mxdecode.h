@@ -325,13 +325,21 @@ int mxd_gemm_gate_up_f16(const uint16_t* Wg, const uint16_t* Wu, const uint16_t*
 /* ---- decode engine ---------------------------------------------------------- */
 
 /* Model shape. Replaces the reference's Config read from the weight file's JSON
- * header (KL/main.swift:75-110). Weights fp16, norm weights fp32, tied LM head. */
+ * header (KL/main.swift:75-110). Weights fp16, norm weights fp32. head_dim 64
+ * (Llama-3.2-1B), 128 or 256 (Gemma-2B). */
 typedef struct mxd_model_config {
     int n_layers, dim, n_heads, n_kv_heads, head_dim, ffn_dim, vocab;
     float rms_eps, rope_theta;
     int act;                  /* MXD_ACT_GELU_TANH (Gemma GeGLU) or MXD_ACT_SILU */
     int norm_plus_one;        /* RMSNorm weight (1 + w) (Gemma) instead of w     */
     int embed_scale_sqrt_dim; /* x = E[tok] * sqrt(dim) (KG/main.swift:397)      */
+    int untied_lm_head;       /* logits from a separate "lm_head" tensor
+                                 (KL/main.swift:306) instead of the embedding
+                                 (tied, KG/main.swift:379-380)                    */
+    /* Llama-3 RoPE frequency scaling (rope_scaling rope_type "llama3",
+     * KL/main.swift:96-107), applied on the host in double when rope_factor > 0 */
+    float rope_factor, rope_low_freq_factor, rope_high_freq_factor;
+    int rope_original_max_positions;
 } mxd_model_config;
 
 typedef struct mxd_engine mxd_engine;
@@ -344,7 +352,8 @@ int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_engine** out
 int mxd_engine_destroy(mxd_engine* e);
 /* Weight tensors by index / name: "embed", "final_norm", "l<i>.attn_norm",
  * "l<i>.wqkv" (rows q|k|v), "l<i>.wo", "l<i>.ffn_norm", "l<i>.wgate",
- * "l<i>.wup", "l<i>.wdown" (names of KL/convert_weights.py:56-69). */
+ * "l<i>.wup", "l<i>.wdown", and "lm_head" when untied (names of
+ * KL/convert_weights.py:56-69). */
 int mxd_engine_num_tensors(const mxd_engine* e);
 int mxd_engine_tensor(const mxd_engine* e, int index, const char** name, void** dev_ptr, size_t* bytes,
                       int* dtype);
@@ -355,9 +364,13 @@ int mxd_engine_find_tensor(const mxd_engine* e, const char* name);
 int mxd_engine_upload(mxd_engine* e, int index, const void* host, size_t bytes);
 int mxd_engine_download(mxd_engine* e, int index, void* host, size_t bytes);
 /* Fills every weight with mxd_fill_normal(seed, tensor id), ids: embed 1,
- * final_norm 2, layer l: 1000 + 16 l + {attn_norm 0, wqkv 1, wo 2, ffn_norm 3,
- * wgate 4, wup 5, wdown 6}. Synchronises. */
+ * final_norm 2, lm_head 3, layer l: 1000 + 16 l + {attn_norm 0, wqkv 1, wo 2,
+ * ffn_norm 3, wgate 4, wup 5, wdown 6}. Synchronises. */
 int mxd_engine_init_random(mxd_engine* e, uint64_t seed, float stddev);
+/* Refills one tensor with mxd_fill_normal(seed, its tensor id, stddev), e.g.
+ * the embedding at its own scale. Synchronises. Like init_random, it stands in
+ * for the converted checkpoint (KL/convert_weights.py:71-89). */
+int mxd_engine_fill_tensor(mxd_engine* e, int index, uint64_t seed, float stddev);
 size_t mxd_engine_weight_bytes(const mxd_engine* e);
 
 /* tokens[start .. start+n) from / to host memory (Engine.setTokens / token(at:),
@@ -386,6 +399,14 @@ int mxd_engine_prefill(mxd_engine* e, int n);
 int mxd_engine_decode(mxd_engine* e, int pos, int count);
 /* Waits for the engine stream (waitUntilCompleted, KL/main.swift:379). */
 int mxd_engine_sync(mxd_engine* e);
+/* Waits until the step at pos queued by mxd_engine_decode has finished, without
+ * waiting for the steps queued after it, and returns the token it sampled
+ * (tokens[pos + 1]). Each decode step writes its token to pinned host memory
+ * and records an event in a ring of 16 steps, so a caller keeps several steps
+ * in flight and waits on the oldest: the per-command-buffer wait of
+ * decodeStreaming (KL/main.swift:477-491). Valid for a pos decoded since the
+ * last prefill / step at that position. */
+int mxd_engine_wait_token(mxd_engine* e, int pos, int32_t* token);
 
 #ifdef __cplusplus
 }

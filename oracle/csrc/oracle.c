@@ -12,7 +12,8 @@
  *   attention     KL/kernels.metal:235-305, GQA map :261, scale KL/main.swift:293
  *   argmax        KL/kernels.metal:310-345   (first maximum wins)
  *   embed         KL/kernels.metal:31-39, sqrt(D) scale KG/main.swift:397
- *   step order    KL/main.swift:321-347, tied head KG/main.swift:379-380
+ *   step order    KL/main.swift:321-347, tied head KG/main.swift:379-380,
+ *                 untied lm_head KL/main.swift:306, llama3 inv_freq KL/main.swift:96-107
  * Values are rounded to fp32 between ops and K/V to fp16, as on the GPU.
  * Weights come from the same counter-based generator as mxd_fill_normal.
  */
@@ -133,6 +134,10 @@ typedef struct {
     int act;          /* 0 gelu_tanh, 1 silu */
     int plus_one;     /* (1 + w) RMSNorm weights */
     int embed_scale;  /* x = E[tok] * sqrt(D) */
+    int untied_head;  /* logits from a separate lm_head tensor (id 3), not the embedding */
+    /* Llama-3 RoPE frequency scaling when rope_factor > 0 */
+    float rope_factor, rope_low_freq_factor, rope_high_freq_factor;
+    int rope_original_max_positions;
 } oracle_cfg;
 
 typedef struct {
@@ -143,7 +148,7 @@ typedef struct {
 typedef struct {
     oracle_cfg c;
     int max_ctx;
-    uint16_t* embed;
+    uint16_t *embed, *lm_head;
     float* final_norm;
     oracle_layer* L;
     uint16_t *k, *v; /* both [layer][kvh][ctx][hd] */
@@ -153,21 +158,46 @@ typedef struct {
 
 static uint64_t tid_of(int layer, int kind) { return 1000 + 16 * (uint64_t)layer + (uint64_t)kind; }
 
-static uint16_t* gen16(size_t n, uint64_t seed, uint64_t id) {
+static uint16_t* gen16(size_t n, uint64_t seed, uint64_t id, float std) {
     uint16_t* p = (uint16_t*)malloc(n * 2);
-    if (p) oracle_fill_normal_f16(p, n, seed, id, 0.02f);
+    if (p) oracle_fill_normal_f16(p, n, seed, id, std);
     return p;
 }
 
-static float* gen32(size_t n, uint64_t seed, uint64_t id) {
+static float* gen32(size_t n, uint64_t seed, uint64_t id, float std) {
     float* p = (float*)malloc(n * 4);
-    if (p) oracle_fill_normal_f32(p, n, seed, id, 0.02f);
+    if (p) oracle_fill_normal_f32(p, n, seed, id, std);
     return p;
+}
+
+/* inv_freq[i] = theta^(-2i/hd) in double, with the Llama-3 band scaling when
+ * rope_factor > 0: wavelengths 2 pi / f below original / high_freq_factor keep
+ * f, above original / low_freq_factor take f / factor, and in between blend the
+ * two linearly in original / wavelength; stored as float. */
+static void compute_inv_freq(const oracle_cfg* c, float* invf) {
+    const int HD = c->head_dim;
+    for (int i = 0; i < HD / 2; ++i) {
+        double f = 1.0 / pow((double)c->theta, (double)(2 * i) / (double)HD);
+        if (c->rope_factor > 0.0f) {
+            const double orig = (double)c->rope_original_max_positions, factor = (double)c->rope_factor;
+            const double lo = (double)c->rope_low_freq_factor, hi = (double)c->rope_high_freq_factor;
+            const double wave = 2.0 * 3.14159265358979323846 / f;
+            if (wave > orig / lo) {
+                f = f / factor;
+            } else if (wave >= orig / hi) {
+                const double t = (orig / wave - lo) / (hi - lo);
+                f = (1.0 - t) * f / factor + t * f;
+            }
+        }
+        invf[i] = (float)f;
+    }
 }
 
 void oracle_model_destroy(oracle_model* m);
 
-oracle_model* oracle_model_create(const oracle_cfg* cfg, int max_ctx, uint64_t seed) {
+/* Synthetic weights: every tensor N(0, std^2) from the hash generator, the
+ * embedding N(0, embed_std^2). */
+oracle_model* oracle_model_create(const oracle_cfg* cfg, int max_ctx, uint64_t seed, float std, float embed_std) {
     oracle_model* m = (oracle_model*)calloc(1, sizeof(oracle_model));
     if (!m) return NULL;
     m->c = *cfg;
@@ -175,19 +205,23 @@ oracle_model* oracle_model_create(const oracle_cfg* cfg, int max_ctx, uint64_t s
     const oracle_cfg* c = &m->c;
     const size_t D = c->dim, F = c->ffn_dim, HD = c->head_dim;
     const size_t qkv = (size_t)(c->n_heads + 2 * c->n_kv) * HD, qd = (size_t)c->n_heads * HD;
-    m->embed = gen16((size_t)c->vocab * D, seed, 1);
-    m->final_norm = gen32(D, seed, 2);
+    m->embed = gen16((size_t)c->vocab * D, seed, 1, embed_std);
+    m->final_norm = gen32(D, seed, 2, std);
+    if (c->untied_head) {
+        m->lm_head = gen16((size_t)c->vocab * D, seed, 3, std);
+        if (!m->lm_head) goto fail;
+    }
     m->L = (oracle_layer*)calloc(c->n_layers, sizeof(oracle_layer));
     if (!m->embed || !m->final_norm || !m->L) goto fail;
     for (int l = 0; l < c->n_layers; ++l) {
         oracle_layer* L = &m->L[l];
-        L->attn_norm = gen32(D, seed, tid_of(l, 0));
-        L->wqkv = gen16(qkv * D, seed, tid_of(l, 1));
-        L->wo = gen16(D * qd, seed, tid_of(l, 2));
-        L->ffn_norm = gen32(D, seed, tid_of(l, 3));
-        L->wgate = gen16(F * D, seed, tid_of(l, 4));
-        L->wup = gen16(F * D, seed, tid_of(l, 5));
-        L->wdown = gen16(D * F, seed, tid_of(l, 6));
+        L->attn_norm = gen32(D, seed, tid_of(l, 0), std);
+        L->wqkv = gen16(qkv * D, seed, tid_of(l, 1), std);
+        L->wo = gen16(D * qd, seed, tid_of(l, 2), std);
+        L->ffn_norm = gen32(D, seed, tid_of(l, 3), std);
+        L->wgate = gen16(F * D, seed, tid_of(l, 4), std);
+        L->wup = gen16(F * D, seed, tid_of(l, 5), std);
+        L->wdown = gen16(D * F, seed, tid_of(l, 6), std);
         if (!L->attn_norm || !L->wqkv || !L->wo || !L->ffn_norm || !L->wgate || !L->wup || !L->wdown) goto fail;
     }
     const size_t kv = (size_t)c->n_layers * c->n_kv * max_ctx * HD;
@@ -205,7 +239,7 @@ oracle_model* oracle_model_create(const oracle_cfg* cfg, int max_ctx, uint64_t s
     m->tmp = (double*)malloc(2 * big * 8);
     m->scores = (double*)malloc((size_t)c->n_heads * max_ctx * 8);
     if (HD > 512 || !m->scores || !m->k || !m->v || !m->x || !m->xn || !m->qkv || !m->att || !m->h || !m->logits || !m->invf || !m->tmp) goto fail;
-    for (size_t i = 0; i < HD / 2; ++i) m->invf[i] = (float)(1.0 / pow((double)c->theta, (double)(2 * i) / (double)HD));
+    compute_inv_freq(c, m->invf);
     return m;
 fail:
     oracle_model_destroy(m);
@@ -220,7 +254,7 @@ void oracle_model_destroy(oracle_model* m) {
             free(L->wqkv); free(L->wo); free(L->wgate); free(L->wup); free(L->wdown);
             free(L->attn_norm); free(L->ffn_norm);
         }
-    free(m->L); free(m->embed); free(m->final_norm); free(m->k); free(m->v);
+    free(m->L); free(m->embed); free(m->lm_head); free(m->final_norm); free(m->k); free(m->v);
     free(m->x); free(m->xn); free(m->qkv); free(m->att); free(m->h); free(m->logits); free(m->invf); free(m->tmp); free(m->scores);
     free(m);
 }
@@ -305,7 +339,7 @@ int oracle_model_step(oracle_model* m, int32_t* tokens, int pos, int sample, flo
         for (int i = 0; i < D; ++i) m->x[i] = m->x[i] + (float)t[i];
     }
     rmsnorm(m->x, m->final_norm, m->xn, D, c->eps, c->plus_one);
-    oracle_matvec_f16(m->embed, m->xn, t, c->vocab, D);
+    oracle_matvec_f16(c->untied_head ? m->lm_head : m->embed, m->xn, t, c->vocab, D);
     int best = 0;
     float b1 = -INFINITY, b2 = -INFINITY;
     for (int i = 0; i < c->vocab; ++i) {
@@ -322,3 +356,6 @@ int oracle_model_step(oracle_model* m, int32_t* tokens, int pos, int sample, flo
 
 int oracle_num_threads(void) { return omp_get_max_threads(); }
 void oracle_set_num_threads(int n) { omp_set_num_threads(n); }
+
+/* The model's inverse RoPE frequencies (head_dim / 2 floats). */
+void oracle_model_inv_freq(const oracle_model* m, float* out) { memcpy(out, m->invf, (size_t)m->c.head_dim / 2 * 4); }

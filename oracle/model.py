@@ -6,6 +6,10 @@ scale (KG/main.swift:397), GeGLU (KG/kernels.metal:205-234), MQA, tied LM head
 (KG/main.swift:379-380), (1 + w) RMSNorm weights. Values are rounded to fp32
 between ops and K/V to fp16, the storage points of the GPU path.
 
+The Llama-3.2-1B shape of the reference's other engine is covered too: an
+untied lm_head (KL/main.swift:306, KL/convert_weights.py:67-68) and Llama-3
+RoPE frequency scaling (KL/main.swift:96-107).
+
 Weights are synthetic: hashrng with one tensor id per named tensor (names as
 in KL/convert_weights.py:56-69).
 """
@@ -36,6 +40,15 @@ class DecodeConfig:
     act: str = "gelu_tanh"
     gemma_embed_scale: bool = True   # x = E[tok] * sqrt(D)
     plus_one: bool = True            # RMSNorm weight (1 + w)
+    tie_embeddings: bool = True      # LM head = embedding; else a separate lm_head
+    # Llama-3 RoPE scaling (factor, low_freq_factor, high_freq_factor,
+    # original_max_position_embeddings), or None
+    rope_scaling: tuple | None = None
+
+    def inv_freq(self) -> np.ndarray:
+        if self.rope_scaling is None:
+            return ops.inv_freq(self.head_dim, self.rope_theta)
+        return ops.inv_freq_llama3(self.head_dim, self.rope_theta, *self.rope_scaling)
 
     @property
     def qkv_dim(self) -> int:
@@ -44,11 +57,15 @@ class DecodeConfig:
 
 GEMMA_2B = DecodeConfig(n_layers=18, dim=2048, n_heads=8, n_kv_heads=1, head_dim=256, ffn_dim=16384, vocab=256000)
 TINY = DecodeConfig(n_layers=2, dim=256, n_heads=4, n_kv_heads=1, head_dim=128, ffn_dim=512, vocab=1000)
+# The reference's Llama engine model (unsloth/Llama-3.2-1B-Instruct config).
+LLAMA32_1B = DecodeConfig(n_layers=16, dim=2048, n_heads=32, n_kv_heads=8, head_dim=64, ffn_dim=8192, vocab=128256,
+                          eps=1e-5, rope_theta=500000.0, act="silu", gemma_embed_scale=False, plus_one=False,
+                          tie_embeddings=True, rope_scaling=(32.0, 1.0, 4.0, 8192))
 
 
 def tensor_id(name: str) -> int:
     """Tensor id of a named weight for the hash generator."""
-    fixed = {"embed": 1, "final_norm": 2}
+    fixed = {"embed": 1, "final_norm": 2, "lm_head": 3}
     if name in fixed:
         return fixed[name]
     layer, kind = name.split(".")
@@ -59,6 +76,8 @@ def tensor_id(name: str) -> int:
 def weight_shapes(cfg: DecodeConfig) -> dict[str, tuple[tuple[int, ...], type]]:
     D, F = cfg.dim, cfg.ffn_dim
     shapes = {"embed": ((cfg.vocab, D), np.float16), "final_norm": ((D,), np.float32)}
+    if not cfg.tie_embeddings:
+        shapes["lm_head"] = ((cfg.vocab, D), np.float16)
     for l in range(cfg.n_layers):
         shapes[f"l{l}.attn_norm"] = ((D,), np.float32)
         shapes[f"l{l}.wqkv"] = ((cfg.qkv_dim, D), np.float16)
@@ -70,9 +89,11 @@ def weight_shapes(cfg: DecodeConfig) -> dict[str, tuple[tuple[int, ...], type]]:
     return shapes
 
 
-def make_weights(cfg: DecodeConfig, seed: int, std: float = 0.02) -> dict[str, np.ndarray]:
+def make_weights(cfg: DecodeConfig, seed: int, std: float = 0.02, embed_std: float | None = None
+                 ) -> dict[str, np.ndarray]:
+    """Every tensor N(0, std^2); the embedding N(0, embed_std^2) if given."""
     return {
-        name: hashrng.normal(shape, dt, seed, tensor_id(name), std)
+        name: hashrng.normal(shape, dt, seed, tensor_id(name), embed_std if name == "embed" and embed_std else std)
         for name, (shape, dt) in weight_shapes(cfg).items()
     }
 
@@ -86,7 +107,7 @@ class OracleDecoder:
         kv_dt = np.float16 if fp16_kv else np.float64
         self.k = np.zeros((cfg.n_layers, cfg.n_kv_heads, max_ctx, cfg.head_dim), kv_dt)
         self.v = np.zeros((cfg.n_layers, cfg.n_kv_heads, max_ctx, cfg.head_dim), kv_dt)
-        self.invf = ops.inv_freq(cfg.head_dim, cfg.rope_theta)
+        self.invf = cfg.inv_freq()
         self.tokens = np.zeros(max_ctx + 1, np.int32)
         self.fp16_kv = fp16_kv
 
@@ -118,7 +139,12 @@ class OracleDecoder:
             h = ops.gate_up(w[f"l{l}.wgate"], w[f"l{l}.wup"], xn, c.act).astype(F32)
             x = (x + ops.matvec(w[f"l{l}.wdown"], h).astype(F32)).astype(F32)
         xn = ops.rmsnorm(x, w["final_norm"], c.eps, c.plus_one).astype(F32)
-        return ops.matvec(w["embed"], xn).astype(F32)
+        return ops.matvec(self._head(), xn).astype(F32)
+
+    def _head(self) -> np.ndarray:
+        """The LM head: the embedding when tied (KG/main.swift:379-380), else
+        lm_head (KL/main.swift:306)."""
+        return self.w["embed"] if self.cfg.tie_embeddings else self.w["lm_head"]
 
     def prefill_chunk(self, pos0: int, rows: int, sample: bool = True, half_acts: bool = True) -> np.ndarray | None:
         """The batched prefill of tokens[pos0 .. pos0 + rows) (encodePrefillChunk,
@@ -147,7 +173,7 @@ class OracleDecoder:
         if not sample:
             return None
         xn = ops.rmsnorm(X[rows - 1], w["final_norm"], c.eps, c.plus_one).astype(F32)
-        logits = ops.matvec(w["embed"], xn).astype(F32)
+        logits = ops.matvec(self._head(), xn).astype(F32)
         self.tokens[pos0 + rows] = ops.argmax(logits)
         return logits
 

@@ -18,7 +18,8 @@ class _Cfg(Structure):
     _fields_ = [
         ("n_layers", c_int), ("dim", c_int), ("n_heads", c_int), ("n_kv", c_int), ("head_dim", c_int),
         ("ffn_dim", c_int), ("vocab", c_int), ("eps", c_float), ("theta", c_float), ("act", c_int),
-        ("plus_one", c_int), ("embed_scale", c_int),
+        ("plus_one", c_int), ("embed_scale", c_int), ("untied_head", c_int), ("rope_factor", c_float),
+        ("rope_low_freq_factor", c_float), ("rope_high_freq_factor", c_float), ("rope_original_max_positions", c_int),
     ]
 
 
@@ -35,7 +36,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_matvec_f16.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_int]
         L.oracle_matvec_q8b32.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int]
         L.oracle_matvec_f32.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_int]
-        L.oracle_model_create.argtypes = [POINTER(_Cfg), c_int, c_uint64]
+        L.oracle_model_create.argtypes = [POINTER(_Cfg), c_int, c_uint64, c_float, c_float]
+        L.oracle_model_inv_freq.argtypes = [c_void_p, c_void_p]
         L.oracle_model_create.restype = c_void_p
         L.oracle_model_destroy.argtypes = [c_void_p]
         L.oracle_model_step.argtypes = [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p]
@@ -86,14 +88,21 @@ def num_threads() -> int:
 class NativeDecoder:
     """Full-size greedy decoder (the C restatement of oracle.model.OracleDecoder)."""
 
-    def __init__(self, cfg: DecodeConfig, max_ctx: int, seed: int):
+    def __init__(self, cfg: DecodeConfig, max_ctx: int, seed: int, std: float = 0.02, embed_std: float | None = None):
+        rs = cfg.rope_scaling or (0.0, 0.0, 0.0, 0)
         c = _Cfg(cfg.n_layers, cfg.dim, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.ffn_dim, cfg.vocab, cfg.eps,
-                 cfg.rope_theta, 1 if cfg.act == "silu" else 0, int(cfg.plus_one), int(cfg.gemma_embed_scale))
+                 cfg.rope_theta, 1 if cfg.act == "silu" else 0, int(cfg.plus_one), int(cfg.gemma_embed_scale),
+                 int(not cfg.tie_embeddings), float(rs[0]), float(rs[1]), float(rs[2]), int(rs[3]))
         self.cfg, self.max_ctx = cfg, max_ctx
-        self._m = lib().oracle_model_create(ctypes.byref(c), max_ctx, seed)
+        self._m = lib().oracle_model_create(ctypes.byref(c), max_ctx, seed, std, embed_std or std)
         if not self._m:
             raise MemoryError("oracle_model_create failed")
         self.tokens = np.zeros(max_ctx + 1, np.int32)
+
+    def inv_freq(self) -> np.ndarray:
+        out = np.empty(self.cfg.head_dim // 2, np.float32)
+        lib().oracle_model_inv_freq(self._m, _p(out))
+        return out
 
     def close(self) -> None:
         if self._m:

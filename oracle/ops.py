@@ -155,8 +155,14 @@ def attention(q: np.ndarray, kcache: np.ndarray, vcache: np.ndarray, n_keys: int
 
 
 def argmax(logits: np.ndarray) -> int:
-    """First maximum = lowest index among ties (KL/kernels.metal:317-331)."""
-    return int(np.argmax(np.asarray(logits)))
+    """The reference's scan `if (v > best)` from best = -inf, index 0
+    (KL/kernels.metal:317-331): the first maximum (lowest index among ties);
+    NaN and -inf are never selected, and a row of nothing else gives 0."""
+    v = np.asarray(logits, dtype=np.float64)
+    live = v > -np.inf  # False for NaN and -inf
+    if not live.any():
+        return 0
+    return int(np.argmax(np.where(live, v, -np.inf)))
 
 
 def embed(E: np.ndarray, token: int, scale: float = 1.0) -> np.ndarray:

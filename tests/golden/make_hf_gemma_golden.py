@@ -9,6 +9,12 @@ nothing is downloaded). The model is float64; weights are the hash-generator
 values (fp16-representable), loaded by name: wqkv splits into q/k/v_proj rows
 (fused order q|k|v, KL/convert_weights.py:9), RMSNorm weights are Gemma's
 (1 + w) parameters, and the LM head is tied to the embedding.
+
+The layer weights are N(0, 0.1^2) and the embedding N(0, 0.02^2): at the
+common N(0, 0.02^2) the sqrt(D)-scaled embedding dominates this two-layer
+model's residual stream and every greedy token repeats the last prompt id;
+with these the 12 greedy tokens are all different (seed chosen for the widest
+top-2 margin among seeds 11..30, 0.023).
 """
 
 from __future__ import annotations
@@ -25,16 +31,18 @@ sys.path.insert(0, str(ROOT))
 from oracle import model as om  # noqa: E402
 
 OUT = Path(__file__).resolve().parent / "hf_gemma_tiny.npz"
-SEED = 11
+SEED = 29
+STD = 0.1
+EMBED_STD = 0.02
 PROMPT = [5, 17, 999, 3, 250, 250, 42]
-N_NEW = 8
+N_NEW = 12
 
 
 def main() -> None:
     from transformers import GemmaConfig, GemmaForCausalLM
 
     cfg = om.TINY
-    w = om.make_weights(cfg, SEED)
+    w = om.make_weights(cfg, SEED, STD, EMBED_STD)
     hc = GemmaConfig(
         vocab_size=cfg.vocab, hidden_size=cfg.dim, intermediate_size=cfg.ffn_dim, num_hidden_layers=cfg.n_layers,
         num_attention_heads=cfg.n_heads, num_key_value_heads=cfg.n_kv_heads, head_dim=cfg.head_dim,
@@ -66,8 +74,8 @@ def main() -> None:
         logits = model(torch.tensor([PROMPT])).logits[0].numpy()
         gen = model.generate(torch.tensor([PROMPT]), max_new_tokens=N_NEW, do_sample=False, temperature=None,
                              top_p=None, top_k=None)[0, len(PROMPT):].tolist()
-    np.savez_compressed(OUT, seed=SEED, prompt=np.array(PROMPT, np.int32), logits=logits.astype(np.float64),
-                        greedy=np.array(gen, np.int32))
+    np.savez_compressed(OUT, seed=SEED, std=STD, embed_std=EMBED_STD, prompt=np.array(PROMPT, np.int32),
+                        logits=logits.astype(np.float64), greedy=np.array(gen, np.int32))
     print(f"wrote {OUT}: logits {logits.shape}, greedy {gen}")
 
 

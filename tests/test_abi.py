@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_library_loads_and_reports_version():
     lib = _lib.load()
-    assert lib.mxd_abi_version() == 1
+    assert lib.mxd_abi_version() == 2
     for name in _lib.SIGNATURES:
         assert hasattr(lib, name)
 
@@ -62,7 +62,7 @@ P = ctypes.c_void_p(16)  # a non-null dummy: argument checks fail before any der
         ("mxd_rmsnorm", (P, P, P, 3, 1, 64, 1e-6, 1, None), _lib.MXD_ERR_INVALID_ARG),
         ("mxd_rope_kv", (P, P, P, P, 8, 1, 255, 64, 0, 1, None), _lib.MXD_ERR_UNSUPPORTED),
         ("mxd_rope_kv", (P, P, P, P, 8, 1, 256, 64, 64, 1, None), _lib.MXD_ERR_INVALID_ARG),
-        ("mxd_attention", (P, P, P, P, 32, 8, 64, 512, 10, None, 0.1, None, 0, None), _lib.MXD_ERR_UNSUPPORTED),
+        ("mxd_attention", (P, P, P, P, 32, 8, 96, 512, 10, None, 0.1, None, 0, None), _lib.MXD_ERR_UNSUPPORTED),
         ("mxd_attention", (P, P, P, P, 32, 8, 128, 500, 10, None, 0.1, None, 0, None), _lib.MXD_ERR_UNSUPPORTED),
         ("mxd_attention", (P, P, P, P, 48, 3, 128, 512, 10, None, 0.1, None, 0, None), _lib.MXD_ERR_UNSUPPORTED),
         ("mxd_attention", (P, P, P, P, 32, 8, 128, 512, 0, None, 0.1, None, 0, None), _lib.MXD_ERR_INVALID_ARG),
@@ -92,3 +92,20 @@ def test_workspace_queries():
     n = _lib.query("mxd_attention_workspace_size", 32, 8, 128, 32768)
     assert n >= 64 * 32 * (128 + 2) * 4
     assert _lib.query("mxd_argmax_workspace_size", 256000) >= 12
+
+
+@pytest.mark.parametrize("bad", [dict(head_dim=96), dict(rope_factor=32.0, rope_low_freq_factor=4.0,
+                                                          rope_high_freq_factor=1.0, rope_original_max_positions=8192),
+                                  dict(rope_factor=0.5, rope_low_freq_factor=1.0, rope_high_freq_factor=4.0,
+                                       rope_original_max_positions=8192)])
+def test_engine_config_rejected_before_allocation(bad):
+    """mxd_engine_create checks the config on the host before any device call."""
+    from gemmagemini4hackathon2026_10_2425_amd.engine import LLAMA32_1B
+
+    cfg = LLAMA32_1B.to_c()
+    for k, v in bad.items():
+        setattr(cfg, k, v)
+    out = ctypes.c_void_p()
+    with pytest.raises(_lib.MxdValueError):
+        _lib.call("mxd_engine_create", ctypes.byref(cfg), 256, ctypes.byref(out))
+    assert not out.value

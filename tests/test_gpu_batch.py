@@ -90,7 +90,7 @@ def _check_paged(dev, rng, lens, nh, nkv, hd, max_keys=None, tol=1e-4):
         assert rel_err(got[b], want) <= tol, (b, n)
 
 
-@pytest.mark.parametrize("nh,nkv,hd", [(32, 8, 128), (8, 1, 256), (16, 16, 128)])
+@pytest.mark.parametrize("nh,nkv,hd", [(32, 8, 128), (8, 1, 256), (16, 16, 128), (32, 8, 64)])
 @pytest.mark.parametrize("max_keys", [None, 32])
 def test_attention_paged(dev, rng, schedule, nh, nkv, hd, max_keys):
     """Ragged lengths around page and block edges, shuffled pages, NaN in every

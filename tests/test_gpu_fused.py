@@ -75,7 +75,7 @@ def test_gate_up_rmsnorm(dev, rng, act):
     assert rel_err(h.cpu().numpy(), ref.gate_up(Wg, Wu, xn, act)) <= 1e-4
 
 
-@pytest.mark.parametrize("nh,nkv,hd,D", [(8, 1, 256, 2048), (32, 8, 128, 4096), (4, 2, 128, 256)])
+@pytest.mark.parametrize("nh,nkv,hd,D", [(8, 1, 256, 2048), (32, 8, 128, 4096), (4, 2, 128, 256), (32, 8, 64, 2048)])
 @pytest.mark.parametrize("pos", [0, 45, 383])
 @pytest.mark.parametrize("device_pos", [False, True])
 def test_qkv_rope_kv(dev, rng, nh, nkv, hd, D, pos, device_pos):
@@ -147,7 +147,7 @@ def test_every_matvec_variant(dev, rng, algo):
         L.set_tunable("MV_ALGO", 0)
 
 
-@pytest.mark.parametrize("nh,nkv,hd,M", [(8, 1, 256, 2048), (32, 8, 128, 4096), (4, 2, 128, 300)])
+@pytest.mark.parametrize("nh,nkv,hd,M", [(8, 1, 256, 2048), (32, 8, 128, 4096), (4, 2, 128, 300), (32, 8, 64, 2048)])
 @pytest.mark.parametrize("L,n_splits", [(1, 3), (45, 3), (384, 3), (129, 8), (1000, 8), (700, 2)])
 @pytest.mark.parametrize("device_pos", [False, True])
 def test_attention_split_merged_by_matvec(dev, rng, nh, nkv, hd, M, L, n_splits, device_pos):

@@ -223,7 +223,7 @@ def test_f32_to_f16(dev, rng):
 # ---------------------------------------------------------------- rope + append
 
 
-@pytest.mark.parametrize("nh,nkv,hd,theta", [(32, 8, 128, 500000.0), (8, 1, 256, 10000.0)])
+@pytest.mark.parametrize("nh,nkv,hd,theta", [(32, 8, 128, 500000.0), (8, 1, 256, 10000.0), (32, 8, 64, 500000.0)])
 @pytest.mark.parametrize("pos", [0, 1, 383, 4095])
 def test_rope_kv(dev, rng, nh, nkv, hd, theta, pos):
     ops = _ops()
@@ -289,11 +289,11 @@ def test_attention_gqa_config(dev, rng, L):
     _close(out.cpu().numpy(), ref.attention(q, kc, vc, L, nh, 1 / math.sqrt(hd)), 1e-3)
 
 
-@pytest.mark.parametrize("nh,nkv,hd", [(8, 1, 256), (8, 8, 128), (16, 8, 256), (4, 1, 128)])
-@pytest.mark.parametrize("L", [1, 45, 384, 1000])
+@pytest.mark.parametrize("nh,nkv,hd", [(8, 1, 256), (8, 8, 128), (16, 8, 256), (4, 1, 128), (32, 8, 64), (8, 1, 64)])
+@pytest.mark.parametrize("L", [1, 45, 384, 1000, 4096])
 def test_attention_shapes(dev, rng, nh, nkv, hd, L):
     ops = _ops()
-    max_ctx = 1024
+    max_ctx = max(1024, L)
     q, kc, vc = _attn_case(rng, nh, nkv, hd, L, max_ctx)
     out = _gpu_attention(dev, q, kc, vc, L, nh)
     _close(out.cpu().numpy(), ref.attention(q, kc, vc, L, nh, 1 / math.sqrt(hd)), 1e-3)
@@ -337,6 +337,25 @@ def test_argmax(dev, rng, N):
         assert int(tokens[trial]) == ref.argmax(logits)
     assert int(tokens[3]) == -5  # untouched slots stay untouched
     assert not ws.any()  # the workspace is left zeroed
+
+
+def test_argmax_never_selects_nan_or_minus_inf(dev, rng):
+    """NaN and -inf logits are never the token, as in the reference's
+    `v > best` scan (KL/kernels.metal:324); a row of nothing else gives 0."""
+    ops = _ops()
+    ws = ops.argmax_workspace(dev)
+    tokens = torch.zeros(8, dtype=torch.int32, device=dev)
+    nan, inf = np.float32("nan"), np.float32("inf")
+    big = rng.standard_normal(256000, dtype=np.float32)
+    big[rng.random(256000) < 0.3] = nan
+    big[123457] = nan
+    rows = [big, np.full(1000, nan, np.float32), np.array([-inf, nan, -inf, nan], np.float32),
+            np.array([nan, -3.0, inf, nan, inf], np.float32)]
+    for i, v in enumerate(rows):
+        ops.argmax(torch.from_numpy(v).to(dev), tokens, i, ws)
+        assert int(tokens[i]) == ref.argmax(v), i
+    assert [int(t) for t in tokens[1:4]] == [0, 0, 2]
+    assert not ws.any()
 
 
 def test_argmax_ties_lowest_index(dev):

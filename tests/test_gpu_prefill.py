@@ -108,7 +108,7 @@ def test_gemm_gate_up_f16(dev, rng, B, F, K, act):
     _close(H.cpu().numpy(), ref.gate_up(Wg, Wu, X.T, act).T)
 
 
-@pytest.mark.parametrize("nh,nkv,hd", [(8, 1, 256), (32, 8, 128), (4, 4, 128), (16, 8, 256)])
+@pytest.mark.parametrize("nh,nkv,hd", [(8, 1, 256), (32, 8, 128), (4, 4, 128), (16, 8, 256), (32, 8, 64)])
 @pytest.mark.parametrize("pos0,rows", [(0, 1), (0, 37), (40, 64), (100, 130)])
 def test_attention_prefill(dev, rng, nh, nkv, hd, pos0, rows):
     """Query t of the chunk sees exactly keys [0, pos0 + t]: the cache past the

@@ -38,7 +38,8 @@ def weights_file(tmp_path_factory):
     from gemmagemini4hackathon2026_10_2425_amd import weights
 
     d = tmp_path_factory.mktemp("hf")
-    _hf_snapshot(d / "snap", om.TINY, int(GOLDEN["seed"]))
+    _hf_snapshot(d / "snap", om.TINY, int(GOLDEN["seed"]), std=float(GOLDEN["std"]),
+                 embed_std=float(GOLDEN["embed_std"]))
     weights.convert_hf(d / "snap", d / "gemma_tiny.bin")
     return d / "gemma_tiny.bin"
 

@@ -10,7 +10,7 @@ import torch
 from gemmagemini4hackathon2026_10_2425_amd import ops
 
 
-@pytest.mark.parametrize("hd", [128, 256])
+@pytest.mark.parametrize("hd", [64, 128, 256])
 @pytest.mark.parametrize("which", ["k", "v"])
 def test_offsets_are_a_tilewise_permutation(hd, which):
     ctx = 96
@@ -57,7 +57,7 @@ def test_to_from_tiles_roundtrip():
 # ---- paged KV cache (16-key pages, one slab per (page, kv head)) -------------
 
 
-@pytest.mark.parametrize("hd", [128, 256])
+@pytest.mark.parametrize("hd", [64, 128, 256])
 @pytest.mark.parametrize("which", ["k", "v"])
 def test_page_offsets_are_a_slab_permutation(hd, which):
     from gemmagemini4hackathon2026_10_2425_amd import batch

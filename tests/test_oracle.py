@@ -292,6 +292,31 @@ def test_argmax_first_max():
     assert ops.argmax(np.zeros(10, np.float32)) == 0
 
 
+def _argmax_scan(v) -> int:
+    """The reference's loop, literally: best = -inf, index 0, take v > best."""
+    best, idx = -math.inf, 0
+    for i, x in enumerate(v):
+        if x > best:
+            best, idx = float(x), i
+    return idx
+
+
+def test_argmax_nan_and_inf_like_the_reference_scan(rng):
+    nan, inf = np.float32("nan"), np.float32("inf")
+    cases = [np.array([nan, 1.0, 3.0, nan], np.float32), np.array([nan, nan], np.float32),
+             np.array([-inf, nan, -inf], np.float32), np.array([2.0, inf, nan, inf], np.float32),
+             np.array([-inf, -5.0], np.float32)]
+    for _ in range(50):
+        v = rng.standard_normal(40).astype(np.float32)
+        v[rng.random(40) < 0.2] = nan
+        v[rng.random(40) < 0.1] = -inf
+        v[rng.random(40) < 0.05] = inf
+        cases.append(v)
+    for v in cases:
+        assert ops.argmax(v) == _argmax_scan(v), v
+    assert ops.argmax(cases[0]) == 2 and ops.argmax(cases[1]) == 0 and ops.argmax(cases[2]) == 0
+
+
 def test_embed_closed_form(rng):
     E = rng.standard_normal((10, 8)).astype(np.float16)
     assert np.array_equal(ops.embed(E, 3, 2.0), E[3].astype(np.float64) * 2.0)
@@ -305,7 +330,8 @@ def test_decode_matches_hf_gemma():
     transformers' GemmaForCausalLM (fp64) on the same weights."""
     z = np.load(__file__.rsplit("/", 1)[0] + "/golden/hf_gemma_tiny.npz")
     cfg = om.TINY
-    d = om.OracleDecoder(cfg, om.make_weights(cfg, int(z["seed"])), 64, fp16_kv=False)
+    d = om.OracleDecoder(cfg, om.make_weights(cfg, int(z["seed"]), float(z["std"]), float(z["embed_std"])), 64,
+                         fp16_kv=False)
     prompt = [int(t) for t in z["prompt"]]
     d.tokens[: len(prompt)] = prompt
     for pos in range(len(prompt)):
@@ -323,7 +349,7 @@ def test_prefill_chunk_pins():
     within the 1e-2 contract of HF's logits and gives HF's first greedy token."""
     z = np.load(__file__.rsplit("/", 1)[0] + "/golden/hf_gemma_tiny.npz")
     cfg = om.TINY
-    w = om.make_weights(cfg, int(z["seed"]))
+    w = om.make_weights(cfg, int(z["seed"]), float(z["std"]), float(z["embed_std"]))
     prompt = [int(t) for t in z["prompt"]]
     P = len(prompt)
     for rows in range(1, P + 1):
@@ -348,19 +374,31 @@ def test_prefill_chunk_pins():
     assert int(whole.tokens[P]) == int(z["greedy"][0])
 
 
-def test_decode_numpy_and_c_restatements_agree():
-    cfg = om.DecodeConfig(n_layers=2, dim=256, n_heads=8, n_kv_heads=1, head_dim=256, ffn_dim=512, vocab=2000)
+_C_VS_NUMPY = [
+    (om.DecodeConfig(n_layers=2, dim=256, n_heads=8, n_kv_heads=1, head_dim=256, ffn_dim=512, vocab=2000), None),
+    # Llama-3.2-1B features: head_dim 64, GQA, Llama-3 RoPE scaling, untied lm_head
+    (om.DecodeConfig(n_layers=2, dim=256, n_heads=8, n_kv_heads=2, head_dim=64, ffn_dim=512, vocab=2000, eps=1e-5,
+                     rope_theta=500000.0, act="silu", gemma_embed_scale=False, plus_one=False, tie_embeddings=False,
+                     rope_scaling=(32.0, 1.0, 4.0, 8192)), None),
+    # the embedding at its own scale
+    (om.DecodeConfig(n_layers=2, dim=256, n_heads=8, n_kv_heads=1, head_dim=256, ffn_dim=512, vocab=2000), 0.005),
+]
+
+
+@pytest.mark.parametrize("cfg,embed_std", _C_VS_NUMPY, ids=["gemma-mqa256", "llama32-hd64-untied", "embed-std"])
+def test_decode_numpy_and_c_restatements_agree(cfg, embed_std):
     seed = 21
-    d = om.OracleDecoder(cfg, om.make_weights(cfg, seed), 64)
-    n = native.NativeDecoder(cfg, 64, seed)
+    d = om.OracleDecoder(cfg, om.make_weights(cfg, seed, embed_std=embed_std), 64)
+    n = native.NativeDecoder(cfg, 64, seed, embed_std=embed_std)
+    assert np.array_equal(n.inv_freq(), d.invf)
     prompt = [7, 1999, 0, 1234, 55]
     t1, m1 = d.generate(prompt, 10)
     t2, m2 = n.generate(prompt, 10)
     assert t1 == t2
     assert np.allclose(m1, m2, rtol=1e-4, atol=1e-5)
-    d2 = om.OracleDecoder(cfg, om.make_weights(cfg, seed), 64)
+    d2 = om.OracleDecoder(cfg, om.make_weights(cfg, seed, embed_std=embed_std), 64)
     d2.tokens[: len(prompt)] = prompt
-    n2 = native.NativeDecoder(cfg, 64, seed)
+    n2 = native.NativeDecoder(cfg, 64, seed, embed_std=embed_std)
     n2.tokens[: len(prompt)] = prompt
     for pos in range(len(prompt)):
         a = d2.forward(pos)

@@ -99,20 +99,52 @@ def test_shape_from_config():
     s = W.shape_from_config(llama)
     assert s.head_dim == 128 and s.act == "silu" and not s.norm_plus_one and not s.embed_scale_sqrt_dim
     assert s.rms_eps == 1e-5 and s.rope_theta == 500000.0
-    for bad, msg in [({"rope_scaling": {"rope_type": "llama3", "factor": 32.0}}, "rope_scaling"),
-                     ({"tie_word_embeddings": False}, "untied"), ({"model_type": "gemma3"}, "model_type"),
+    assert s.tie_embeddings and s.rope_scaling is None
+    assert not W.shape_from_config(dict(llama, tie_word_embeddings=False)).tie_embeddings
+    l3 = {"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+          "original_max_position_embeddings": 8192}
+    assert W.shape_from_config(dict(llama, rope_scaling=l3)).rope_scaling == (32.0, 1.0, 4.0, 8192)
+    for bad, msg in [({"rope_scaling": {"rope_type": "llama3", "factor": 32.0}}, "lacks"),
+                     ({"rope_scaling": {"rope_type": "yarn", "factor": 4.0}}, "not supported"),
+                     ({"model_type": "gemma3"}, "model_type"),
                      ({"hidden_act": "relu"}, "activation"), ({"attention_bias": True}, "bias")]:
         with pytest.raises(ValueError, match=msg):
             W.shape_from_config(dict(llama, **bad))
 
 
-def _hf_snapshot(d: Path, cfg, seed: int, bf16_norms: bool = False) -> dict:
+def test_shape_from_transformers5_configs():
+    """transformers 5.x keeps rope_theta and the scaling inside rope_parameters
+    (the layout of every checkpoint the installed version saves); a Llama-3.2-1B
+    config maps to the engine's Llama-3.2-1B shape."""
+    from transformers import LlamaConfig
+
+    from gemmagemini4hackathon2026_10_2425_amd.engine import LLAMA32_1B
+
+    W = _w()
+    rp = {"rope_type": "llama3", "rope_theta": 500000.0, "factor": 32.0, "low_freq_factor": 1.0,
+          "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}
+    hc = LlamaConfig(vocab_size=128256, hidden_size=2048, intermediate_size=8192, num_hidden_layers=16,
+                     num_attention_heads=32, num_key_value_heads=8, head_dim=64, rms_norm_eps=1e-5,
+                     max_position_embeddings=131072, tie_word_embeddings=True, rope_parameters=rp).to_dict()
+    assert "rope_theta" not in hc  # the layout this test is about
+    assert W.shape_from_config(hc) == LLAMA32_1B
+    plain = LlamaConfig(hidden_size=512, intermediate_size=1024, num_attention_heads=4, num_hidden_layers=1,
+                        rope_parameters={"rope_type": "default", "rope_theta": 250000.0}).to_dict()
+    s = W.shape_from_config(plain)
+    assert s.rope_theta == 250000.0 and s.rope_scaling is None
+    yarn = dict(plain, rope_parameters={"rope_type": "yarn", "rope_theta": 1e4, "factor": 4.0})
+    with pytest.raises(ValueError, match="not supported"):
+        W.shape_from_config(yarn)
+
+
+def _hf_snapshot(d: Path, cfg, seed: int, bf16_norms: bool = False, std: float = 0.02,
+                 embed_std: float | None = None) -> dict:
     """A local HF-layout checkpoint (config.json + model.safetensors) whose
     tensors are the oracle's synthetic weights split back into q/k/v."""
     import torch
     from safetensors.torch import save_file
 
-    w = om.make_weights(cfg, seed)
+    w = om.make_weights(cfg, seed, std, embed_std)
     hd, nh, nkv = cfg.head_dim, cfg.n_heads, cfg.n_kv_heads
     sd = {"model.embed_tokens.weight": w["embed"], "model.norm.weight": w["final_norm"]}
     for l in range(cfg.n_layers):
