@@ -200,23 +200,26 @@ def test_engine_long_context_decode(dev, cfg, max_ctx):
     ref.tokens[:P] = prompt
     for pos in range(P - 1):
         ref.step(pos, sample=False)
+    _, _, want = ref.step(P - 1, want_logits=True, sample=True)
     with _engine(cfg, max_ctx, seed) as a, _engine(cfg, max_ctx, seed) as b:
         _lib.set_tunable("ENG_NO_GEMM", 1)
         try:
             for e in (a, b):
                 e.set_tokens(prompt)
-                e.prefill(P - 1)  # positions 0 .. P-2, as the oracle above
+                e.prefill(P)  # positions 0 .. P-1 step by step, sampling tokens[P]
         finally:
             _lib.set_tunable("ENG_NO_GEMM", 0)
-        for pos in range(P - 1, P - 1 + N):
+        assert rel_err(a.logits(), want) <= 1e-3
+        assert a.token(P) == int(ref.tokens[P])
+        for pos in range(P, P + N):
             _, _, want = ref.step(pos, want_logits=True, sample=True)
             a.decode(pos, 1)
             b.step(pos)
             got = a.logits()
             assert rel_err(got, want) <= 1e-3, f"pos {pos}"
             assert np.array_equal(got, b.logits()), f"pos {pos}: graph and eager steps differ"
-        assert a.tokens(P, N) == [int(t) for t in ref.tokens[P : P + N]]
-        assert b.tokens(P, N) == a.tokens(P, N)
+        assert a.tokens(P, N + 1) == [int(t) for t in ref.tokens[P : P + N + 1]]
+        assert b.tokens(P, N + 1) == a.tokens(P, N + 1)
 
 
 @pytest.mark.parametrize("window", [1, 3, 16])

@@ -5,8 +5,11 @@ kernel_runner.py:29-44, and the benchmark harness, ios_kernels/benchmarking/
 bench.py:45-61, start it) and must reproduce HF transformers' greedy tokens and
 logits for that checkpoint (tests/golden/hf_gemma_tiny.npz).
 
-Tolerances: logits max|got - ref| / max|ref| <= 1e-3 (fp16 weights, fp32
-accumulation against HF in float64; the contract is 1e-2); token ids identical.
+Tolerances: token ids identical. Logits, max|got - ref| / max|ref| against HF
+in float64: <= 1e-3 through the token-by-token prefill (fp16 weights, fp32
+activations and accumulation), and the 1e-2 contract through the batched
+prefill, which rounds its activation rows to fp16 where the reference's prefill
+chunk does (xnHalf / attHalf / hidHalf, KL/main.swift:412-446).
 """
 
 from __future__ import annotations
@@ -55,10 +58,19 @@ def test_load_engine_matches_hf(dev, weights_file):
     """In process: the loaded engine's greedy tokens equal HF's."""
     from gemmagemini4hackathon2026_10_2425_amd.weights import load_engine
 
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
     with load_engine(weights_file, 64) as e:
         assert e.generate(PROMPT, len(GREEDY)) == GREEDY
         e.set_tokens(PROMPT)
         e.prefill(len(PROMPT))
+        assert rel_err(e.logits(), GOLDEN["logits"][-1]) <= 1e-2
+        _lib.set_tunable("ENG_NO_GEMM", 1)
+        try:
+            e.set_tokens(PROMPT)
+            e.prefill(len(PROMPT))
+        finally:
+            _lib.set_tunable("ENG_NO_GEMM", 0)
         assert rel_err(e.logits(), GOLDEN["logits"][-1]) <= 1e-3
 
 
@@ -105,7 +117,13 @@ def test_cli_generate_and_dump_logits(dev, weights_file, tmp_path):
     r = json.loads(out.strip().splitlines()[-1])
     assert r["tokens"] == GREEDY and r["decode_tok_s"] > 0
     logits = np.fromfile(tmp_path / "logits.f32", "<f4")
-    assert logits.shape == (om.TINY.vocab,) and rel_err(logits, GOLDEN["logits"][-1]) <= 1e-3
+    assert logits.shape == (om.TINY.vocab,) and rel_err(logits, GOLDEN["logits"][-1]) <= 1e-2
+    rc, out, err = _run(["--weights", weights_file, "--max-ctx", 64, "--prompt-ids", ",".join(map(str, PROMPT)),
+                         "--gen", len(GREEDY), "--dump-logits", tmp_path / "logits_nogemm.f32", "--no-gemm"])
+    assert rc == 0, err[-2000:]
+    assert json.loads(out.strip().splitlines()[-1])["tokens"] == GREEDY
+    logits = np.fromfile(tmp_path / "logits_nogemm.f32", "<f4")
+    assert rel_err(logits, GOLDEN["logits"][-1]) <= 1e-3
 
 
 def test_cli_bench_lines(dev, weights_file):
