@@ -106,6 +106,8 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_rope_kv": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),
     "mxd_attention_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "mxd_attention": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, P, c_size_t, P]),
+    "mxd_attention_noalloc_max_scratch": (c_size_t, []),
+    "mxd_attention_noalloc": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, P]),
     "mxd_attention_split": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, c_int, P, c_size_t, P]),
     "mxd_attention_prefill": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P]),
     "mxd_argmax_workspace_size": (c_size_t, [c_int]),

@@ -44,7 +44,9 @@
 //  * K and V are read with nontemporal loads: they stream through once.
 #include "common.hpp"
 
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 namespace {
 
@@ -1110,4 +1112,60 @@ extern "C" int mxd_attention_paged(const float* q, int q_stride, const uint16_t*
             hipLaunchKernelGGL(attn_paged_merge_kernel<HD>, dim3(n_heads * HD / MG_D, n_seqs), dim3(MG_T), 0, s, a);
     });
     return mxd::check_launch("mxd_attention_paged");
+}
+
+// ---------------------------------------------------------------------------
+// mxd_attention without a workspace argument, for callers that cannot
+// allocate: the split partials live in a file-scope device array, one per GPU,
+// held until the process ends. Its device address comes from
+// hipGetSymbolAddress on each device's first call (the host-side name of the
+// array is not a device address) and is kept per device.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)8 << 20;  // 8 MiB per GPU
+__device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_dev;  // scratch's address on device d, or null
+
+int scratch_address(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return mxd::fail(MXD_ERR_HIP, "mxd_attention_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((size_t)dev >= g_scratch_dev.size()) g_scratch_dev.resize(dev + 1, nullptr);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return mxd::fail(MXD_ERR_HIP, "mxd_attention_noalloc: hipGetSymbolAddress(scratch): %s",
+                             hipGetErrorString(e));
+        g_scratch_dev[dev] = p;
+    }
+    *out = g_scratch_dev[dev];
+    return MXD_OK;
+}
+
+}  // namespace
+
+extern "C" size_t mxd_attention_noalloc_max_scratch(void) { return NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int mxd_attention_noalloc(const float* q, const uint16_t* kcache, const uint16_t* vcache, float* out,
+                                     int n_heads, int n_kv_heads, int head_dim, int max_ctx, int n_keys,
+                                     const int32_t* n_keys_dev, float scale, mxd_stream_t stream) {
+    // The partials mxd_attention would take from its workspace; the shape
+    // itself is checked there.
+    MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && max_ctx > 0, MXD_ERR_INVALID_ARG,
+                "mxd_attention_noalloc: n_heads=%d n_kv_heads=%d head_dim=%d max_ctx=%d", n_heads, n_kv_heads,
+                head_dim, max_ctx);
+    const int splits = splits_for(n_keys_dev ? max_ctx : max(n_keys, 1), n_kv_heads);
+    const size_t need = (size_t)splits * n_heads * (head_dim + 2) * sizeof(float);
+    MXD_REQUIRE(need <= NOALLOC_SCRATCH_BYTES, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_noalloc: this shape needs %zu bytes of split partials, above the %zu-byte scratch",
+                need, NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if (int rc = scratch_address(&ws)) return rc;
+    return mxd_attention(q, kcache, vcache, out, n_heads, n_kv_heads, head_dim, max_ctx, n_keys, n_keys_dev, scale,
+                         ws, NOALLOC_SCRATCH_BYTES, stream);
 }

@@ -192,6 +192,19 @@ int mxd_attention(const float* q, const uint16_t* kcache, const uint16_t* vcache
                   const int32_t* n_keys_dev, float scale, void* workspace, size_t ws_bytes,
                   mxd_stream_t stream);
 
+/* mxd_attention for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): the same
+ * kernels and arguments without the workspace; no reference counterpart. The
+ * split partials live in a device array of mxd_attention_noalloc_max_scratch()
+ * bytes (8 MiB) that the library holds on each GPU it runs on until the process
+ * ends; a shape needing more returns MXD_ERR_UNSUPPORTED. The call allocates
+ * nothing. Every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU (different streams, or threads) race: serialise them. */
+size_t mxd_attention_noalloc_max_scratch(void);
+int mxd_attention_noalloc(const float* q, const uint16_t* kcache, const uint16_t* vcache, float* out,
+                          int n_heads, int n_kv_heads, int head_dim, int max_ctx, int n_keys,
+                          const int32_t* n_keys_dev, float scale, mxd_stream_t stream);
+
 /* The split half of mxd_attention without its merge: split s of n_splits
  * (1 .. 512) takes the 32-key blocks s, s + n_splits, ... and writes its
  * unnormalised partial, O to partials[s][h][0..hd) and (max, sum) of its
