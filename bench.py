@@ -317,16 +317,21 @@ def ragged_layer_leg(steps: int, warmup: int, dev, n_seqs: int = 64) -> dict:
             "kv_tokens": int(lens.sum()), "tok_s": n_seqs / ms * 1e3, "gemm_tflops": flops / ms / 1e9}
 
 
-def decode_leg(n_new: int = 256, prompt_len: int = 128, reps: int = 3) -> dict:
-    """Gemma-2B-shaped greedy decode, timed like the reference's --bench-tg
-    (KL/main.swift:605-618): wall clock over a run of pipelined steps that
-    sample on the GPU, one host sync at the end."""
+def decode_leg(n_new: int = 256, prompt_len: int = 128, reps: int = 3, max_ctx: int | None = None,
+               model: str = "gemma2b", window: int = 0) -> dict:
+    """Greedy decode of the Gemma-2B (or Llama-3.2-1B) shape, timed like the
+    reference's --bench-tg (KL/main.swift:605-618): wall clock over a run of
+    pipelined steps that sample on the GPU, one host sync at the end. max_ctx
+    defaults to the run's length (384); the serve binary's default is 4096,
+    where the attention runs as split + merge launches sized for the whole
+    context. With window > 0 the run is the streaming decode the --serve path
+    uses (window steps in flight, the host waiting for each token)."""
     import numpy as np
 
-    from gemmagemini4hackathon2026_10_2425_amd.engine import GEMMA_2B, Engine
+    from gemmagemini4hackathon2026_10_2425_amd.engine import GEMMA_2B, LLAMA32_1B, Engine
 
-    shape = GEMMA_2B
-    max_ctx = (prompt_len + n_new + 31) // 32 * 32
+    shape = GEMMA_2B if model == "gemma2b" else LLAMA32_1B
+    max_ctx = max_ctx or (prompt_len + n_new + 31) // 32 * 32
     with Engine(shape, max_ctx) as e:
         e.init_random(1234)
         prompt = np.random.default_rng(1234).integers(0, shape.vocab, prompt_len).tolist()
@@ -336,15 +341,21 @@ def decode_leg(n_new: int = 256, prompt_len: int = 128, reps: int = 3) -> dict:
         rates = []
         for _ in range(reps):
             t0 = time.perf_counter()
-            e.decode(prompt_len, n_new - 1)
+            if window:
+                e.decode_streaming(prompt_len, n_new - 1, lambda t: True, window)
+            else:
+                e.decode(prompt_len, n_new - 1)
             rates.append((n_new - 1) / (time.perf_counter() - t0))
     rate = float(np.median(rates))
-    # bytes per token: every weight once (tied LM head read twice: embed row + head) + the KV read
+    # bytes per token: every weight once (a tied head is read twice: embed row + head) + the KV read
     kv_avg = 2 * shape.n_layers * shape.n_kv_heads * shape.head_dim * 2 * (prompt_len + n_new / 2)
     per_tok = shape.weight_bytes + kv_avg
-    return {"tok_s": rate, "ms_per_token": 1e3 / rate, "bytes_per_token": per_tok, "gbs": per_tok * rate / 1e9,
-            "frac": per_tok * rate / 1e9 / PEAK_HBM_GBS, "roof_tok_s": PEAK_HBM_GBS * 1e9 / per_tok,
-            "prompt": prompt_len, "generated": n_new}
+    out = {"tok_s": rate, "ms_per_token": 1e3 / rate, "bytes_per_token": per_tok, "gbs": per_tok * rate / 1e9,
+           "frac": per_tok * rate / 1e9 / PEAK_HBM_GBS, "roof_tok_s": PEAK_HBM_GBS * 1e9 / per_tok,
+           "prompt": prompt_len, "generated": n_new, "max_ctx": max_ctx}
+    if window:
+        out["streaming_window"] = window
+    return out
 
 
 def prefill_leg(prompt_len: int = 512, reps: int = 3) -> dict:
@@ -408,8 +419,8 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemv_f16",
-                    choices=["gemv_f16", "gemv_q8", "gemv_size_fit", "attention", "decode", "prefill", "ragged_layer",
-                             "copy"])
+                    choices=["gemv_f16", "gemv_q8", "gemv_size_fit", "attention", "decode", "decode_4096",
+                             "decode_streaming", "decode_llama32_1b", "prefill", "ragged_layer", "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-detail", action="store_true", help="skip the int8 / attention detail legs")
     args = ap.parse_args(argv)
@@ -434,6 +445,9 @@ def main(argv=None) -> int:
                 "gemv_size_fit": lambda: gemv_size_fit_leg(args.steps, args.warmup, dev),
                 "attention": lambda: attention_leg(args.steps, args.warmup, dev),
                 "decode": decode_leg,
+                "decode_4096": lambda: decode_leg(max_ctx=4096),
+                "decode_streaming": lambda: decode_leg(max_ctx=4096, window=3),
+                "decode_llama32_1b": lambda: decode_leg(model="llama32_1b"),
                 "prefill": prefill_leg,
                 "ragged_layer": lambda: ragged_layer_leg(args.steps, args.warmup, dev),
                 "copy": lambda: copy_leg(args.steps, args.warmup, dev)}
@@ -453,6 +467,15 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
         log("decode leg")
         detail["decode_gemma2b"] = decode_leg()
+        torch.cuda.empty_cache()
+        log("decode leg at the serve default max_ctx 4096")
+        detail["decode_gemma2b_maxctx4096"] = decode_leg(max_ctx=4096)
+        torch.cuda.empty_cache()
+        log("streaming decode leg (window 3, max_ctx 4096)")
+        detail["decode_gemma2b_streaming"] = decode_leg(max_ctx=4096, window=3)
+        torch.cuda.empty_cache()
+        log("Llama-3.2-1B decode leg")
+        detail["decode_llama32_1b"] = decode_leg(model="llama32_1b")
         torch.cuda.empty_cache()
         log("ragged batch leg")
         detail["ragged_layer_llama8b_64seq"] = ragged_layer_leg(args.steps, args.warmup, dev)
