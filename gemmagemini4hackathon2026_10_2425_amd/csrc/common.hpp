@@ -145,4 +145,53 @@ __host__ __device__ __forceinline__ int v_page_offset(int r, int d) {
     return (((d >> 4) * 2 + (r >> 3)) * 16 + (d & 15)) * 8 + (r & 7);
 }
 
+
+// ---------------------------------------------------------------------------
+// Tagged handoff words. A kernel whose workgroups pass values to each other
+// (the fused decode attention block) stores each fp32 value with a 32-bit tag
+// in one 8-byte word, written and read whole with agent-scope relaxed atomics
+// (coherent across the XCDs' L2s without fences). A reader takes a word only
+// once it carries the current launch's tag; stale words from earlier launches
+// carry older tags. Waits are bounded: past TAG_SPIN_LIMIT polls the reader
+// records an error in *err and goes on with what it read, and once the error
+// is set every later wait returns at once.
+// ---------------------------------------------------------------------------
+constexpr unsigned TAG_SPIN_LIMIT = 1u << 16;
+
+__device__ __forceinline__ void tag_put(uint64_t* p, uint32_t tag, float v) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t tag_peek(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool tag_ok(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+
+__device__ __forceinline__ float tag_value(uint64_t w) { return __uint_as_float((uint32_t)w); }
+
+// Loads N words per lane (p[i], or nothing where p[i] is null) until every
+// lane of the wave holds words carrying `tag`; returns their values.
+template <int N>
+__device__ __forceinline__ void tag_wait(const uint64_t* const (&p)[N], uint32_t tag, float (&v)[N], int* err) {
+    unsigned spins = 0;
+    const bool failed = err && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+    while (true) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            if (!p[i]) continue;
+            const uint64_t w = tag_peek(p[i]);
+            ok = ok && tag_ok(w, tag);
+            v[i] = tag_value(w);
+        }
+        if (__all(ok) || failed) return;
+        if (++spins > TAG_SPIN_LIMIT) {
+            if (err) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+}
+
 }  // namespace mxd

@@ -97,6 +97,14 @@ struct mxd_engine {
     // The position the last decode run left in the device counter (-1: not
     // known), so a run that continues from it needs no counter write.
     int pos_next = -1;
+    // The fused attention half of each layer (attn_block): its workspace of
+    // tagged words, the step counter its tags come from (advanced by the
+    // embedding kernel of every step) and its error word.
+    bool fused = false;
+    void* ab_ws = nullptr;
+    size_t ab_ws_bytes = 0;
+    int32_t* step = nullptr;
+    int* ab_err = nullptr;
     // prefill chunk buffers: rows x {dim f32, dim f16, qkv f32, q f32, ffn f32}
     // (the products round fp32 rows to fp16 as they load them), and the
     // products' split-K workspace
@@ -172,30 +180,39 @@ int encode_step(mxd_engine* e, int pos, int32_t* pos_dev, bool sample) {
     const float escale = c.embed_scale_sqrt_dim ? sqrtf((float)D) : 1.0f;
     const float ascale = 1.0f / sqrtf((float)HD);
     int rc;
-    if ((rc = mxd::embed_dev(e->embed, e->tokens, pos, pos_dev, 1, e->x, D, escale, V, s))) return rc;
-    // Per layer, five launches: [rmsnorm + qkv + rope + append], attention,
-    // [wo + residual], [rmsnorm + gate_up], [down + residual].
+    if ((rc = mxd::embed_dev(e->embed, e->tokens, pos, pos_dev, 1, e->x, D, escale, V, s, e->step))) return rc;
+    // Per layer, three launches: [rmsnorm + qkv + rope + append + attention +
+    // wo + residual] (attn_block), [rmsnorm + gate_up], [down + residual]; or,
+    // unfused, five: [rmsnorm + qkv + rope + append], attention, [wo +
+    // residual], [rmsnorm + gate_up], [down + residual].
     for (int l = 0; l < c.n_layers; ++l) {
         const LayerPtrs& Lp = e->L[l];
-        if ((rc = mxd_qkv_rope_kv(Lp.wqkv, e->x, Lp.attn_norm, c.rms_eps, c.norm_plus_one, e->qkv, Lp.kc, Lp.vc,
-                                  e->invf, NH, NKV, HD, D, e->max_ctx, pos, pos_dev, ms)))
-            return rc;
-        if (e->att_splits) {
-            // The attention leaves its splits' partials; the o projection
-            // merges them as it loads its input (no merge launch).
-            float* part = static_cast<float*>(e->attn_ws);
-            if ((rc = mxd_attention_split(e->qkv, Lp.kc, Lp.vc, NH, NKV, HD, e->max_ctx, pos + 1, pos_dev, ascale,
-                                          e->att_splits, part, e->attn_ws_bytes, ms)))
-                return rc;
-            if ((rc = mxd_matvec_f16_attn_merge(Lp.wo, part, e->att_splits, NH, HD, e->max_ctx, pos + 1, pos_dev,
-                                                e->x, D, MXD_EPI_ADD, nullptr, ms)))
+        if (e->fused) {
+            if ((rc = mxd::attn_block(Lp.wqkv, Lp.wo, e->x, Lp.attn_norm, c.rms_eps, c.norm_plus_one, Lp.kc, Lp.vc,
+                                      e->invf, NH, NKV, HD, D, e->max_ctx, pos, pos_dev, ascale, e->step, l, e->ab_ws,
+                                      e->ab_ws_bytes, s)))
                 return rc;
         } else {
-            if ((rc = mxd_attention(e->qkv, Lp.kc, Lp.vc, e->att, NH, NKV, HD, e->max_ctx, pos + 1, pos_dev, ascale,
-                                    e->attn_ws, e->attn_ws_bytes, ms)))
+            if ((rc = mxd_qkv_rope_kv(Lp.wqkv, e->x, Lp.attn_norm, c.rms_eps, c.norm_plus_one, e->qkv, Lp.kc, Lp.vc,
+                                      e->invf, NH, NKV, HD, D, e->max_ctx, pos, pos_dev, ms)))
                 return rc;
-            if ((rc = mxd_matvec_f16(Lp.wo, e->att, MXD_F32, e->x, D, e->q_dim(), MXD_EPI_ADD, nullptr, ms)))
-                return rc;
+            if (e->att_splits) {
+                // The attention leaves its splits' partials; the o projection
+                // merges them as it loads its input (no merge launch).
+                float* part = static_cast<float*>(e->attn_ws);
+                if ((rc = mxd_attention_split(e->qkv, Lp.kc, Lp.vc, NH, NKV, HD, e->max_ctx, pos + 1, pos_dev, ascale,
+                                              e->att_splits, part, e->attn_ws_bytes, ms)))
+                    return rc;
+                if ((rc = mxd_matvec_f16_attn_merge(Lp.wo, part, e->att_splits, NH, HD, e->max_ctx, pos + 1, pos_dev,
+                                                    e->x, D, MXD_EPI_ADD, nullptr, ms)))
+                    return rc;
+            } else {
+                if ((rc = mxd_attention(e->qkv, Lp.kc, Lp.vc, e->att, NH, NKV, HD, e->max_ctx, pos + 1, pos_dev,
+                                        ascale, e->attn_ws, e->attn_ws_bytes, ms)))
+                    return rc;
+                if ((rc = mxd_matvec_f16(Lp.wo, e->att, MXD_F32, e->x, D, e->q_dim(), MXD_EPI_ADD, nullptr, ms)))
+                    return rc;
+            }
         }
         if ((rc = mxd_gate_up_rmsnorm(Lp.wgate, Lp.wup, e->x, Lp.ffn_norm, c.rms_eps, c.norm_plus_one, e->h, F, D,
                                       c.act, ms)))
@@ -326,6 +343,14 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
         const size_t need = (size_t)splits * c.n_heads * (c.head_dim + 2) * sizeof(float);
         if (e->att_splits && e->attn_ws_bytes < need) e->attn_ws_bytes = need;
     }
+    // The fused attention block (ENG_FUSED = 1) takes the attention half of
+    // every layer in one launch (models of at most 64 layers and attention
+    // heads of at most 8192 values). Off by default: measured on MI355X, its
+    // in-kernel handoffs between XCDs cost more than the kernel boundaries
+    // they replace (Gemma-2B layer: 31 us against 18.8 us for the three
+    // launches; per-workgroup stamps put 5-12 us on each handoff).
+    e->fused = mxd::tunable("ENG_FUSED", 2) == 1 && c.n_layers <= 64 && c.n_heads * c.head_dim <= 8192;
+    e->ab_ws_bytes = e->fused ? mxd::attn_block_workspace_size(c.n_heads, c.n_kv_heads, c.head_dim, max_ctx) : 0;
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
@@ -336,6 +361,7 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
     const size_t o_att = take((size_t)e->q_dim() * 4), o_h = take(F * 4), o_logits = take((size_t)c.vocab * 4);
     const size_t o_invf = take((size_t)c.head_dim / 2 * 4), o_tok = take(((size_t)max_ctx + 1) * 4), o_pos = take(4);
     const size_t o_aws = take(e->attn_ws_bytes), o_am = take(mxd_argmax_workspace_size(c.vocab));
+    const size_t o_abws = take(max(e->ab_ws_bytes, (size_t)16)), o_step = take(4);
     const size_t B = (size_t)(e->max_rows = min(PREFILL_ROWS, max_ctx));
     e->gm_ws_bytes = prefill_ws_bytes(c, e->qkv_dim(), e->q_dim(), e->max_rows);
     const size_t o_bx = take(B * D * 4), o_bxn = take(B * D * 2), o_bqkv = take(B * e->qkv_dim() * 4);
@@ -377,6 +403,11 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
     e->pos = reinterpret_cast<int32_t*>(a + o_pos);
     e->attn_ws = a + o_aws;
     e->am_ws = a + o_am;
+    e->step = reinterpret_cast<int32_t*>(a + o_step);
+    if (e->fused) {
+        e->ab_ws = a + o_abws;
+        e->ab_err = mxd::attn_block_err(e->ab_ws, c.n_heads, c.n_kv_heads, c.head_dim, max_ctx);
+    }
     e->bx = reinterpret_cast<float*>(a + o_bx);
     e->bxn = reinterpret_cast<uint16_t*>(a + o_bxn);
     e->bqkv = reinterpret_cast<float*>(a + o_bqkv);
@@ -590,6 +621,12 @@ extern "C" int mxd_engine_wait_token(mxd_engine* e, int pos, int32_t* token) {
 extern "C" int mxd_engine_sync(mxd_engine* e) {
     MXD_REQUIRE(e, MXD_ERR_INVALID_ARG, "mxd_engine_sync: null engine");
     HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_sync");
+    if (e->ab_err) {
+        int err = 0;
+        HIP_OK(hipMemcpy(&err, e->ab_err, sizeof(int), hipMemcpyDeviceToHost), "mxd_engine_sync");
+        MXD_REQUIRE(err == 0, MXD_ERR_HIP, "mxd_engine_sync: a wait between workgroups of the fused attention block "
+                                           "ran out (results of this run are not valid)");
+    }
     return MXD_OK;
 }
 

@@ -8,8 +8,21 @@
 
 namespace mxd {
 
+// With step_counter, the kernel also advances *step_counter by one (the decode
+// step count the fused attention block derives its tags from).
 int embed_dev(const uint16_t* E, const int32_t* tokens, int pos, const int32_t* pos_dev, int rows, float* x, int D,
-              float scale, int vocab, hipStream_t s);
+              float scale, int vocab, hipStream_t s, int32_t* step_counter = nullptr);
+
+// The fused attention half of a decode layer (attn_block.hip): x +=
+// Wo . attention(RoPE(q), K, V) with [q|k|v] = Wqkv . rmsnorm(x), the new k, v
+// appended at pos (or *pos_dev), in one launch. step_dev: a counter advanced
+// once per decode step; layer < 64 tells the layers of a step apart.
+size_t attn_block_workspace_size(int n_heads, int n_kv, int hd, int max_ctx);
+int attn_block(const uint16_t* wqkv, const uint16_t* wo, float* x, const float* norm_w, float eps, int plus_one,
+               uint16_t* kcache, uint16_t* vcache, const float* inv_freq, int n_heads, int n_kv, int hd, int dim,
+               int max_ctx, int pos, const int32_t* pos_dev, float scale, const int32_t* step_dev, int layer,
+               void* workspace, size_t ws_bytes, hipStream_t s);
+int* attn_block_err(void* workspace, int n_heads, int n_kv, int hd, int max_ctx);
 
 int rope_kv_dev(float* qkv, uint16_t* kcache, uint16_t* vcache, const float* inv_freq, int n_heads, int n_kv, int hd,
                 int max_ctx, int pos0, int rows, const int32_t* pos_dev, hipStream_t s);

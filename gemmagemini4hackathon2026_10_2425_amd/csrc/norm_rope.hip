@@ -74,9 +74,10 @@ rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w, YT* __r
 // With pos_dev set, the position is read on the device (a replayed step).
 __global__ void __launch_bounds__(256) embed_kernel(const uint16_t* __restrict__ E, const int32_t* __restrict__ tokens,
                                                     int pos, const int32_t* __restrict__ pos_dev, float* __restrict__ x,
-                                                    int D, float scale, int vocab) {
+                                                    int D, float scale, int vocab, int32_t* step_counter) {
     const int r = blockIdx.y;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (step_counter && i == 0 && r == 0) step_counter[0] += 1;
     if (i >= D) return;
     if (pos_dev) pos = pos_dev[0];
     const int tok = tokens[pos + r];
@@ -173,9 +174,9 @@ rope_kv_paged_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kpool, uint
 namespace mxd {
 
 int embed_dev(const uint16_t* E, const int32_t* tokens, int pos, const int32_t* pos_dev, int rows, float* x, int D,
-              float scale, int vocab, hipStream_t s) {
+              float scale, int vocab, hipStream_t s, int32_t* step_counter) {
     hipLaunchKernelGGL(embed_kernel, dim3((D + 255) / 256, rows), dim3(256), 0, s, E, tokens, pos, pos_dev, x, D, scale,
-                       vocab);
+                       vocab, step_counter);
     return check_launch("embed");
 }
 

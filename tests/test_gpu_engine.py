@@ -72,8 +72,22 @@ def test_engine_untied_head_and_scaled_rope_weights(dev):
         assert not np.array_equal(got, e.download("embed", np.float16).reshape(cfg.vocab, cfg.dim))
 
 
+@pytest.fixture(params=["fused", "unfused"])
+def attn_mode(request):
+    """The attention half of each layer as one fused launch (attn_block, the
+    default) or as the qkv, attention and o-projection launches (ENG_FUSED=2);
+    read when an engine is created."""
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
+    _lib.set_tunable("ENG_FUSED", 1 if request.param == "fused" else 2)
+    try:
+        yield request.param
+    finally:
+        _lib.set_tunable("ENG_FUSED", 0)
+
+
 @pytest.mark.parametrize("cfg", CONFIGS, ids=CONFIG_IDS)
-def test_engine_steps_match_oracle(dev, cfg):
+def test_engine_steps_match_oracle(dev, cfg, attn_mode):
     seed, max_ctx = 5, 96
     prompt = [3, 999 % cfg.vocab, 0, 17, 250, 250, 42]
     ref = om.OracleDecoder(cfg, om.make_weights(cfg, seed), max_ctx)
@@ -156,7 +170,7 @@ def test_engine_batched_prefill_logits(dev, cfg):
             assert rel_err(e.logits(), ref.forward(P)) <= 1e-3, f"step after prefill, P {P}"
 
 
-def test_graph_decode_equals_eager_steps(dev):
+def test_graph_decode_equals_eager_steps(dev, attn_mode):
     """decode() replays one captured step at a device-held position; it must give
     bit-identical tokens and logits to eager steps."""
     cfg, seed, max_ctx = SMALL_GQA, 3, 128
@@ -183,7 +197,7 @@ def test_graph_decode_equals_eager_steps(dev):
 @pytest.mark.parametrize("cfg", [SMALL_GQA, SMALL_LLAMA32, SMALL_MQA256], ids=["llama-gqa", "llama32-hd64-untied",
                                                                               "gemma-mqa256"])
 @pytest.mark.parametrize("max_ctx", [2048, 4096])
-def test_engine_long_context_decode(dev, cfg, max_ctx):
+def test_engine_long_context_decode(dev, cfg, max_ctx, attn_mode):
     """Past 1024 keys of max_ctx the engine's step runs the attention as split
     and merge launches sized for the whole context, inside the captured graph
     (the serve binary's default max_ctx is 4096). A 1500-token prompt stepped
