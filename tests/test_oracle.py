@@ -507,3 +507,60 @@ def test_batch_layer_step_ragged_equals_single_sequences():
     for b in range(len(lens)):
         alone = _stagger(cfg, W, [lens[b]], [0], [X[b]], half_acts=True, kv_dtype=np.float16)[0]
         assert np.allclose(together[b], alone, rtol=1e-6, atol=1e-7), b
+
+
+# ---------------------------------------------------------------- Gemma-4 (oracle.gemma4)
+
+
+def _g4_golden():
+    from oracle import gemma4 as g4
+
+    z = np.load(Path(__file__).resolve().parent / "golden" / "hf_gemma4_tiny.npz")
+    return g4, z, [int(t) for t in z["prompt"]]
+
+
+def test_gemma4_matches_hf_gemma4():
+    """Every prompt position's logits (softcapped) equal transformers'
+    Gemma4ForCausalLM in float64 on the same weights, up to the oracle's fp32
+    storage between ops (K/V kept in fp64 here), and the greedy continuation
+    with the device's fp16 K/V is HF's: sliding window, proportional RoPE, KV
+    sharing, double-width MLPs, q/k/v norms, sandwich norms, per-layer
+    embeddings and layer scalars are all in the tiny config."""
+    g4, z, prompt = _g4_golden()
+    cfg = g4.G4_TINY
+    w = g4.make_weights(cfg, int(z["seed"]))
+    d = g4.G4Decoder(cfg, w, 64, fp16_kv=False)
+    d.tokens[: len(prompt)] = prompt
+    for pos in range(len(prompt)):
+        lg = d.softcap(d.forward(pos))
+        ref = z["logits"][pos]
+        assert np.abs(lg - ref).max() / np.abs(ref).max() < 2e-5, pos
+    toks, margins = g4.G4Decoder(cfg, w, 64).generate(prompt, len(z["greedy"]))
+    assert toks == [int(t) for t in z["greedy"]]
+    assert len(set(toks)) == len(toks)  # a run that changes token every step
+
+
+def test_gemma4_e2b_layer_facts():
+    """The E2B per-layer facts as the reference's converter resolves them
+    (KG/convert_weights.py engine_config, KG/PLAN.md:25-44)."""
+    from oracle import gemma4 as g4
+
+    L = g4.G4_E2B.layers
+    assert len(L) == 35
+    assert [l for l, lay in enumerate(L) if not lay.sliding] == [4, 9, 14, 19, 24, 29, 34]
+    assert all(lay.kv_layer == l for l, lay in enumerate(L[:15]))
+    assert all(lay.kv_layer == (13 if lay.sliding else 14) for lay in L[15:])
+    assert {lay.ffn_dim for lay in L[:15]} == {6144} and {lay.ffn_dim for lay in L[15:]} == {12288}
+    assert {(lay.head_dim, lay.rope_pairs, lay.rope_theta) for lay in L} == {(256, 128, 1e4), (512, 64, 1e6)}
+    invf = g4.G4_E2B.inv_freq(4)
+    assert np.count_nonzero(invf) == 64 and invf[63] == np.float32(1e6 ** (-126 / 512))
+
+
+def test_gemma4_softcap_keeps_the_argmax(rng):
+    from oracle import gemma4 as g4
+
+    d = g4.G4Decoder(g4.G4_TINY, g4.make_weights(g4.G4_TINY, 1), 8)
+    x = (rng.standard_normal(1000) * 40).astype(np.float32)
+    c = d.softcap(x)
+    assert np.argmax(c) == np.argmax(x) and np.abs(c).max() < 30
+    assert np.allclose(c, 30 * np.tanh(x.astype(np.float64) / 30), rtol=1e-6)
