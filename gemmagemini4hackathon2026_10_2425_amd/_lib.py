@@ -64,11 +64,31 @@ class ModelConfig(ctypes.Structure):
     ]
 
 
+class Gemma4Layer(ctypes.Structure):
+    """mxd_gemma4_layer (include/mxdecode.h)."""
+
+    _fields_ = [
+        ("head_dim", c_int), ("ffn_dim", c_int), ("sliding", c_int), ("kv_layer", c_int), ("rope_pairs", c_int),
+        ("rope_theta", c_float), ("layer_scalar", c_float),
+    ]
+
+
+class Gemma4Config(ctypes.Structure):
+    """mxd_gemma4_config (include/mxdecode.h)."""
+
+    _fields_ = [
+        ("n_layers", c_int), ("dim", c_int), ("n_heads", c_int), ("n_kv_heads", c_int), ("vocab", c_int),
+        ("ple_dim", c_int), ("ple_vocab", c_int), ("window", c_int), ("rms_eps", c_float), ("softcap", c_float),
+        ("layers", ctypes.POINTER(Gemma4Layer)),
+    ]
+
+
 P = c_void_p
 E = c_void_p  # mxd_engine*
 # name -> (restype, argtypes); must match include/mxdecode.h one for one.
 SIGNATURES: dict[str, tuple] = {
     "mxd_engine_create": (c_int, [ctypes.POINTER(ModelConfig), c_int, ctypes.POINTER(c_void_p)]),
+    "mxd_engine_create_gemma4": (c_int, [ctypes.POINTER(Gemma4Config), c_int, ctypes.POINTER(c_void_p)]),
     "mxd_engine_destroy": (c_int, [E]),
     "mxd_engine_num_tensors": (c_int, [E]),
     "mxd_engine_tensor": (c_int, [E, c_int, ctypes.POINTER(c_char_p), ctypes.POINTER(c_void_p),
@@ -110,6 +130,14 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_attention_noalloc": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, P]),
     "mxd_attention_split": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, c_int, P, c_size_t, P]),
     "mxd_attention_prefill": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P]),
+    "mxd_attention_window": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_int, c_float, P, c_size_t,
+                                     P]),
+    "mxd_attention_prefill_window": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int,
+                                             c_int, c_float, P]),
+    "mxd_rmsnorm_add": (c_int, [P, P, P, c_int, c_int, c_float, c_float, P]),
+    "mxd_ple_combine": (c_int, [P, P, P, c_int, c_int, c_int, c_float, c_float, P]),
+    "mxd_qk_norm_rope_kv": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_int, P,
+                                    P]),
     "mxd_argmax_workspace_size": (c_size_t, [c_int]),
     "mxd_argmax": (c_int, [P, P, c_int, c_int, P, c_size_t, P]),
     "mxd_rope_kv_paged": (c_int, [P, P, P, c_int, P, c_int, c_int, c_int, P, c_int, P, c_int, P]),

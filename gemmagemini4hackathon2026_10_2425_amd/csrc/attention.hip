@@ -52,13 +52,15 @@
 
 namespace {
 
-// Split `split` of S over the kv head's n keys: partials at split-major rows
-// [split][n_heads] of ws_o / ws_ml, or the output directly when one split is
-// active. An empty sequence writes a zero output.
+// Split `split` of S over the kv head's n keys (the last a.window of them
+// under a sliding window): partials at split-major rows [split][n_heads] of
+// ws_o / ws_ml, or the output directly when one split is active. An empty
+// sequence writes a zero output.
 template <int HD, int W, bool PF, typename KV>
 __device__ __forceinline__ void attn_split(const AttnArgs& a, const KV& src, int n, int S, int split, int kvh,
                                            const float* qrow, float* orow, float* ws_o, float* ws_ml) {
     const int nblocks = (n + BLK - 1) / BLK;
+    const int lo = window_lo(a, n), blo = lo / BLK;
     const size_t g0 = (size_t)kvh * a.G;
     if (nblocks == 0) {
         if (split == 0 && a.partials_only) {  // a zero output as a partial: O = 0, (max, sum) = (0, 1)
@@ -72,11 +74,11 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a, const KV& src, int
         }
         return;
     }
-    const int n_active = min(S, nblocks);
+    const int n_active = min(S, nblocks - blo);
     if (split >= n_active) return;  // an empty split
     const size_t prow = (size_t)split * a.n_heads + g0;
     const CoreOut out{orow + g0 * HD, ws_o + prow * HD, ws_ml + prow * 2, n_active == 1 && !a.partials_only};
-    attn_core<HD, W, PF>(a, src, n, split, S, nblocks, qrow + g0 * HD, out);
+    attn_core<HD, W, PF>(a, src, n, blo + split, S, nblocks, qrow + g0 * HD, out, 0, lo);
 }
 
 template <int HD, int W, bool PF>
@@ -84,7 +86,7 @@ __global__ void __launch_bounds__(W * 64) attn_split_kernel(AttnArgs a) {
     const int kvh = blockIdx.y;
     const ContigKV<HD> src{a.k + (size_t)kvh * a.max_ctx * HD, a.v + (size_t)kvh * a.max_ctx * HD};
     const int n = n_keys_of(a);
-    attn_split<HD, W, PF>(a, src, n, active_splits(a, (n + BLK - 1) / BLK), blockIdx.x, kvh, a.q, a.out, a.ws_o,
+    attn_split<HD, W, PF>(a, src, n, active_splits(a, attended_blocks(a, n)), blockIdx.x, kvh, a.q, a.out, a.ws_o,
                           a.ws_ml);
 }
 
@@ -361,7 +363,7 @@ __device__ __forceinline__ void attn_merge_core(const AttnArgs& a, int n_active,
 // of head x / (HD/MG_D).
 template <int HD>
 __global__ void __launch_bounds__(MG_T) attn_merge_kernel(AttnArgs a) {
-    const int nblocks = (n_keys_of(a) + BLK - 1) / BLK;
+    const int nblocks = attended_blocks(a, n_keys_of(a));
     const int n_active = min(active_splits(a, nblocks), nblocks);
     constexpr int NCH = HD / MG_D;
     attn_merge_core<HD>(a, n_active, blockIdx.x / NCH, blockIdx.x % NCH, a.out, a.ws_o, a.ws_ml);
@@ -386,11 +388,18 @@ __global__ void __launch_bounds__(MG_T) attn_paged_merge_kernel(AttnArgs a) {
 int att_waves() { return mxd::tunable("ATT_W", ATT_WAVES) == 8 ? 8 : 4; }
 bool att_prefetch(int hd) { (void)hd; return mxd::tunable("ATT_PF", 2) == 1; }
 
+// Waves per workgroup at head_dim hd: head_dim 512 always takes 4 (its
+// per-wave O rows fill 129 KiB of LDS at 4 waves).
+int waves_for(int hd) { return hd >= 512 ? 4 : att_waves(); }
+
 template <int HD>
 void launch_split(const dim3& grid, hipStream_t s, const AttnArgs& a) {
-    const int w = att_waves();
+    const int w = waves_for(HD);
     const bool pf = att_prefetch(HD);
-    if (w == 8) {
+    if constexpr (HD >= 512) {
+        if (pf) hipLaunchKernelGGL((attn_split_kernel<HD, 4, true>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((attn_split_kernel<HD, 4, false>), grid, dim3(256), 0, s, a);
+    } else if (w == 8) {
         if (pf) hipLaunchKernelGGL((attn_split_kernel<HD, 8, true>), grid, dim3(512), 0, s, a);
         else hipLaunchKernelGGL((attn_split_kernel<HD, 8, false>), grid, dim3(512), 0, s, a);
     } else {
@@ -438,23 +447,35 @@ int target_splits(int n_kv) {
 // it saves). Longer contexts take enough splits that every wave has at most
 // one block, capped by the occupancy target. active_splits is the same rule
 // on the device.
-int single_blocks() { return mxd::tunable("ATT_SINGLE", 4 * att_waves()); }
-int splits_for(int max_keys, int n_kv) {
+int single_blocks(int hd) { return mxd::tunable("ATT_SINGLE", 4 * waves_for(hd)); }
+int splits_for(int max_keys, int n_kv, int hd) {
     const int nblocks = (max_keys + BLK - 1) / BLK;
-    const int w = att_waves();
-    if (nblocks <= single_blocks()) return 1;
+    const int w = waves_for(hd);
+    if (nblocks <= single_blocks(hd)) return 1;
     const int one_per_wave = (nblocks + w - 1) / w;
     return max(1, min(one_per_wave, target_splits(n_kv)));
 }
 
+// Blocks a query attends to at most: a sliding window of `window` keys starts
+// anywhere inside a block, so it spans up to (window + 31) / 32 + 1 of them.
+int max_keys_attended(int max_keys, int window) {
+    return window > 0 ? min(max_keys, window + BLK) : max_keys;
+}
+
 // Calls f with std::integral_constant<int, HD> for the supported head dims
-// (64: Llama-3.2-1B; 128: Llama-3-8B; 256: Gemma-2B); the callers have
+// (64: Llama-3.2-1B; 128: Llama-3-8B; 256: Gemma-2B and Gemma-4's sliding
+// layers; with WIDE also 512: Gemma-4's full layers); the callers have
 // checked head_dim.
-template <typename F>
+template <bool WIDE = false, typename F>
 void with_head_dim(int head_dim, F&& f) {
     if (head_dim == 64) f(std::integral_constant<int, 64>{});
     else if (head_dim == 128) f(std::integral_constant<int, 128>{});
-    else f(std::integral_constant<int, 256>{});
+    else if constexpr (WIDE) {
+        if (head_dim == 512) f(std::integral_constant<int, 512>{});
+        else f(std::integral_constant<int, 256>{});
+    } else {
+        f(std::integral_constant<int, 256>{});
+    }
 }
 
 }  // namespace
@@ -466,31 +487,35 @@ extern "C" size_t mxd_attention_workspace_size(int n_heads, int n_kv_heads, int 
     return splits * n_heads * (head_dim + 2) * sizeof(float);
 }
 
-extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint16_t* vcache, float* out, int n_heads,
-                             int n_kv_heads, int head_dim, int max_ctx, int n_keys, const int32_t* pos_dev,
-                             float scale, void* workspace, size_t ws_bytes, mxd_stream_t stream) {
-    MXD_REQUIRE(q && kcache && vcache && out, MXD_ERR_INVALID_ARG, "mxd_attention: null pointer");
+namespace {
+
+// mxd_attention / mxd_attention_window.
+int attention_impl(const char* name, const float* q, const uint16_t* kcache, const uint16_t* vcache, float* out,
+                   int n_heads, int n_kv_heads, int head_dim, int max_ctx, int n_keys, const int32_t* pos_dev,
+                   int window, float scale, void* workspace, size_t ws_bytes, mxd_stream_t stream) {
+    MXD_REQUIRE(q && kcache && vcache && out, MXD_ERR_INVALID_ARG, "%s: null pointer", name);
     MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, MXD_ERR_INVALID_ARG,
-                "mxd_attention: n_heads=%d must be a positive multiple of n_kv_heads=%d", n_heads, n_kv_heads);
+                "%s: n_heads=%d must be a positive multiple of n_kv_heads=%d", name, n_heads, n_kv_heads);
     const int G = n_heads / n_kv_heads;
     MXD_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, MXD_ERR_UNSUPPORTED,
-                "mxd_attention: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", G);
-    MXD_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED, "mxd_attention: head_dim %d (64, 128 or 256)",
-                head_dim);
+                "%s: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", name, G);
+    MXD_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512, MXD_ERR_UNSUPPORTED,
+                "%s: head_dim %d (64, 128, 256 or 512)", name, head_dim);
     MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED,
-                "mxd_attention: max_ctx=%d must be a positive multiple of 32", max_ctx);
+                "%s: max_ctx=%d must be a positive multiple of 32", name, max_ctx);
     MXD_REQUIRE(pos_dev || (n_keys >= 1 && n_keys <= max_ctx), MXD_ERR_INVALID_ARG,
-                "mxd_attention: n_keys=%d outside [1, max_ctx=%d]", n_keys, max_ctx);
+                "%s: n_keys=%d outside [1, max_ctx=%d]", name, n_keys, max_ctx);
+    MXD_REQUIRE(window >= 0, MXD_ERR_INVALID_ARG, "%s: window=%d", name, window);
     const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kcache) |
                          reinterpret_cast<uintptr_t>(vcache);
-    MXD_REQUIRE((al & 15) == 0, MXD_ERR_UNSUPPORTED, "mxd_attention: q, kcache, vcache must be 16-byte aligned");
+    MXD_REQUIRE((al & 15) == 0, MXD_ERR_UNSUPPORTED, "%s: q, kcache, vcache must be 16-byte aligned", name);
 
-    const int n_splits = splits_for(pos_dev ? max_ctx : n_keys, n_kv_heads);
+    const int n_splits = splits_for(max_keys_attended(pos_dev ? max_ctx : n_keys, window), n_kv_heads, head_dim);
     const size_t need = (size_t)n_splits * n_heads * (head_dim + 2) * sizeof(float);
     MXD_REQUIRE(n_splits == 1 || (workspace && ws_bytes >= need), MXD_ERR_WORKSPACE,
-                "mxd_attention: workspace of %zu bytes needed (got %zu)", need, ws_bytes);
+                "%s: workspace of %zu bytes needed (got %zu)", name, need, ws_bytes);
     MXD_REQUIRE(!workspace || (reinterpret_cast<uintptr_t>(workspace) & 15) == 0, MXD_ERR_UNSUPPORTED,
-                "mxd_attention: workspace must be 16-byte aligned");
+                "%s: workspace must be 16-byte aligned", name);
 
     AttnArgs a;
     a.q = q;
@@ -509,17 +534,35 @@ extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint1
     a.n_splits = n_splits;
     a.qscale = scale * LOG2E;
     a.auto_splits = true;
-    a.single_blocks = single_blocks();
-    a.waves = att_waves();
+    a.single_blocks = single_blocks(head_dim);
+    a.waves = waves_for(head_dim);
+    a.window = window;
 
     hipStream_t s = mxd::as_stream(stream);
     const dim3 grid(n_splits, n_kv_heads);
-    with_head_dim(head_dim, [&](auto hd) {
+    with_head_dim<true>(head_dim, [&](auto hd) {
         constexpr int HD = decltype(hd)::value;
         launch_split<HD>(grid, s, a);
         if (n_splits > 1) hipLaunchKernelGGL(attn_merge_kernel<HD>, dim3(n_heads * HD / MG_D), dim3(MG_T), 0, s, a);
     });
-    return mxd::check_launch("mxd_attention");
+    return mxd::check_launch(name);
+}
+
+}  // namespace
+
+extern "C" int mxd_attention(const float* q, const uint16_t* kcache, const uint16_t* vcache, float* out, int n_heads,
+                             int n_kv_heads, int head_dim, int max_ctx, int n_keys, const int32_t* pos_dev,
+                             float scale, void* workspace, size_t ws_bytes, mxd_stream_t stream) {
+    return attention_impl("mxd_attention", q, kcache, vcache, out, n_heads, n_kv_heads, head_dim, max_ctx, n_keys,
+                          pos_dev, 0, scale, workspace, ws_bytes, stream);
+}
+
+extern "C" int mxd_attention_window(const float* q, const uint16_t* kcache, const uint16_t* vcache, float* out,
+                                    int n_heads, int n_kv_heads, int head_dim, int max_ctx, int n_keys,
+                                    const int32_t* pos_dev, int window, float scale, void* workspace,
+                                    size_t ws_bytes, mxd_stream_t stream) {
+    return attention_impl("mxd_attention_window", q, kcache, vcache, out, n_heads, n_kv_heads, head_dim, max_ctx,
+                          n_keys, pos_dev, window, scale, workspace, ws_bytes, stream);
 }
 
 extern "C" int mxd_attention_split(const float* q, const uint16_t* kcache, const uint16_t* vcache, int n_heads,
@@ -625,27 +668,31 @@ size_t sk_workspace(int nw, int n_seqs, int n_heads, int n_kv, int hd) {
 }
 }  // namespace
 
-extern "C" int mxd_attention_prefill(const float* q, int q_stride, const uint16_t* kcache, const uint16_t* vcache,
-                                     float* out, int out_stride, int n_heads, int n_kv_heads, int head_dim,
-                                     int max_ctx, int pos0, int rows, float scale, mxd_stream_t stream) {
-    MXD_REQUIRE(q && kcache && vcache && out, MXD_ERR_INVALID_ARG, "mxd_attention_prefill: null pointer");
+namespace {
+
+int attention_prefill_impl(const char* name, const float* q, int q_stride, const uint16_t* kcache,
+                           const uint16_t* vcache, float* out, int out_stride, int n_heads, int n_kv_heads,
+                           int head_dim, int max_ctx, int pos0, int rows, int window, float scale,
+                           mxd_stream_t stream) {
+    MXD_REQUIRE(q && kcache && vcache && out, MXD_ERR_INVALID_ARG, "%s: null pointer", name);
     MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, MXD_ERR_INVALID_ARG,
-                "mxd_attention_prefill: n_heads=%d must be a positive multiple of n_kv_heads=%d", n_heads, n_kv_heads);
+                "%s: n_heads=%d must be a positive multiple of n_kv_heads=%d", name, n_heads, n_kv_heads);
     const int G = n_heads / n_kv_heads;
     MXD_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, MXD_ERR_UNSUPPORTED,
-                "mxd_attention_prefill: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", G);
-    MXD_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED,
-                "mxd_attention_prefill: head_dim %d (64, 128 or 256)", head_dim);
+                "%s: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", name, G);
+    MXD_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512, MXD_ERR_UNSUPPORTED,
+                "%s: head_dim %d (64, 128, 256 or 512)", name, head_dim);
     MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED,
-                "mxd_attention_prefill: max_ctx=%d must be a positive multiple of 32", max_ctx);
+                "%s: max_ctx=%d must be a positive multiple of 32", name, max_ctx);
     MXD_REQUIRE(rows >= 1 && pos0 >= 0 && (long long)pos0 + rows <= max_ctx, MXD_ERR_INVALID_ARG,
-                "mxd_attention_prefill: positions [%d, %d + %d) outside [0, max_ctx=%d)", pos0, pos0, rows, max_ctx);
+                "%s: positions [%d, %d + %d) outside [0, max_ctx=%d)", name, pos0, pos0, rows, max_ctx);
     MXD_REQUIRE(q_stride >= n_heads * head_dim && out_stride >= n_heads * head_dim && q_stride % 4 == 0,
-                MXD_ERR_INVALID_ARG, "mxd_attention_prefill: q_stride=%d out_stride=%d below n_heads * head_dim = %d "
-                "(q_stride a multiple of 4)", q_stride, out_stride, n_heads * head_dim);
+                MXD_ERR_INVALID_ARG, "%s: q_stride=%d out_stride=%d below n_heads * head_dim = %d "
+                "(q_stride a multiple of 4)", name, q_stride, out_stride, n_heads * head_dim);
+    MXD_REQUIRE(window >= 0, MXD_ERR_INVALID_ARG, "%s: window=%d", name, window);
     const uintptr_t al = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kcache) |
                          reinterpret_cast<uintptr_t>(vcache);
-    MXD_REQUIRE((al & 15) == 0, MXD_ERR_UNSUPPORTED, "mxd_attention_prefill: q, kcache, vcache must be 16-byte aligned");
+    MXD_REQUIRE((al & 15) == 0, MXD_ERR_UNSUPPORTED, "%s: q, kcache, vcache must be 16-byte aligned", name);
     AttnArgs a;
     a.q = q;
     a.k = kcache;
@@ -663,13 +710,31 @@ extern "C" int mxd_attention_prefill(const float* q, int q_stride, const uint16_
     a.n_keys = pos0 + 1;
     a.n_splits = 1;
     a.qscale = scale * LOG2E;
+    a.window = window;
     hipStream_t s = mxd::as_stream(stream);
     const dim3 grid(rows, n_kv_heads);
-    with_head_dim(head_dim, [&](auto hd) {
+    with_head_dim<true>(head_dim, [&](auto hd) {
         hipLaunchKernelGGL((attn_prefill_kernel<decltype(hd)::value, ATT_WAVES, false>), grid, dim3(ATT_WAVES * 64), 0,
                            s, a);
     });
-    return mxd::check_launch("mxd_attention_prefill");
+    return mxd::check_launch(name);
+}
+
+}  // namespace
+
+extern "C" int mxd_attention_prefill(const float* q, int q_stride, const uint16_t* kcache, const uint16_t* vcache,
+                                     float* out, int out_stride, int n_heads, int n_kv_heads, int head_dim,
+                                     int max_ctx, int pos0, int rows, float scale, mxd_stream_t stream) {
+    return attention_prefill_impl("mxd_attention_prefill", q, q_stride, kcache, vcache, out, out_stride, n_heads,
+                                  n_kv_heads, head_dim, max_ctx, pos0, rows, 0, scale, stream);
+}
+
+extern "C" int mxd_attention_prefill_window(const float* q, int q_stride, const uint16_t* kcache,
+                                            const uint16_t* vcache, float* out, int out_stride, int n_heads,
+                                            int n_kv_heads, int head_dim, int max_ctx, int pos0, int rows,
+                                            int window, float scale, mxd_stream_t stream) {
+    return attention_prefill_impl("mxd_attention_prefill_window", q, q_stride, kcache, vcache, out, out_stride,
+                                  n_heads, n_kv_heads, head_dim, max_ctx, pos0, rows, window, scale, stream);
 }
 
 extern "C" size_t mxd_attention_paged_workspace_size(int n_heads, int n_kv_heads, int head_dim, int n_seqs,
@@ -812,7 +877,7 @@ extern "C" int mxd_attention_noalloc(const float* q, const uint16_t* kcache, con
     MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && max_ctx > 0, MXD_ERR_INVALID_ARG,
                 "mxd_attention_noalloc: n_heads=%d n_kv_heads=%d head_dim=%d max_ctx=%d", n_heads, n_kv_heads,
                 head_dim, max_ctx);
-    const int splits = splits_for(n_keys_dev ? max_ctx : max(n_keys, 1), n_kv_heads);
+    const int splits = splits_for(n_keys_dev ? max_ctx : max(n_keys, 1), n_kv_heads, head_dim);
     const size_t need = (size_t)splits * n_heads * (head_dim + 2) * sizeof(float);
     MXD_REQUIRE(need <= NOALLOC_SCRATCH_BYTES, MXD_ERR_UNSUPPORTED,
                 "mxd_attention_noalloc: this shape needs %zu bytes of split partials, above the %zu-byte scratch",

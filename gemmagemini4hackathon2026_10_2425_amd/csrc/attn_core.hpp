@@ -46,6 +46,9 @@ struct AttnArgs {
     bool auto_splits = false;
     int single_blocks = 0;  // contexts of up to this many blocks take one split
     int waves = 4;
+    // Sliding window (contiguous cache): a query with n visible keys attends to
+    // keys [max(0, n - window), n); 0 = all n.
+    int window = 0;
     // Tagged mode (the fused decode attention block): the q rows ([n_heads][HD])
     // and the new key / value rows of position patch_pos ([n_kv][HD], fp32
     // before their fp16 rounding) arrive as tagged words of `tag`; the block of
@@ -64,6 +67,14 @@ struct AttnArgs {
 __device__ __forceinline__ int n_keys_of(const AttnArgs& a) {
     const int n = a.pos_dev ? a.pos_dev[0] + 1 : a.n_keys;
     return max(0, min(n, a.max_ctx));
+}
+
+// First key a query with n visible keys attends to.
+__device__ __forceinline__ int window_lo(const AttnArgs& a, int n) { return a.window > 0 ? max(0, n - a.window) : 0; }
+
+// 32-key blocks holding the keys [window_lo, n).
+__device__ __forceinline__ int attended_blocks(const AttnArgs& a, int n) {
+    return (n + BLK - 1) / BLK - window_lo(a, n) / BLK;
 }
 
 // Splits of a context of nblocks 32-key blocks under auto_splits: one up to
@@ -238,10 +249,11 @@ __device__ __forceinline__ void stage_tagged(const AttnArgs& a, int kvh, float* 
 // One kv head of one sequence with n keys, over the 32-key blocks first,
 // first + S, first + 2S, ... below bend, dealt round-robin to the W waves
 // (wave w takes first + S*w, then steps by S*W). qg points at the q rows of
-// the kv head's G query heads. The range must hold at least one block.
+// the kv head's G query heads. The range must hold at least one block. Keys
+// below lo (a sliding window's start) are masked like keys past n.
 template <int HD, int W, bool PREFETCH, typename KV, bool TAGGED = false>
 __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int n, int first, int S, int bend,
-                                          const float* qg, const CoreOut& out, int kvh = 0) {
+                                          const float* qg, const CoreOut& out, int kvh = 0, int lo = 0) {
     constexpr int NC = HD / 32;  // MFMA k-chunks over head_dim for Q.K
     constexpr int ND = HD / 16;  // 16-wide dim tiles for P.V
     constexpr int NT = W * 64;
@@ -336,13 +348,14 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
 #pragma unroll
             for (int i = 0; i < 4; ++i) s[4 * t + i] = acc[i];
         }
-        const bool tail = key0 + BLK > n;
-        const int nvalid = n - key0;  // keys of this block inside [0, n)
+        const bool tail = key0 + BLK > n || key0 < lo;
+        const int nvalid = n - key0;  // keys of this block inside [lo, n) are
+        const int nskip = lo - key0;  // the slots in [nskip, nvalid)
         float mb = -INFINITY;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             s[j] += mxd::dpp_f32<0x128>(s[j]);  // row_ror:8 = column h + 8: hi + lo
-            if (tail) s[j] = KV::key(g, j) < nvalid ? s[j] : -INFINITY;
+            if (tail) s[j] = KV::key(g, j) < nvalid && KV::key(g, j) >= nskip ? s[j] : -INFINITY;
             mb = fmaxf(mb, s[j]);
         }
         mb = fmaxf(mb, __shfl_xor(mb, 16));
@@ -377,9 +390,11 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
         if (tail) {
             u4_t keep;
 #pragma unroll
-            for (int w = 0; w < 4; ++w)
-                keep[w] = (KV::key(g, 2 * w) < nvalid ? 0x0000FFFFu : 0u) |
-                          (KV::key(g, 2 * w + 1) < nvalid ? 0xFFFF0000u : 0u);
+            for (int w = 0; w < 4; ++w) {
+                const int k0 = KV::key(g, 2 * w), k1 = KV::key(g, 2 * w + 1);
+                keep[w] = (k0 < nvalid && k0 >= nskip ? 0x0000FFFFu : 0u) |
+                          (k1 < nvalid && k1 >= nskip ? 0xFFFF0000u : 0u);
+            }
 #pragma unroll
             for (int d = 0; d < ND; ++d) {
                 u4_t v;

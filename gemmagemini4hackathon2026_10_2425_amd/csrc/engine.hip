@@ -22,110 +22,17 @@
 // the last chunk goes through the decode path's LM head and argmax. The
 // ENG_NO_GEMM tunable (the reference's --no-gemm) steps the decode path
 // instead.
-#include "internal.hpp"
+#include "engine.hpp"
 
 #include <math.h>
 #include <stdio.h>
 #include <string.h>
 
-#include <string>
-#include <unordered_map>
-#include <vector>
+using namespace mxd_eng;
 
 namespace {
-
-struct TensorInfo {
-    std::string name;
-    size_t offset, bytes;
-    int dtype;  // MXD_F16 / MXD_F32
-    uint64_t id;
-};
-
-struct LayerPtrs {
-    float *attn_norm, *ffn_norm;
-    uint16_t *wqkv, *wo, *wgate, *wup, *wdown;
-    uint16_t *kc, *vc;
-};
-
-size_t align256(size_t n) { return (n + 255) / 256 * 256; }
-
-constexpr int PREFILL_ROWS = 256;  // prompt rows per prefill chunk
-
-#define HIP_OK(expr, what)                                                                         \
-    do {                                                                                           \
-        hipError_t e_ = (expr);                                                                    \
-        if (e_ != hipSuccess) return mxd::fail(MXD_ERR_HIP, "%s: %s", what, hipGetErrorString(e_)); \
-    } while (0)
 
 __global__ void set_int_kernel(int32_t* p, int v) { *p = v; }
-
-}  // namespace
-
-struct mxd_engine {
-    mxd_model_config c{};
-    int max_ctx = 0;
-    hipStream_t stream = nullptr;
-    std::vector<TensorInfo> tensors;
-    std::unordered_map<std::string, int> index;
-    char* wbase = nullptr;
-    size_t wbytes = 0;
-    char* abase = nullptr;
-    size_t abytes = 0;
-    std::vector<LayerPtrs> L;
-    uint16_t* embed = nullptr;
-    uint16_t* head = nullptr;  // the LM head: embed (tied) or lm_head
-    float* final_norm = nullptr;
-    float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *h = nullptr, *logits = nullptr;
-    float* invf = nullptr;
-    int32_t *tokens = nullptr, *pos = nullptr;
-    void* attn_ws = nullptr;
-    size_t attn_ws_bytes = 0;
-    // Splits of the decode attention when its merge is folded into the o
-    // projection (one 32-key block per wave at max_ctx); 0 = the separate
-    // attention with its own merge.
-    int att_splits = 0;
-    void* am_ws = nullptr;
-    hipGraphExec_t graph = nullptr;
-    // Streaming decode: the captured step's argmax also writes each token to
-    // pinned host memory (htokens, its device view htokens_dev), and every
-    // replayed step records an event in a ring indexed by its position, so a
-    // caller waits for one step without draining the ones queued after it.
-    int32_t* htokens = nullptr;
-    int32_t* htokens_dev = nullptr;
-    static constexpr int RING = 16;
-    hipEvent_t step_done[RING] = {};
-    // The position the last decode run left in the device counter (-1: not
-    // known), so a run that continues from it needs no counter write.
-    int pos_next = -1;
-    // The fused attention half of each layer (attn_block): its workspace of
-    // tagged words, the step counter its tags come from (advanced by the
-    // embedding kernel of every step) and its error word.
-    bool fused = false;
-    void* ab_ws = nullptr;
-    size_t ab_ws_bytes = 0;
-    int32_t* step = nullptr;
-    int* ab_err = nullptr;
-    // prefill chunk buffers: rows x {dim f32, dim f16, qkv f32, q f32, ffn f32}
-    // (the products round fp32 rows to fp16 as they load them), and the
-    // products' split-K workspace
-    int max_rows = 0;
-    float *bx = nullptr, *bqkv = nullptr, *batt = nullptr, *bh = nullptr;
-    uint16_t* bxn = nullptr;
-    void* gm_ws = nullptr;
-    size_t gm_ws_bytes = 0;
-
-    int qkv_dim() const { return (c.n_heads + 2 * c.n_kv_heads) * c.head_dim; }
-    int q_dim() const { return c.n_heads * c.head_dim; }
-};
-
-namespace {
-
-void add_tensor(mxd_engine* e, const std::string& name, size_t elems, int dtype, uint64_t id, size_t& off) {
-    const size_t bytes = elems * (dtype == MXD_F32 ? 4 : 2);
-    e->index[name] = (int)e->tensors.size();
-    e->tensors.push_back({name, off, bytes, dtype, id});
-    off += align256(bytes);
-}
 
 // Tensor ids of the synthetic-weight generator: embed 1, final_norm 2,
 // lm_head 3 (untied heads only), and 1000 + 16 * layer + {attn_norm 0, wqkv 1,
@@ -152,27 +59,11 @@ void plan_weights(mxd_engine* e) {
     e->wbytes = off;
 }
 
-template <typename T>
-T* wptr(mxd_engine* e, const std::string& name) {
-    return reinterpret_cast<T*>(e->wbase + e->tensors[e->index.at(name)].offset);
-}
-
-void destroy(mxd_engine* e) {
-    if (!e) return;
-    if (e->graph) hipGraphExecDestroy(e->graph);
-    for (hipEvent_t& ev : e->step_done)
-        if (ev) hipEventDestroy(ev);
-    if (e->htokens) hipHostFree(e->htokens);
-    if (e->wbase) hipFree(e->wbase);
-    if (e->abase) hipFree(e->abase);
-    if (e->stream) hipStreamDestroy(e->stream);
-    delete e;
-}
-
 // One decode step: reads tokens[pos], appends K/V at pos, and with `sample`
 // writes argmax(logits) to tokens[pos + 1]. With pos_dev the position is read
 // on the device and advanced by the argmax (the captured form).
 int encode_step(mxd_engine* e, int pos, int32_t* pos_dev, bool sample) {
+    if (e->arch == ENG_GEMMA4) return g4_step(e, pos, pos_dev, sample);
     const mxd_model_config& c = e->c;
     hipStream_t s = e->stream;
     mxd_stream_t ms = reinterpret_cast<mxd_stream_t>(s);
@@ -320,6 +211,32 @@ int check_config(const mxd_model_config* c, int max_ctx) {
 
 }  // namespace
 
+int mxd_eng::allocate(mxd_engine* e) {
+    hipError_t he;
+    if ((he = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking)) != hipSuccess ||
+        (he = hipMalloc(&e->wbase, e->wbytes)) != hipSuccess || (he = hipMalloc(&e->abase, e->abytes)) != hipSuccess ||
+        (he = hipHostMalloc(reinterpret_cast<void**>(&e->htokens), ((size_t)e->max_ctx + 1) * 4,
+                            hipHostMallocMapped | hipHostMallocCoherent)) != hipSuccess ||
+        (he = hipHostGetDevicePointer(reinterpret_cast<void**>(&e->htokens_dev), e->htokens, 0)) != hipSuccess) {
+        const size_t wb = e->wbytes, ab = e->abytes;
+        destroy(e);
+        return mxd::fail(MXD_ERR_ALLOC, "mxd_engine_create: %s (weights %zu B, buffers %zu B)", hipGetErrorString(he),
+                         wb, ab);
+    }
+    for (hipEvent_t& ev : e->step_done) {
+        if ((he = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) {
+            destroy(e);
+            return mxd::fail(MXD_ERR_HIP, "mxd_engine_create: %s", hipGetErrorString(he));
+        }
+    }
+    // Zero every buffer once (caches, token buffer, argmax workspace), off any graph.
+    if ((he = hipMemsetAsync(e->abase, 0, e->abytes, e->stream)) != hipSuccess) {
+        destroy(e);
+        return mxd::fail(MXD_ERR_HIP, "mxd_engine_create: %s", hipGetErrorString(he));
+    }
+    return MXD_OK;
+}
+
 extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_engine** out) {
     MXD_REQUIRE(out, MXD_ERR_INVALID_ARG, "mxd_engine_create: null out");
     *out = nullptr;
@@ -374,23 +291,7 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
     }
     e->abytes = off;
 
-    hipError_t he;
-    if ((he = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking)) != hipSuccess ||
-        (he = hipMalloc(&e->wbase, e->wbytes)) != hipSuccess || (he = hipMalloc(&e->abase, e->abytes)) != hipSuccess ||
-        (he = hipHostMalloc(reinterpret_cast<void**>(&e->htokens), ((size_t)max_ctx + 1) * 4,
-                                hipHostMallocMapped | hipHostMallocCoherent)) !=
-            hipSuccess ||
-        (he = hipHostGetDevicePointer(reinterpret_cast<void**>(&e->htokens_dev), e->htokens, 0)) != hipSuccess) {
-        destroy(e);
-        return mxd::fail(MXD_ERR_ALLOC, "mxd_engine_create: %s (weights %zu B, buffers %zu B)", hipGetErrorString(he),
-                         e->wbytes, off);
-    }
-    for (hipEvent_t& ev : e->step_done) {
-        if ((he = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess) {
-            destroy(e);
-            return mxd::fail(MXD_ERR_HIP, "mxd_engine_create: %s", hipGetErrorString(he));
-        }
-    }
+    if (int rc = allocate(e)) return rc;
     char* a = e->abase;
     e->x = reinterpret_cast<float*>(a + o_x);
     e->xn = reinterpret_cast<float*>(a + o_xn);
@@ -431,16 +332,11 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
         Lp.kc = reinterpret_cast<uint16_t*>(a + o_kc[l]);
         Lp.vc = reinterpret_cast<uint16_t*>(a + o_vc[l]);
     }
-    // Zero everything once (caches, token buffer, argmax workspace), off any graph.
-    if ((he = hipMemsetAsync(e->abase, 0, e->abytes, e->stream)) != hipSuccess) {
-        destroy(e);
-        return mxd::fail(MXD_ERR_HIP, "mxd_engine_create: %s", hipGetErrorString(he));
-    }
     // RoPE inverse frequencies in double, stored as float (KL/main.swift:92-94),
     // with the Llama-3 band scaling when configured (KL/main.swift:96-107).
     std::vector<float> invf(c.head_dim / 2);
     for (int i = 0; i < c.head_dim / 2; ++i) invf[i] = (float)rope_inv_freq(c, i);
-    he = hipMemcpyAsync(e->invf, invf.data(), invf.size() * 4, hipMemcpyHostToDevice, e->stream);
+    hipError_t he = hipMemcpyAsync(e->invf, invf.data(), invf.size() * 4, hipMemcpyHostToDevice, e->stream);
     if (he == hipSuccess) he = hipStreamSynchronize(e->stream);
     if (he != hipSuccess) {
         destroy(e);
@@ -452,7 +348,7 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
 
 extern "C" int mxd_engine_destroy(mxd_engine* e) {
     if (e) {
-        hipStreamSynchronize(e->stream);
+        (void)hipStreamSynchronize(e->stream);
         destroy(e);
     }
     return MXD_OK;
@@ -482,8 +378,7 @@ extern "C" int mxd_engine_init_random(mxd_engine* e, uint64_t seed, float stddev
     MXD_REQUIRE(e, MXD_ERR_INVALID_ARG, "mxd_engine_init_random: null engine");
     for (const TensorInfo& t : e->tensors) {
         const uint64_t n = t.bytes / (t.dtype == MXD_F32 ? 4 : 2);
-        if (int rc = mxd_fill_normal(e->wbase + t.offset, t.dtype, n, seed, t.id, stddev,
-                                     reinterpret_cast<mxd_stream_t>(e->stream)))
+        if (int rc = mxd::fill_normal_dev(e->wbase + t.offset, t.dtype, n, seed, t.id, stddev, t.shift, e->stream))
             return rc;
     }
     HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_init_random");
@@ -495,8 +390,7 @@ extern "C" int mxd_engine_fill_tensor(mxd_engine* e, int i, uint64_t seed, float
                 i);
     const TensorInfo& t = e->tensors[i];
     const uint64_t n = t.bytes / (t.dtype == MXD_F32 ? 4 : 2);
-    if (int rc = mxd_fill_normal(e->wbase + t.offset, t.dtype, n, seed, t.id, stddev,
-                                 reinterpret_cast<mxd_stream_t>(e->stream)))
+    if (int rc = mxd::fill_normal_dev(e->wbase + t.offset, t.dtype, n, seed, t.id, stddev, t.shift, e->stream))
         return rc;
     HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_fill_tensor");
     return MXD_OK;
@@ -550,6 +444,12 @@ extern "C" int mxd_engine_get_logits(mxd_engine* e, float* host) {
     HIP_OK(hipMemcpyAsync(host, e->logits, (size_t)e->c.vocab * 4, hipMemcpyDeviceToHost, e->stream),
            "mxd_engine_get_logits");
     HIP_OK(hipStreamSynchronize(e->stream), "mxd_engine_get_logits");
+    // Gemma-4's final softcap, applied to the dumped logits on the host as the
+    // reference's --dump-logits does (KG/main.swift:657-662); argmax ran on
+    // the raw logits (the cap is monotonic).
+    const float cap = e->arch == ENG_GEMMA4 ? e->g4.softcap : 0.0f;
+    if (cap > 0.0f)
+        for (int i = 0; i < e->c.vocab; ++i) host[i] = cap * tanhf(host[i] / cap);
     return MXD_OK;
 }
 
@@ -562,6 +462,7 @@ extern "C" int mxd_engine_step(mxd_engine* e, int pos, int sample) {
 
 extern "C" int mxd_engine_prefill(mxd_engine* e, int n) {
     MXD_REQUIRE(e && n >= 1 && n <= e->max_ctx, MXD_ERR_INVALID_ARG, "mxd_engine_prefill: n=%d", n);
+    if (e->arch == ENG_GEMMA4) return g4_prefill(e, n);
     if (n > 1 && mxd::tunable("ENG_NO_GEMM", 0) != 1) {
         for (int done = 0; done < n;) {
             const int rows = min(e->max_rows, n - done);
@@ -586,12 +487,12 @@ extern "C" int mxd_engine_decode(mxd_engine* e, int pos, int count) {
         const int rc = encode_step(e, 0, e->pos, true);
         const hipError_t ce = hipStreamEndCapture(e->stream, &g);
         if (rc) {
-            if (g) hipGraphDestroy(g);
+            if (g) (void)hipGraphDestroy(g);
             return rc;
         }
         HIP_OK(ce, "mxd_engine_decode: end capture");
         const hipError_t ie = hipGraphInstantiate(&e->graph, g, nullptr, nullptr, 0);
-        hipGraphDestroy(g);
+        (void)hipGraphDestroy(g);
         HIP_OK(ie, "mxd_engine_decode: instantiate");
     }
     if (pos != e->pos_next) {

@@ -33,6 +33,11 @@ int rope_kv_dev(float* qkv, uint16_t* kcache, uint16_t* vcache, const float* inv
 int argmax_dev(const float* logits, int32_t* tokens, int N, int out_idx, int32_t* pos_dev, bool advance,
                void* workspace, hipStream_t s, int32_t* host_tokens = nullptr);
 
+// mxd_fill_normal with every fp32 value then shifted by `shift` (fp32 add;
+// shift != 0 needs MXD_F32).
+int fill_normal_dev(void* dst, int dtype, uint64_t n, uint64_t seed, uint64_t tensor_id, float stddev, float shift,
+                    hipStream_t s);
+
 // fp16 (MXD_W_F16) or int8 block-32 (MXD_W_Q8B32) matvec whose fp32 x is
 // rounded to fp16 as it is loaded.
 int matvec_xr16(int w_format, const void* W, const uint16_t* scales, const float* x, float* y, int M, int K,

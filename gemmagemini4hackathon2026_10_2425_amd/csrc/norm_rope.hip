@@ -169,6 +169,107 @@ rope_kv_paged_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kpool, uint
     }
 }
 
+// ---- Gemma-4 operators --------------------------------------------------------
+
+// Sandwich-norm residual update, one workgroup per row (KG/kernels.metal:100-125):
+//   x[r][i] = (x[r][i] + src[r][i] * rsqrt(mean(src[r]^2) + eps) * w[i]) * post
+// post is the layer scalar after a layer's last residual add, else 1.
+__global__ void __launch_bounds__(NORM_THREADS)
+rmsnorm_add_kernel(const float* __restrict__ src, const float* __restrict__ w, float* __restrict__ x, int D, float eps,
+                   float post) {
+    __shared__ float scratch[NORM_THREADS / 64];
+    const float* sr = src + (size_t)blockIdx.x * D;
+    float* xr = x + (size_t)blockIdx.x * D;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < D; i += NORM_THREADS) ss = fmaf(sr[i], sr[i], ss);
+    ss = block_sum(ss, scratch);
+    const float scale = rsqrtf(ss / (float)D + eps);
+    for (int i = threadIdx.x; i < D; i += NORM_THREADS) xr[i] = (xr[i] + sr[i] * scale * w[i]) * post;
+}
+
+// Per-layer-embedding combine, one workgroup per (layer slice, row) of P values
+// (KG/kernels.metal:127-149):
+//   ple[r][l][i] = (rmsnorm(proj[r][l] * proj_scale)[i] * w[i] + ple[r][l][i]) / sqrt(2)
+// ple holds the scaled token-identity embedding on entry.
+__global__ void __launch_bounds__(NORM_THREADS)
+ple_combine_kernel(const float* __restrict__ proj, float* __restrict__ ple, const float* __restrict__ w, int P,
+                   int LP, float proj_scale, float eps) {
+    __shared__ float scratch[NORM_THREADS / 64];
+    const size_t base = (size_t)blockIdx.y * LP + (size_t)blockIdx.x * P;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < P; i += NORM_THREADS) {
+        const float v = proj[base + i] * proj_scale;
+        ss = fmaf(v, v, ss);
+    }
+    ss = block_sum(ss, scratch);
+    const float scale = rsqrtf(ss / (float)P + eps);
+    for (int i = threadIdx.x; i < P; i += NORM_THREADS) {
+        const float v = proj[base + i] * proj_scale;
+        ple[base + i] = (v * scale * w[i] + ple[base + i]) * 0.70710678118654752f;
+    }
+}
+
+// Per-head RMSNorm of q and k (weights q_w, k_w) and v (no weight), RoPE on q
+// and k over the first rope_pairs rotation pairs (the rest are the identity),
+// and the k, v append (KG/kernels.metal:236-304). qkv rows are
+// [q n_heads*hd | k n_kv*hd | v n_kv*hd], row t at position pos0 + t (or
+// *pos_dev + t); with n_kv == 0 (a KV-shared layer) only q is there. One
+// workgroup per (head, row), thread i of hd/2 owns the pair (i, i + hd/2).
+__global__ void __launch_bounds__(256)
+qk_norm_rope_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kcache, uint16_t* __restrict__ vcache,
+                    const float* __restrict__ q_w, const float* __restrict__ k_w, const float* __restrict__ inv_freq,
+                    int n_heads, int n_kv, int hd, int rope_pairs, int max_ctx, float eps, int pos0,
+                    const int32_t* __restrict__ pos_dev) {
+    __shared__ float scratch[4];
+    const int h = blockIdx.x, t = blockIdx.y, i = threadIdx.x, half_d = hd >> 1;
+    if (pos_dev) pos0 = pos_dev[0];
+    const int pos = pos0 + t;
+    const bool in_cache = pos >= 0 && pos < max_ctx;
+    float* v = qkv + (size_t)t * (n_heads + 2 * n_kv) * hd + (size_t)h * hd;
+    const bool live = i < half_d;
+    float a = live ? v[i] : 0.0f, b = live ? v[i + half_d] : 0.0f;
+    // the head's sum of squares across the workgroup's waves
+    float ss = mxd::wave_sum(fmaf(a, a, b * b));
+    if ((i & 63) == 0) scratch[i >> 6] = ss;
+    __syncthreads();
+    ss = scratch[0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) ss += scratch[w];
+    if (!live) return;
+    const float scale = rsqrtf(ss / (float)hd + eps);
+    a *= scale;
+    b *= scale;
+    const int k = pos & 31;
+    if (h >= n_heads + n_kv) {  // v: no weight, no rotation
+        if (!in_cache) return;
+        const int kvh = h - n_heads - n_kv;
+        const size_t tile = ((size_t)kvh * max_ctx + (pos & ~31)) * hd;
+        vcache[tile + mxd::v_tile_offset(k, i)] = mxd::f2h_bits(a);
+        vcache[tile + mxd::v_tile_offset(k, i + half_d)] = mxd::f2h_bits(b);
+        return;
+    }
+    const float* w = h < n_heads ? q_w : k_w;
+    a *= w[i];
+    b *= w[i + half_d];
+    if (i < rope_pairs) {
+        const float ang = (float)pos * inv_freq[i];
+        float sn, cs;
+        sincosf(ang, &sn, &cs);
+        const float ra = a * cs - b * sn;
+        const float rb = b * cs + a * sn;
+        a = ra;
+        b = rb;
+    }
+    if (h < n_heads) {
+        v[i] = a;
+        v[i + half_d] = b;
+    } else if (in_cache) {
+        const int kvh = h - n_heads;
+        const size_t tile = ((size_t)kvh * max_ctx + (pos & ~31)) * hd;
+        kcache[tile + mxd::k_tile_offset(k, i, hd)] = mxd::f2h_bits(a);
+        kcache[tile + mxd::k_tile_offset(k, i + half_d, hd)] = mxd::f2h_bits(b);
+    }
+}
+
 }  // namespace
 
 namespace mxd {
@@ -261,4 +362,48 @@ extern "C" int mxd_rope_kv_paged(float* qkv, uint16_t* kpool, uint16_t* vpool, i
                        qkv, kpool, vpool, inv_freq, n_heads, n_kv_heads, head_dim, page_table, max_pages, seq_lens,
                        n_pages);
     return mxd::check_launch("mxd_rope_kv_paged");
+}
+
+// ---- Gemma-4 entry points -------------------------------------------------------
+
+extern "C" int mxd_rmsnorm_add(const float* src, const float* w, float* x, int rows, int D, float eps, float post,
+                               mxd_stream_t stream) {
+    MXD_REQUIRE(src && w && x, MXD_ERR_INVALID_ARG, "mxd_rmsnorm_add: null pointer");
+    MXD_REQUIRE(rows > 0 && D > 0, MXD_ERR_INVALID_ARG, "mxd_rmsnorm_add: rows=%d D=%d must be positive", rows, D);
+    hipLaunchKernelGGL(rmsnorm_add_kernel, dim3(rows), dim3(NORM_THREADS), 0, mxd::as_stream(stream), src, w, x, D,
+                       eps, post);
+    return mxd::check_launch("mxd_rmsnorm_add");
+}
+
+extern "C" int mxd_ple_combine(const float* proj, float* ple, const float* w, int rows, int n_layers, int P,
+                               float proj_scale, float eps, mxd_stream_t stream) {
+    MXD_REQUIRE(proj && ple && w, MXD_ERR_INVALID_ARG, "mxd_ple_combine: null pointer");
+    MXD_REQUIRE(rows > 0 && n_layers > 0 && P > 0, MXD_ERR_INVALID_ARG, "mxd_ple_combine: rows=%d n_layers=%d P=%d",
+                rows, n_layers, P);
+    hipLaunchKernelGGL(ple_combine_kernel, dim3(n_layers, rows), dim3(NORM_THREADS), 0, mxd::as_stream(stream), proj,
+                       ple, w, P, n_layers * P, proj_scale, eps);
+    return mxd::check_launch("mxd_ple_combine");
+}
+
+extern "C" int mxd_qk_norm_rope_kv(float* qkv, uint16_t* kcache, uint16_t* vcache, const float* q_w, const float* k_w,
+                                   const float* inv_freq, int n_heads, int n_kv_heads, int head_dim, int rope_pairs,
+                                   int max_ctx, float eps, int pos0, int rows, const int32_t* pos_dev,
+                                   mxd_stream_t stream) {
+    MXD_REQUIRE(qkv && q_w && inv_freq, MXD_ERR_INVALID_ARG, "mxd_qk_norm_rope_kv: null pointer");
+    MXD_REQUIRE(n_heads > 0 && n_kv_heads >= 0 && rows > 0, MXD_ERR_INVALID_ARG,
+                "mxd_qk_norm_rope_kv: n_heads=%d n_kv_heads=%d rows=%d", n_heads, n_kv_heads, rows);
+    MXD_REQUIRE(n_kv_heads == 0 || (kcache && vcache && k_w), MXD_ERR_INVALID_ARG,
+                "mxd_qk_norm_rope_kv: kv heads need caches and k_w");
+    MXD_REQUIRE(head_dim >= 32 && head_dim <= 512 && head_dim % 32 == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_qk_norm_rope_kv: head_dim %d (a multiple of 32 up to 512)", head_dim);
+    MXD_REQUIRE(rope_pairs >= 0 && rope_pairs <= head_dim / 2, MXD_ERR_INVALID_ARG,
+                "mxd_qk_norm_rope_kv: rope_pairs %d outside [0, %d]", rope_pairs, head_dim / 2);
+    MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED, "mxd_qk_norm_rope_kv: max_ctx=%d", max_ctx);
+    MXD_REQUIRE(pos_dev || (pos0 >= 0 && (n_kv_heads == 0 || pos0 + rows <= max_ctx)), MXD_ERR_INVALID_ARG,
+                "mxd_qk_norm_rope_kv: positions [%d, %d) outside [0, %d)", pos0, pos0 + rows, max_ctx);
+    const int threads = (head_dim / 2 + 63) / 64 * 64;
+    hipLaunchKernelGGL(qk_norm_rope_kernel, dim3(n_heads + 2 * n_kv_heads, rows), dim3(threads), 0,
+                       mxd::as_stream(stream), qkv, kcache, vcache, q_w, k_w, inv_freq, n_heads, n_kv_heads, head_dim,
+                       rope_pairs, max_ctx, eps, pos0, pos_dev);
+    return mxd::check_launch("mxd_qk_norm_rope_kv");
 }

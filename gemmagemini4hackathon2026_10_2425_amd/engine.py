@@ -67,16 +67,150 @@ LLAMA32_1B = ModelShape(n_layers=16, dim=2048, n_heads=32, n_kv_heads=8, head_di
                         embed_scale_sqrt_dim=False, tie_embeddings=True, rope_scaling=(32.0, 1.0, 4.0, 8192))
 
 
+@dataclass(frozen=True)
+class Gemma4Layer:
+    """Per-layer facts of a Gemma-4 text model (mxd_gemma4_layer), as the
+    reference's converter resolves them (KG/convert_weights.py engine_config)."""
+
+    head_dim: int
+    ffn_dim: int
+    sliding: bool
+    kv_layer: int
+    rope_pairs: int
+    rope_theta: float
+    layer_scalar: float = 1.0
+
+
+@dataclass(frozen=True)
+class Gemma4Shape:
+    """A Gemma-4 text model (mxd_gemma4_config; KG/main.swift:80-101)."""
+
+    dim: int
+    n_heads: int
+    n_kv_heads: int
+    vocab: int
+    ple_dim: int
+    ple_vocab: int
+    window: int
+    layers: tuple
+    rms_eps: float = 1e-6
+    softcap: float = 30.0
+
+    @property
+    def n_layers(self) -> int:
+        return len(self.layers)
+
+    def to_c(self) -> tuple[_lib.Gemma4Config, ctypes.Array]:
+        """The C config and the layer array it points at (keep both alive)."""
+        arr = (_lib.Gemma4Layer * self.n_layers)(*[
+            _lib.Gemma4Layer(y.head_dim, y.ffn_dim, int(y.sliding), y.kv_layer, y.rope_pairs, y.rope_theta,
+                             y.layer_scalar) for y in self.layers])
+        cfg = _lib.Gemma4Config(self.n_layers, self.dim, self.n_heads, self.n_kv_heads, self.vocab, self.ple_dim,
+                                self.ple_vocab, self.window, self.rms_eps, self.softcap, arr)
+        return cfg, arr
+
+    @property
+    def weight_bytes(self) -> int:
+        """Bytes of weights one decode step streams: every layer's matrices and
+        norms, the per-layer-embedding projection and the tied head; of the
+        per-layer-embedding table only the token's row."""
+        D, P, L, NH = self.dim, self.ple_dim, self.n_layers, self.n_heads
+        b = 2 * self.vocab * D + 2 * L * P * D + 2 * L * P + 4 * (P + D)
+        for l, y in enumerate(self.layers):
+            own = y.kv_layer == l
+            qkv = (NH + (2 * self.n_kv_heads if own else 0)) * y.head_dim
+            b += 2 * (qkv * D + D * NH * y.head_dim + 3 * y.ffn_dim * D + 2 * P * D)
+            b += 4 * (4 * D + y.head_dim * (2 if own else 1))
+        return b
+
+    @staticmethod
+    def layers_from_hf(c: dict, layer_scalars=None) -> tuple:
+        """Per-layer facts from an HF Gemma-4 text config, as
+        KG/convert_weights.py engine_config resolves them: a KV-shared layer
+        (index >= n_layers - num_kv_shared_layers) reads the cache of the last
+        non-shared layer of its type and, with use_double_wide_mlp, has twice
+        the MLP width; "proportional" RoPE rotates partial_rotary_factor of
+        the pairs."""
+        types = list(c["layer_types"])
+        n = int(c["num_hidden_layers"])
+        if len(types) != n:
+            raise ValueError(f"layer_types has {len(types)} entries for {n} layers")
+        first_shared = n - int(c.get("num_kv_shared_layers", 0) or 0)
+        last_of_type = {t: i for i, t in enumerate(types[:first_shared])}
+        out = []
+        for i, t in enumerate(types):
+            if t not in ("sliding_attention", "full_attention"):
+                raise ValueError(f"layer type {t!r} is not supported")
+            sliding = t == "sliding_attention"
+            hd = int(c["head_dim"] if sliding else c.get("global_head_dim") or c["head_dim"])
+            rope = c["rope_parameters"][t]
+            if rope.get("rope_type", "default") == "default":
+                pairs = hd // 2
+            elif rope["rope_type"] == "proportional":
+                pairs = int(rope.get("partial_rotary_factor", 1.0) * hd // 2)
+            else:
+                raise ValueError(f"rope type {rope['rope_type']!r} is not supported (default or proportional)")
+            shared = i >= first_shared
+            if shared and t not in last_of_type:
+                raise ValueError(f"layer {i} shares the cache of a {t} layer, but none precedes it")
+            double = bool(c.get("use_double_wide_mlp", False)) and shared
+            out.append(Gemma4Layer(head_dim=hd, ffn_dim=int(c["intermediate_size"]) * (2 if double else 1),
+                                   sliding=sliding, kv_layer=last_of_type[t] if shared else i, rope_pairs=pairs,
+                                   rope_theta=float(rope["rope_theta"]),
+                                   layer_scalar=1.0 if layer_scalars is None else float(layer_scalars[i])))
+        return tuple(out)
+
+    @classmethod
+    def from_hf(cls, c: dict, layers=None) -> "Gemma4Shape":
+        """Shape of an HF Gemma-4 text config (the keys KG/main.swift:86-95
+        reads); layers: the resolved per-layer facts, else layers_from_hf(c)."""
+        if int(c.get("num_key_value_heads", 1)) < 1:
+            raise ValueError("num_key_value_heads must be positive")
+        if c.get("enable_moe_block") or c.get("attention_k_eq_v"):
+            raise ValueError("only the dense Gemma-4 layout (E2B / E4B) is supported")
+        return cls(dim=int(c["hidden_size"]), n_heads=int(c["num_attention_heads"]),
+                   n_kv_heads=int(c.get("num_key_value_heads", 1)), vocab=int(c["vocab_size"]),
+                   ple_dim=int(c["hidden_size_per_layer_input"]),
+                   ple_vocab=int(c.get("vocab_size_per_layer_input", c["vocab_size"])),
+                   window=int(c["sliding_window"]), layers=tuple(layers) if layers else cls.layers_from_hf(c),
+                   rms_eps=float(c.get("rms_norm_eps", 1e-6)),
+                   softcap=float(c.get("final_logit_softcapping") or 0.0))
+
+
+# google/gemma-4-E2B-it's text model (KG/PLAN.md, "The model"): 35 layers of
+# [sliding x4, full] x7, hidden 1536, 8 query heads / 1 KV head, head_dim 256
+# (sliding, window 512, RoPE theta 1e4) / 512 (full, theta 1e6, a quarter of
+# the pairs rotated), the last 20 layers sharing the caches of layers 13 / 14
+# with double-width MLPs (6144 -> 12288), per-layer embeddings of 256, vocab
+# 262144, softcap 30. Layer scalars are learned (1 here: synthetic weights).
+GEMMA4_E2B_TEXT_CONFIG = {
+    "hidden_size": 1536, "num_hidden_layers": 35, "num_attention_heads": 8, "num_key_value_heads": 1,
+    "head_dim": 256, "global_head_dim": 512, "intermediate_size": 6144, "vocab_size": 262144,
+    "vocab_size_per_layer_input": 262144, "hidden_size_per_layer_input": 256, "sliding_window": 512,
+    "rms_norm_eps": 1e-6, "final_logit_softcapping": 30.0, "num_kv_shared_layers": 20, "use_double_wide_mlp": True,
+    "layer_types": (["sliding_attention"] * 4 + ["full_attention"]) * 7,
+    "rope_parameters": {"sliding_attention": {"rope_type": "default", "rope_theta": 10000.0},
+                        "full_attention": {"rope_type": "proportional", "partial_rotary_factor": 0.25,
+                                           "rope_theta": 1000000.0}},
+}
+GEMMA4_E2B = Gemma4Shape.from_hf(GEMMA4_E2B_TEXT_CONFIG)
+
+
 class Engine:
     """Device-resident greedy decoder. Token t of a run is written by the GPU
-    into tokens[t + 1]; decode() queues all steps without a host sync."""
+    into tokens[t + 1]; decode() queues all steps without a host sync. The
+    shape picks the model family: ModelShape (Llama / Gemma) or Gemma4Shape."""
 
-    def __init__(self, shape: ModelShape, max_ctx: int = 4096):
+    def __init__(self, shape: ModelShape | Gemma4Shape, max_ctx: int = 4096):
         lib = _lib.load()
         self.shape, self.max_ctx = shape, max_ctx
-        cfg = shape.to_c()
         h = ctypes.c_void_p()
-        call("mxd_engine_create", ctypes.byref(cfg), max_ctx, ctypes.byref(h))
+        if isinstance(shape, Gemma4Shape):
+            cfg, _layers = shape.to_c()
+            call("mxd_engine_create_gemma4", ctypes.byref(cfg), max_ctx, ctypes.byref(h))
+        else:
+            cfg = shape.to_c()
+            call("mxd_engine_create", ctypes.byref(cfg), max_ctx, ctypes.byref(h))
         self._h = h
         self._lib = lib
 
@@ -163,6 +297,7 @@ class Engine:
         return self.tokens(at, 1)[0]
 
     def logits(self) -> np.ndarray:
+        """fp32 logits of the last sampled step (Gemma-4: after the softcap)."""
         a = np.empty(self.shape.vocab, np.float32)
         call("mxd_engine_get_logits", self._h, a.ctypes.data)
         return a

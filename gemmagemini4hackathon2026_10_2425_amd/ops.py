@@ -13,6 +13,10 @@ KG = the Gemma-4-E2B kernel folder):
     attention                                           KL/kernels.metal:235-305
     argmax                                              KL/kernels.metal:310-345
     f32_to_f16                                          KL/kernels.metal:361-365
+    attention(window=) / attention_prefill(window=)     KG/kernels.metal:306-393
+    rmsnorm_add                                         KG/kernels.metal:100-125
+    ple_combine                                         KG/kernels.metal:127-149
+    qk_norm_rope_kv (qkv_norm_rope)                     KG/kernels.metal:236-304
 
 Every function checks shapes on the host and raises ValueError before any
 launch (the reference's host preconditions, KG/main.swift:306, crash instead).
@@ -274,9 +278,10 @@ def attention_workspace(n_heads: int, n_kv_heads: int, head_dim: int, max_ctx: i
 
 
 def attention(q, kcache, vcache, n_keys: int, n_heads: int, scale: float | None = None, out=None, workspace=None,
-              pos_dev=None) -> torch.Tensor:
+              pos_dev=None, window: int = 0) -> torch.Tensor:
     """Single-query attention of q [n_heads*hd] over keys [0, n_keys) of the
-    tiled caches (kcache, vcache [n_kv, max_ctx, hd], see to_tiles)."""
+    tiled caches (kcache, vcache [n_kv, max_ctx, hd], see to_tiles); with a
+    window, over the last `window` of them (a Gemma-4 sliding layer)."""
     _on_gpu(q, kcache, vcache)
     n_kv, max_ctx, hd = _check_caches(kcache, vcache, "attention")
     _need(q.numel() == n_heads * hd and q.dtype == torch.float32, "attention: q float32 [n_heads*hd]")
@@ -284,6 +289,12 @@ def attention(q, kcache, vcache, n_keys: int, n_heads: int, scale: float | None 
     out = torch.empty(n_heads * hd, dtype=torch.float32, device=q.device) if out is None else out
     if workspace is None:
         workspace = attention_workspace(n_heads, n_kv, hd, max_ctx, q.device)
+    if window:
+        call(
+            "mxd_attention_window", _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(out), n_heads, n_kv, hd, max_ctx,
+            int(n_keys), _ptr(pos_dev), int(window), float(scale), _ptr(workspace), workspace.numel(), _stream(),
+        )
+        return out
     call(
         "mxd_attention", _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(out), n_heads, n_kv, hd, max_ctx, int(n_keys),
         _ptr(pos_dev), float(scale), _ptr(workspace), workspace.numel(), _stream(),
@@ -328,11 +339,11 @@ def matvec_f16_attn_merge(W, partials, n_splits: int, n_heads: int, head_dim: in
 
 
 def attention_prefill(q, kcache, vcache, pos0: int, n_heads: int, scale: float | None = None, out=None,
-                      q_stride: int | None = None, rows: int | None = None) -> torch.Tensor:
+                      q_stride: int | None = None, rows: int | None = None, window: int = 0) -> torch.Tensor:
     """Causal attention of a prefill chunk: row t of q (rows q_stride floats
     apart; the q part of a qkv row [rows, qkv_dim] works in place) is the query
-    at position pos0 + t over keys [0, pos0 + t] of the tiled caches. Returns
-    out [rows, n_heads * hd]."""
+    at position pos0 + t over keys [0, pos0 + t] of the tiled caches (with a
+    window, the last `window` of them). Returns out [rows, n_heads * hd]."""
     _on_gpu(q, kcache, vcache)
     n_kv, max_ctx, hd = _check_caches(kcache, vcache, "attention_prefill")
     _need(q.dtype == torch.float32 and q.is_contiguous() and q.dim() == 2, "attention_prefill: q float32 [rows, stride]")
@@ -343,9 +354,63 @@ def attention_prefill(q, kcache, vcache, pos0: int, n_heads: int, scale: float |
     out = torch.empty((rows, n_heads * hd), dtype=torch.float32, device=q.device) if out is None else out
     _need(out.dtype == torch.float32 and out.is_contiguous() and out.numel() == rows * n_heads * hd,
           "attention_prefill: out float32 [rows, n_heads * hd]")
+    if window:
+        call("mxd_attention_prefill_window", _ptr(q), q_stride, _ptr(kcache), _ptr(vcache), _ptr(out), n_heads * hd,
+             n_heads, n_kv, hd, max_ctx, int(pos0), int(rows), int(window), float(scale), _stream())
+        return out
     call("mxd_attention_prefill", _ptr(q), q_stride, _ptr(kcache), _ptr(vcache), _ptr(out), n_heads * hd, n_heads,
          n_kv, hd, max_ctx, int(pos0), int(rows), float(scale), _stream())
     return out
+
+
+# ---------------------------------------------------------------- Gemma-4
+
+
+def rmsnorm_add(src, w, x, eps: float, post: float = 1.0) -> torch.Tensor:
+    """x = (x + rmsnorm(src) * w) * post per row (src, x float32 [rows, D] or [D])."""
+    _on_gpu(src, w, x)
+    D = w.numel()
+    _need(src.dtype == torch.float32 and x.dtype == torch.float32 and w.dtype == torch.float32,
+          "rmsnorm_add: float32 tensors")
+    _need(src.numel() == x.numel() and x.numel() % D == 0, "rmsnorm_add: src and x are rows of len(w)")
+    call("mxd_rmsnorm_add", _ptr(src), _ptr(w), _ptr(x), x.numel() // D, D, float(eps), float(post), _stream())
+    return x
+
+
+def ple_combine(proj, ple, w, n_layers: int, dim: int, eps: float) -> torch.Tensor:
+    """ple = (rmsnorm(proj / sqrt(dim)) * w + ple) / sqrt(2) over each of the
+    n_layers slices of len(w) values per row (proj, ple float32 [rows, n_layers * P])."""
+    _on_gpu(proj, ple, w)
+    P = w.numel()
+    _need(proj.dtype == ple.dtype == w.dtype == torch.float32, "ple_combine: float32 tensors")
+    _need(proj.numel() == ple.numel() and ple.numel() % (n_layers * P) == 0,
+          "ple_combine: proj and ple are rows of n_layers * len(w)")
+    rows = ple.numel() // (n_layers * P)
+    call("mxd_ple_combine", _ptr(proj), _ptr(ple), _ptr(w), rows, n_layers, P, 1.0 / math.sqrt(dim), float(eps),
+         _stream())
+    return ple
+
+
+def qk_norm_rope_kv(qkv, kcache, vcache, q_w, k_w, inv_freq_t, n_heads: int, rope_pairs: int, eps: float,
+                    pos0: int = 0, pos_dev=None, head_dim: int | None = None) -> None:
+    """Per-head RMSNorm of q (q_w), k (k_w), v (no weight), RoPE over the first
+    rope_pairs pairs of q and k, q back in place, k and v appended (fp16) at
+    pos0 + row. kcache None: q only (a layer sharing another's cache; give
+    head_dim)."""
+    _on_gpu(qkv, q_w, inv_freq_t)
+    if kcache is not None:
+        _on_gpu(kcache, vcache, k_w)
+        n_kv, max_ctx, hd = _check_caches(kcache, vcache, "qk_norm_rope_kv")
+    else:
+        _need(head_dim is not None, "qk_norm_rope_kv: head_dim is needed without caches")
+        n_kv, max_ctx, hd = 0, 32, head_dim
+    row_len = (n_heads + 2 * n_kv) * hd
+    _need(qkv.dtype == torch.float32 and qkv.numel() % row_len == 0, f"qk_norm_rope_kv: qkv rows of {row_len} floats")
+    _need(q_w.numel() == hd and (k_w is None or k_w.numel() == hd), "qk_norm_rope_kv: norm weights of head_dim")
+    _need(inv_freq_t.numel() >= hd // 2, "qk_norm_rope_kv: inv_freq has head_dim/2 entries")
+    call("mxd_qk_norm_rope_kv", _ptr(qkv), _ptr(kcache), _ptr(vcache), _ptr(q_w), _ptr(k_w), _ptr(inv_freq_t),
+         n_heads, n_kv, hd, int(rope_pairs), max_ctx, float(eps), int(pos0), qkv.numel() // row_len, _ptr(pos_dev),
+         _stream())
 
 
 def gemm_workspace(n_rows: int, M: int, K: int, glu: bool = False, device="cuda") -> torch.Tensor:

@@ -181,8 +181,8 @@ size_t mxd_attention_workspace_size(int n_heads, int n_kv_heads, int head_dim, i
  * every query head h, kvh = h / (n_heads / n_kv_heads) (GQA/MQA), fp32 scores
  * and softmax. Split over the key axis with an online softmax and a
  * log-sum-exp merge, so n_keys is bounded only by max_ctx; the G = n_heads /
- * n_kv_heads query heads of a group share each K/V tile. head_dim 128 or 256;
- * max_ctx % 32 == 0. q [n_heads*hd] fp32, out [n_heads*hd] fp32.
+ * n_kv_heads query heads of a group share each K/V tile. head_dim 64, 128, 256
+ * or 512; max_ctx % 32 == 0. q [n_heads*hd] fp32, out [n_heads*hd] fp32.
  * If n_keys_dev is not NULL the key count is read on the device from
  * *n_keys_dev (+1), so a captured step replays at a moving position.
  * Replaces attention (KL/kernels.metal:235-305, KG/kernels.metal:317-399;
@@ -230,6 +230,47 @@ int mxd_attention_split(const float* q, const uint16_t* kcache, const uint16_t* 
 int mxd_attention_prefill(const float* q, int q_stride, const uint16_t* kcache, const uint16_t* vcache,
                           float* out, int out_stride, int n_heads, int n_kv_heads, int head_dim, int max_ctx,
                           int pos0, int rows, float scale, mxd_stream_t stream);
+
+/* Sliding-window forms: a query that sees n keys attends to keys
+ * [max(0, n - window), n) (window 0: all n). Gemma-4's sliding layers
+ * (window 512; KG/kernels.metal:306-393, start = pos + 1 - window,
+ * AttnParams.window; host KG/main.swift:358-376). Otherwise identical to
+ * mxd_attention / mxd_attention_prefill, head_dim 512 included. */
+int mxd_attention_window(const float* q, const uint16_t* kcache, const uint16_t* vcache, float* out,
+                         int n_heads, int n_kv_heads, int head_dim, int max_ctx, int n_keys,
+                         const int32_t* n_keys_dev, int window, float scale, void* workspace, size_t ws_bytes,
+                         mxd_stream_t stream);
+int mxd_attention_prefill_window(const float* q, int q_stride, const uint16_t* kcache, const uint16_t* vcache,
+                                 float* out, int out_stride, int n_heads, int n_kv_heads, int head_dim,
+                                 int max_ctx, int pos0, int rows, int window, float scale, mxd_stream_t stream);
+
+/* ---- Gemma-4 operators ---------------------------------------------------- */
+
+/* Sandwich-norm residual update, per row r of D values:
+ * x[r] = (x[r] + src[r] * rsqrt(mean(src[r]^2) + eps) * w) * post, fp32.
+ * post is the layer scalar after a layer's last residual add, else 1.
+ * Replaces rmsnorm_add (KG/kernels.metal:100-125; host KG/main.swift:273-285). */
+int mxd_rmsnorm_add(const float* src, const float* w, float* x, int rows, int D, float eps, float post,
+                    mxd_stream_t stream);
+
+/* Per-layer-embedding combine, rows x n_layers slices of P values:
+ * ple[r][l] = (rmsnorm(proj[r][l] * proj_scale) * w + ple[r][l]) / sqrt(2),
+ * with ple holding the scaled token-identity rows on entry.
+ * Replaces ple_combine (KG/kernels.metal:127-149; host KG/main.swift:287-299). */
+int mxd_ple_combine(const float* proj, float* ple, const float* w, int rows, int n_layers, int P,
+                    float proj_scale, float eps, mxd_stream_t stream);
+
+/* qkv rows [q n_heads*hd | k n_kv_heads*hd | v n_kv_heads*hd] fp32 (row r at
+ * position pos0 + r, or *pos_dev + r): per-head RMSNorm of q (weight q_w),
+ * k (k_w) and v (no weight), HF rotate_half RoPE on q and k over the rotation
+ * pairs i < rope_pairs (the rest unrotated), q written back in place, k and
+ * v appended as fp16 to the tiled caches. n_kv_heads 0: q only (a layer that
+ * reads another layer's cache). head_dim a multiple of 32 up to 512.
+ * Replaces qkv_norm_rope (KG/kernels.metal:236-304; host KG/main.swift:338-356). */
+int mxd_qk_norm_rope_kv(float* qkv, uint16_t* kcache, uint16_t* vcache, const float* q_w, const float* k_w,
+                        const float* inv_freq, int n_heads, int n_kv_heads, int head_dim, int rope_pairs,
+                        int max_ctx, float eps, int pos0, int rows, const int32_t* pos_dev,
+                        mxd_stream_t stream);
 
 /* ---- greedy sample -------------------------------------------------------- */
 
@@ -355,6 +396,29 @@ typedef struct mxd_model_config {
     int rope_original_max_positions;
 } mxd_model_config;
 
+/* Gemma-4 per-layer facts, as the reference's converter resolves them into
+ * the weight file's "engine" header (KG/convert_weights.py engine_config;
+ * read at KG/main.swift:75-101). */
+typedef struct mxd_gemma4_layer {
+    int head_dim;     /* 64, 128, 256 (E2B sliding) or 512 (E2B full)              */
+    int ffn_dim;      /* doubled on KV-shared layers                               */
+    int sliding;      /* 1: attends to the last `window` keys                      */
+    int kv_layer;     /* the layer whose K/V cache it reads (itself, or shared)     */
+    int rope_pairs;   /* rotated pairs (hd/2 default RoPE; fewer: proportional)    */
+    float rope_theta;
+    float layer_scalar;
+} mxd_gemma4_layer;
+
+/* Gemma-4 text model (KG/main.swift:80-101): tied embedding scaled by
+ * sqrt(dim), per-layer embeddings of ple_dim per layer, RMSNorm weights
+ * multiplied as stored (w, not 1 + w), attention scale 1 (q/k norms), GeGLU,
+ * final logit softcap (applied where logits are read, not before argmax). */
+typedef struct mxd_gemma4_config {
+    int n_layers, dim, n_heads, n_kv_heads, vocab, ple_dim, ple_vocab, window;
+    float rms_eps, softcap;
+    const mxd_gemma4_layer* layers; /* n_layers entries, copied at create */
+} mxd_gemma4_config;
+
 typedef struct mxd_engine mxd_engine;
 
 /* Allocates weights (one arena, tensors 256-byte aligned as in the reference's
@@ -362,6 +426,17 @@ typedef struct mxd_engine mxd_engine;
  * max_ctx + 1 ids and fp16 KV caches; owns one HIP stream. Replaces Engine.init
  * (KL/main.swift:168-215). Weights start uninitialised. */
 int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_engine** out);
+/* The Gemma-4 engine (KG/main.swift:148-457) behind the same handle: every
+ * mxd_engine_* call below serves it. Tensors (KG/convert_weights.py): "embed",
+ * "ple_embed" [ple_vocab][n_layers*ple_dim], "ple_proj" [n_layers*ple_dim][dim],
+ * "ple_norm", "final_norm", and per layer "l<i>.attn_norm", "l<i>.wqkv" (q|k|v
+ * rows; q only on a layer with kv_layer != i), "l<i>.q_norm", "l<i>.k_norm"
+ * (own K/V only), "l<i>.wo", "l<i>.post_attn_norm", "l<i>.ffn_norm",
+ * "l<i>.wgate", "l<i>.wup", "l<i>.wdown", "l<i>.post_ffn_norm",
+ * "l<i>.ple_gate", "l<i>.ple_out", "l<i>.post_ple_norm". K/V caches exist for
+ * the layers that own them. mxd_engine_get_logits returns softcapped logits
+ * (--dump-logits, KG/main.swift:657-662). */
+int mxd_engine_create_gemma4(const mxd_gemma4_config* cfg, int max_ctx, mxd_engine** out);
 int mxd_engine_destroy(mxd_engine* e);
 /* Weight tensors by index / name: "embed", "final_norm", "l<i>.attn_norm",
  * "l<i>.wqkv" (rows q|k|v), "l<i>.wo", "l<i>.ffn_norm", "l<i>.wgate",
@@ -378,7 +453,11 @@ int mxd_engine_upload(mxd_engine* e, int index, const void* host, size_t bytes);
 int mxd_engine_download(mxd_engine* e, int index, void* host, size_t bytes);
 /* Fills every weight with mxd_fill_normal(seed, tensor id), ids: embed 1,
  * final_norm 2, lm_head 3, layer l: 1000 + 16 l + {attn_norm 0, wqkv 1, wo 2,
- * ffn_norm 3, wgate 4, wup 5, wdown 6}. Synchronises. */
+ * ffn_norm 3, wgate 4, wup 5, wdown 6}. Gemma-4 adds ple_embed 4, ple_proj 5,
+ * ple_norm 6 and per layer {q_norm 7, k_norm 8, post_attn_norm 9,
+ * post_ffn_norm 10, ple_gate 11, ple_out 12, post_ple_norm 13}; its norm
+ * weights are 1 + the generated value (fp32 sum), as they multiply unshifted.
+ * Synchronises. */
 int mxd_engine_init_random(mxd_engine* e, uint64_t seed, float stddev);
 /* Refills one tensor with mxd_fill_normal(seed, its tensor id, stddev), e.g.
  * the embedding at its own scale. Synchronises. Like init_random, it stands in

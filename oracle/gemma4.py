@@ -13,7 +13,7 @@ pairs, layer_scalar), and the operators:
   qkv_norm_rope    per-head RMSNorm of q, k (weights) and v (none), RoPE on
                    the first rope_pairs pairs, k, v to the cache     :246-304
   attention        scale 1, sliding layers over keys (pos - window, pos]
-                                                                     :317-399
+                                                                     :306-393
   LM head          tied embedding; logits 30 tanh(logits / 30) only where
                    they are dumped (KG/main.swift:657-662), argmax unchanged
 RMSNorm multiplies by w (not 1 + w); the embedding is scaled by sqrt(D), the
@@ -154,12 +154,17 @@ def weight_shapes(cfg: G4Config) -> dict[str, tuple[tuple[int, ...], type]]:
     return s
 
 
-def make_weights(cfg: G4Config, seed: int, std: float = 0.02) -> dict[str, np.ndarray]:
+def make_weights(cfg: G4Config, seed: int, std: float = 0.02, qk_norm_scale: float = 1.0) -> dict[str, np.ndarray]:
+    """qk_norm_scale multiplies the q_norm / k_norm weights (an fp32 product):
+    below 1 it softens the attention (scale 1 over unit-RMS q and k), which
+    keeps small test models well conditioned under fp16 K/V."""
     w = {}
     for name, (shape, dt) in weight_shapes(cfg).items():
         v = hashrng.normal(shape, dt, seed, tensor_id(name), std)
         kind = name.split(".")[-1]
         w[name] = (v + F32(1.0)).astype(F32) if kind in NORMS else v
+        if kind in ("q_norm", "k_norm") and qk_norm_scale != 1.0:
+            w[name] = (w[name] * F32(qk_norm_scale)).astype(F32)
     return w
 
 

@@ -1,0 +1,282 @@
+"""Gemma-4 on the GPU against the oracle (oracle/gemma4.py, itself pinned to
+transformers' Gemma4ForCausalLM): the new operators one by one (sandwich-norm
+residual add, per-layer-embedding combine, per-head q/k/v norm + partial RoPE +
+append, sliding-window attention and head_dim 512), then the engine on the tiny
+Gemma-4 config (every feature of the reference's E2B engine at small size):
+synthetic weights bit for bit, softcapped logits at every position, greedy
+tokens equal to transformers' (tests/golden/hf_gemma4_tiny.npz), and the
+graph-replayed decode equal to eager steps.
+
+Tolerances: operators max|got - ref| / max|ref| <= 1e-4 (fp32 math; attention
+1e-3 through its fp16 matrix-core split); the contract is 1e-2. Engine logits
+<= 2e-3: the GPU and the oracle store the same fp16 K/V, but fp32 rounding
+differences of ~1e-7 flip single fp16 roundings, and the model passes such
+flips on to the logits the way storing K/V in fp16 at all does, which moves
+the fixture model's logits by at most 6.3e-4 (oracle with fp16 against fp64
+K/V over the fixture's 31 positions). The fixture's q/k norm weights are
+scaled by 0.25 for that conditioning (with weight 1, unit-RMS q and k at
+attention scale 1 give near one-hot softmaxes and a 1.1e-2 sensitivity).
+Token ids are exact: the fixture's greedy margins exceed 2% of the largest
+logit. Cache bits are exact.
+"""
+
+from __future__ import annotations
+
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemma4 as g4
+from oracle import ops as ref
+from tests.conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "hf_gemma4_tiny.npz"
+TOL_CONTRACT = 1e-2
+
+
+def _ops():
+    from gemmagemini4hackathon2026_10_2425_amd import ops
+
+    return ops
+
+
+def _close(got, want, tol):
+    e = rel_err(got, want)
+    assert e <= TOL_CONTRACT, f"relative error {e:.3e} above the 1e-2 contract"
+    assert e <= tol, f"relative error {e:.3e} above the expected {tol:.0e}"
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+# ---------------------------------------------------------------- operators
+
+
+@pytest.mark.parametrize("rows,D", [(1, 256), (3, 1536), (2, 100)])
+@pytest.mark.parametrize("post", [1.0, 0.7])
+def test_rmsnorm_add(dev, rng, rows, D, post):
+    src = rng.standard_normal((rows, D), dtype=np.float32) * 3
+    x = rng.standard_normal((rows, D), dtype=np.float32)
+    w = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    got = _ops().rmsnorm_add(_t(src, dev), _t(w, dev), _t(x, dev), 1e-6, post).cpu().numpy()
+    want = (x.astype(np.float64) + g4.rmsnorm_w(src, w, 1e-6)) * post
+    _close(got, want, 1e-6)
+
+
+@pytest.mark.parametrize("rows,L,P,D", [(1, 6, 32, 256), (2, 35, 256, 1536)])
+def test_ple_combine(dev, rng, rows, L, P, D):
+    proj = rng.standard_normal((rows, L * P), dtype=np.float32) * 5
+    ple = rng.standard_normal((rows, L * P), dtype=np.float32)
+    w = (1 + 0.1 * rng.standard_normal(P)).astype(np.float32)
+    got = _ops().ple_combine(_t(proj, dev), _t(ple, dev), _t(w, dev), L, D, 1e-6).cpu().numpy()
+    p = proj.reshape(rows, L, P).astype(np.float64) * np.float32(D ** -0.5)
+    want = (g4.rmsnorm_w(p, w, 1e-6) + ple.reshape(rows, L, P)) * 2 ** -0.5
+    _close(got.reshape(rows, L, P), want, 1e-6)
+
+
+def _tile_rows(tiles, pos, which):
+    """Cache rows [n_kv, hd] at position pos of the tiled layout."""
+    ops = _ops()
+    n_kv, ctx, hd = tiles.shape
+    off = ops.tile_offsets(ctx, hd, which)[pos]
+    return tiles.reshape(n_kv, -1)[:, off]
+
+
+@pytest.mark.parametrize("nh,nkv,hd,pairs", [(8, 1, 256, 128), (8, 1, 512, 64), (4, 1, 64, 32), (4, 2, 128, 16),
+                                             (8, 0, 512, 64), (4, 0, 64, 32)])
+@pytest.mark.parametrize("pos", [0, 17, 1023])
+def test_qk_norm_rope_kv(dev, rng, nh, nkv, hd, pairs, pos):
+    ops = _ops()
+    max_ctx = 1024
+    qkv = rng.standard_normal((nh + 2 * nkv) * hd, dtype=np.float32) * 2
+    qw = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    kw = (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+    i = np.arange(hd // 2, dtype=np.float64)
+    invf = np.where(i < pairs, 1.0 / 1e6 ** (2 * i / hd), 0.0).astype(np.float32)
+    qkv_d = _t(qkv, dev)
+    if nkv:
+        kd = torch.zeros((nkv, max_ctx, hd), dtype=torch.float16, device=dev)
+        vd = torch.zeros_like(kd)
+        ops.qk_norm_rope_kv(qkv_d, kd, vd, _t(qw, dev), _t(kw, dev), _t(invf, dev), nh, pairs, 1e-6, pos0=pos)
+    else:
+        ops.qk_norm_rope_kv(qkv_d, None, None, _t(qw, dev), None, _t(invf, dev), nh, pairs, 1e-6, pos0=pos,
+                            head_dim=hd)
+    heads = qkv.reshape(nh + 2 * nkv, hd)
+    q_want = np.stack([ref.rope(g4.rmsnorm_w(h, qw, 1e-6).astype(np.float32), pos, invf) for h in heads[:nh]])
+    got = qkv_d.cpu().numpy().reshape(nh + 2 * nkv, hd)
+    _close(got[:nh], q_want, 1e-5)
+    if not nkv:
+        assert np.array_equal(got[nh:], heads[nh:])
+        return
+    k_want = np.stack([ref.rope(g4.rmsnorm_w(h, kw, 1e-6).astype(np.float32), pos, invf)
+                       for h in heads[nh:nh + nkv]]).astype(np.float16)
+    v_want = np.stack([g4.rmsnorm_w(h, None, 1e-6) for h in heads[nh + nkv:]]).astype(np.float32).astype(np.float16)
+    kg = _tile_rows(kd.cpu().numpy(), pos, "k").astype(np.float64)
+    vg = _tile_rows(vd.cpu().numpy(), pos, "v").astype(np.float64)
+    # fp16 of fp32 values: one fp16 ulp for the sin/cos and rsqrt rounding
+    for g, w in ((kg, k_want), (vg, v_want)):
+        w = w.astype(np.float64)
+        assert np.max(np.abs(g - w) / np.maximum(np.abs(w), 6e-5)) <= 2 ** -10
+    assert np.count_nonzero(kd.cpu().numpy()) == np.count_nonzero(k_want)
+
+
+def _attn_case(rng, nh, nkv, hd, L, max_ctx):
+    q = rng.standard_normal(nh * hd, dtype=np.float32) / math.sqrt(hd) * 4
+    kc = np.zeros((nkv, max_ctx, hd), np.float16)
+    vc = np.zeros((nkv, max_ctx, hd), np.float16)
+    kc[:, :L] = rng.standard_normal((nkv, L, hd), dtype=np.float32).astype(np.float16)
+    vc[:, :L] = rng.standard_normal((nkv, L, hd), dtype=np.float32).astype(np.float16)
+    return q, kc, vc
+
+
+def _window_ref(q, kc, vc, L, nh, window, scale=1.0):
+    start = max(0, L - window) if window else 0
+    return ref.attention(q, kc[:, start:L], vc[:, start:L], L - start, nh, scale)
+
+
+@pytest.mark.parametrize("nh,nkv,hd", [(8, 1, 256), (8, 1, 512), (4, 1, 64), (8, 2, 128)])
+@pytest.mark.parametrize("L,window", [(1, 16), (16, 16), (17, 16), (40, 16), (600, 512), (1000, 512),
+                                      (4096, 512), (3000, 0), (33, 0)])
+def test_attention_window(dev, rng, nh, nkv, hd, L, window):
+    ops = _ops()
+    max_ctx = max(64, (L + 31) // 32 * 32)
+    q, kc, vc = _attn_case(rng, nh, nkv, hd, L, max_ctx)
+    qd, kd, vd = _t(q, dev), _t(ops.to_tiles(kc, "k"), dev), _t(ops.to_tiles(vc, "v"), dev)
+    out = ops.attention(qd, kd, vd, L, nh, scale=1.0, window=window)
+    _close(out.cpu().numpy(), _window_ref(q, kc, vc, L, nh, window), 1e-3)
+    # the position read on the device gives the same keys
+    pos = torch.tensor([L - 1], dtype=torch.int32, device=dev)
+    out2 = ops.attention(qd, kd, vd, 0, nh, scale=1.0, window=window, pos_dev=pos)
+    assert torch.equal(out, out2)
+
+
+def test_attention_window_ignores_keys_before_start(dev, rng):
+    """Keys before the window start hold NaN/inf garbage; they must not leak in."""
+    ops = _ops()
+    nh, nkv, hd, L, window, max_ctx = 8, 1, 256, 100, 40, 128
+    q, kc, vc = _attn_case(rng, nh, nkv, hd, L, max_ctx)
+    kg, vg = kc.copy(), vc.copy()
+    kg[:, : L - window] = np.float16(np.nan)
+    vg[:, : L - window] = np.float16(np.inf)
+    out = ops.attention(_t(q, dev), _t(ops.to_tiles(kg, "k"), dev), _t(ops.to_tiles(vg, "v"), dev), L, nh,
+                        scale=1.0, window=window)
+    _close(out.cpu().numpy(), _window_ref(q, kc, vc, L, nh, window), 1e-3)
+
+
+@pytest.mark.parametrize("hd,window", [(128, 16), (512, 0), (256, 48)])
+def test_attention_prefill_window(dev, rng, hd, window):
+    ops = _ops()
+    nh, nkv, pos0, rows, max_ctx = 4, 1, 37, 30, 128
+    L = pos0 + rows
+    q_rows = rng.standard_normal((rows, nh * hd), dtype=np.float32) / math.sqrt(hd) * 4
+    _, kc, vc = _attn_case(rng, nh, nkv, hd, L, max_ctx)
+    out = ops.attention_prefill(_t(q_rows, dev), _t(ops.to_tiles(kc, "k"), dev), _t(ops.to_tiles(vc, "v"), dev),
+                                pos0, nh, scale=1.0, window=window).cpu().numpy()
+    want = np.stack([_window_ref(q_rows[t], kc, vc, pos0 + t + 1, nh, window) for t in range(rows)])
+    _close(out, want, 1e-3)
+
+
+# ---------------------------------------------------------------- engine
+
+
+def _shape(cfg: g4.G4Config):
+    from gemmagemini4hackathon2026_10_2425_amd.engine import Gemma4Layer, Gemma4Shape
+
+    layers = tuple(Gemma4Layer(y.head_dim, y.ffn_dim, y.sliding, y.kv_layer, y.rope_pairs, y.rope_theta,
+                               y.layer_scalar) for y in cfg.layers)
+    return Gemma4Shape(cfg.dim, cfg.n_heads, 1, cfg.vocab, cfg.ple_dim, cfg.ple_vocab, cfg.window, layers, cfg.eps,
+                       cfg.softcap)
+
+
+def _engine(cfg, max_ctx, seed, qk_norm_scale=1.0):
+    """Engine with the synthetic weights; q/k norm weights scaled as the
+    oracle's make_weights(qk_norm_scale) does (uploaded from it)."""
+    from gemmagemini4hackathon2026_10_2425_amd.engine import Engine
+
+    e = Engine(_shape(cfg), max_ctx)
+    e.init_random(seed, 0.02)
+    if qk_norm_scale != 1.0:
+        w = g4.make_weights(cfg, seed, qk_norm_scale=qk_norm_scale)
+        for name in w:
+            if name.endswith(("q_norm", "k_norm")):
+                e.upload(name, w[name])
+    return e
+
+
+def _golden():
+    z = np.load(GOLDEN)
+    return z, int(z["seed"]), float(z["qk_norm_scale"]), z["prompt"].tolist(), z["greedy"].tolist()
+
+
+def test_gemma4_engine_weights_are_the_generator(dev):
+    cfg = g4.G4_TINY
+    want = g4.make_weights(cfg, 17)
+    with _engine(cfg, 64, 17) as e:
+        names = [n for n, _, _ in e.tensor_specs()]
+        assert sorted(names) == sorted(want)
+        for name, w in want.items():
+            got = e.download(name, w.dtype).reshape(w.shape)
+            assert np.array_equal(got.view(np.uint8), w.view(np.uint8)), name
+
+
+def test_gemma4_engine_matches_oracle_every_position(dev):
+    """Softcapped logits after every step of prompt + greedy continuation, the
+    positions past the sliding window (16) included."""
+    cfg = g4.G4_TINY
+    _, seed, qk, prompt, greedy = _golden()
+    oracle = g4.G4Decoder(cfg, g4.make_weights(cfg, seed, qk_norm_scale=qk), 64)
+    oracle.tokens[: len(prompt)] = prompt
+    with _engine(cfg, 64, seed, qk) as e:
+        e.set_tokens(prompt)
+        for pos in range(len(prompt) + len(greedy) - 1):
+            e.step(pos, sample=True)
+            raw = oracle.forward(pos)
+            _close(e.logits(), oracle.softcap(raw), 2e-3)
+            if pos >= len(prompt) - 1:
+                tok = ref.argmax(raw)
+                oracle.tokens[pos + 1] = tok
+                assert e.token(pos + 1) == tok, f"pos {pos}"
+            else:
+                e.set_tokens([prompt[pos + 1]], pos + 1)
+        assert e.tokens(len(prompt), len(greedy)) == greedy
+
+
+def test_gemma4_engine_generate_matches_transformers(dev):
+    """Prefill (token by token) then the graph-replayed decode: the greedy
+    tokens of transformers' Gemma4ForCausalLM."""
+    cfg = g4.G4_TINY
+    _, seed, qk, prompt, greedy = _golden()
+    with _engine(cfg, 64, seed, qk) as e:
+        assert e.generate(prompt, len(greedy)) == greedy
+
+
+def test_gemma4_engine_prefill_logits_match_transformers(dev):
+    """The last prompt position's softcapped logits against transformers (fp64,
+    K/V unrounded): the fp16 K/V cache bounds the difference."""
+    cfg = g4.G4_TINY
+    gold, seed, qk, prompt, _ = _golden()
+    with _engine(cfg, 64, seed, qk) as e:
+        e.set_tokens(prompt)
+        e.prefill(len(prompt))
+        _close(e.logits(), gold["logits"][-1], 2e-3)
+
+
+def test_gemma4_engine_decode_graph_equals_steps(dev):
+    cfg = g4.G4_TINY
+    prompt = [5, 17, 999, 3, 250]
+    with _engine(cfg, 64, 3, 0.25) as a, _engine(cfg, 64, 3, 0.25) as b:
+        a.set_tokens(prompt)
+        a.prefill(len(prompt))
+        a.decode(len(prompt), 40)
+        b.set_tokens(prompt)
+        b.prefill(len(prompt))
+        for pos in range(len(prompt), len(prompt) + 40):
+            b.step(pos)
+        b.sync()
+        assert a.tokens(len(prompt), 41) == b.tokens(len(prompt), 41)

@@ -528,7 +528,7 @@ def test_gemma4_matches_hf_gemma4():
     embeddings and layer scalars are all in the tiny config."""
     g4, z, prompt = _g4_golden()
     cfg = g4.G4_TINY
-    w = g4.make_weights(cfg, int(z["seed"]))
+    w = g4.make_weights(cfg, int(z["seed"]), qk_norm_scale=float(z["qk_norm_scale"]))
     d = g4.G4Decoder(cfg, w, 64, fp16_kv=False)
     d.tokens[: len(prompt)] = prompt
     for pos in range(len(prompt)):
@@ -537,7 +537,8 @@ def test_gemma4_matches_hf_gemma4():
         assert np.abs(lg - ref).max() / np.abs(ref).max() < 2e-5, pos
     toks, margins = g4.G4Decoder(cfg, w, 64).generate(prompt, len(z["greedy"]))
     assert toks == [int(t) for t in z["greedy"]]
-    assert len(set(toks)) == len(toks)  # a run that changes token every step
+    assert len(set(toks)) >= 9  # not a run stuck on one token
+    assert min(margins) > 0.01
 
 
 def test_gemma4_e2b_layer_facts():
