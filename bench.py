@@ -317,9 +317,21 @@ def ragged_layer_leg(steps: int, warmup: int, dev, n_seqs: int = 64) -> dict:
             "kv_tokens": int(lens.sum()), "tok_s": n_seqs / ms * 1e3, "gemm_tflops": flops / ms / 1e9}
 
 
+def _kv_bytes(shape, n_keys: float) -> float:
+    """fp16 K and V bytes one decode step reads at n_keys visible keys: every
+    layer's cache (Gemma-4: the layer it reads, the last `window` keys on a
+    sliding layer)."""
+    from gemmagemini4hackathon2026_10_2425_amd.engine import Gemma4Shape
+
+    if isinstance(shape, Gemma4Shape):
+        return sum(2 * 2 * shape.n_kv_heads * y.head_dim * (min(n_keys, shape.window) if y.sliding else n_keys)
+                   for y in shape.layers)
+    return 2 * 2 * shape.n_layers * shape.n_kv_heads * shape.head_dim * n_keys
+
+
 def decode_leg(n_new: int = 256, prompt_len: int = 128, reps: int = 3, max_ctx: int | None = None,
                model: str = "gemma2b", window: int = 0) -> dict:
-    """Greedy decode of the Gemma-2B (or Llama-3.2-1B) shape, timed like the
+    """Greedy decode of the Gemma-2B, Llama-3.2-1B or Gemma-4-E2B shape, timed like the
     reference's --bench-tg (KL/main.swift:605-618): wall clock over a run of
     pipelined steps that sample on the GPU, one host sync at the end. max_ctx
     defaults to the run's length (384); the serve binary's default is 4096,
@@ -328,9 +340,9 @@ def decode_leg(n_new: int = 256, prompt_len: int = 128, reps: int = 3, max_ctx: 
     uses (window steps in flight, the host waiting for each token)."""
     import numpy as np
 
-    from gemmagemini4hackathon2026_10_2425_amd.engine import GEMMA_2B, LLAMA32_1B, Engine
+    from gemmagemini4hackathon2026_10_2425_amd.engine import GEMMA4_E2B, GEMMA_2B, LLAMA32_1B, Engine
 
-    shape = GEMMA_2B if model == "gemma2b" else LLAMA32_1B
+    shape = {"gemma2b": GEMMA_2B, "llama32_1b": LLAMA32_1B, "gemma4_e2b": GEMMA4_E2B}[model]
     max_ctx = max_ctx or (prompt_len + n_new + 31) // 32 * 32
     with Engine(shape, max_ctx) as e:
         e.init_random(1234)
@@ -348,8 +360,7 @@ def decode_leg(n_new: int = 256, prompt_len: int = 128, reps: int = 3, max_ctx: 
             rates.append((n_new - 1) / (time.perf_counter() - t0))
     rate = float(np.median(rates))
     # bytes per token: every weight once (a tied head is read twice: embed row + head) + the KV read
-    kv_avg = 2 * shape.n_layers * shape.n_kv_heads * shape.head_dim * 2 * (prompt_len + n_new / 2)
-    per_tok = shape.weight_bytes + kv_avg
+    per_tok = shape.weight_bytes + _kv_bytes(shape, prompt_len + n_new / 2)
     out = {"tok_s": rate, "ms_per_token": 1e3 / rate, "bytes_per_token": per_tok, "gbs": per_tok * rate / 1e9,
            "frac": per_tok * rate / 1e9 / PEAK_HBM_GBS, "roof_tok_s": PEAK_HBM_GBS * 1e9 / per_tok,
            "prompt": prompt_len, "generated": n_new, "max_ctx": max_ctx}
@@ -420,7 +431,8 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemv_f16",
                     choices=["gemv_f16", "gemv_q8", "gemv_size_fit", "attention", "decode", "decode_4096",
-                             "decode_streaming", "decode_llama32_1b", "prefill", "ragged_layer", "copy"])
+                             "decode_streaming", "decode_llama32_1b", "decode_gemma4_e2b", "prefill", "ragged_layer",
+                             "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-detail", action="store_true", help="skip the int8 / attention detail legs")
     args = ap.parse_args(argv)
@@ -448,6 +460,7 @@ def main(argv=None) -> int:
                 "decode_4096": lambda: decode_leg(max_ctx=4096),
                 "decode_streaming": lambda: decode_leg(max_ctx=4096, window=3),
                 "decode_llama32_1b": lambda: decode_leg(model="llama32_1b"),
+                "decode_gemma4_e2b": lambda: decode_leg(model="gemma4_e2b"),
                 "prefill": prefill_leg,
                 "ragged_layer": lambda: ragged_layer_leg(args.steps, args.warmup, dev),
                 "copy": lambda: copy_leg(args.steps, args.warmup, dev)}
@@ -476,6 +489,7 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
         log("Llama-3.2-1B decode leg")
         detail["decode_llama32_1b"] = decode_leg(model="llama32_1b")
+        detail["decode_gemma4_e2b"] = decode_leg(model="gemma4_e2b")
         torch.cuda.empty_cache()
         log("ragged batch leg")
         detail["ragged_layer_llama8b_64seq"] = ragged_layer_leg(args.steps, args.warmup, dev)

@@ -136,6 +136,7 @@ SIGNATURES: dict[str, tuple] = {
                                              c_int, c_float, P]),
     "mxd_rmsnorm_add": (c_int, [P, P, P, c_int, c_int, c_float, c_float, P]),
     "mxd_ple_combine": (c_int, [P, P, P, c_int, c_int, c_int, c_float, c_float, P]),
+    "mxd_ple_gate_act": (c_int, [P, P, P, c_int, c_int, c_int, P]),
     "mxd_qk_norm_rope_kv": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_float, c_int, c_int, P,
                                     P]),
     "mxd_argmax_workspace_size": (c_size_t, [c_int]),

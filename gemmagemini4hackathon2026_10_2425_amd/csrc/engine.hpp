@@ -108,7 +108,7 @@ struct mxd_engine {
     float* ple_norm = nullptr;
     float *tmp = nullptr, *ple = nullptr, *pleproj = nullptr, *pleg = nullptr;
     float *btmp = nullptr, *bple = nullptr, *bpleproj = nullptr, *bpleg = nullptr;
-    uint16_t *bh16 = nullptr, *bpleg16 = nullptr;
+    uint16_t* bpleg16 = nullptr;
 
     int qkv_dim() const { return (c.n_heads + 2 * c.n_kv_heads) * c.head_dim; }
     int q_dim() const { return c.n_heads * c.head_dim; }

@@ -165,7 +165,98 @@ int mxd_eng::g4_step(mxd_engine* e, int pos, int32_t* pos_dev, bool sample) {
                            pos_dev ? e->htokens_dev : nullptr);
 }
 
+namespace {
+
+// The batched prefill of tokens[pos0 .. pos0 + T) (encodePrefillChunk,
+// KG/main.swift:486-520): activations rounded to fp16 where the reference's
+// chunk rounds them (the products round fp32 rows as they load them), the
+// row-batched norms, q/k/v norm + RoPE + append and sliding-window causal
+// attention; with sample, the last row takes the decode path's LM head and
+// argmax into tokens[pos0 + T].
+int g4_prefill_chunk(mxd_engine* e, int pos0, int T, bool sample) {
+    const mxd_gemma4_config& c = e->g4;
+    hipStream_t s = e->stream;
+    mxd_stream_t ms = reinterpret_cast<mxd_stream_t>(s);
+    const int D = c.dim, NH = c.n_heads, NKV = c.n_kv_heads, P = c.ple_dim, L = c.n_layers, V = c.vocab;
+    const int LP = L * P;
+    const float eps = c.rms_eps;
+    void* ws = e->gm_ws;
+    const size_t wsb = e->gm_ws_bytes;
+    int rc;
+    if ((rc = mxd::embed_dev(e->embed, e->tokens, pos0, nullptr, T, e->bx, D, sqrtf((float)D), V, s))) return rc;
+    if ((rc = mxd::embed_dev(e->ple_embed, e->tokens, pos0, nullptr, T, e->bple, LP, sqrtf((float)P), c.ple_vocab, s)))
+        return rc;
+    if ((rc = mxd_gemm_f16(e->ple_proj, e->bx, MXD_F32, e->bpleproj, T, LP, D, MXD_EPI_STORE, ws, wsb, ms))) return rc;
+    if ((rc = mxd_ple_combine(e->bpleproj, e->bple, e->ple_norm, T, L, P, 1.0f / sqrtf((float)D), eps, ms))) return rc;
+    for (int l = 0; l < L; ++l) {
+        const mxd_gemma4_layer& y = e->g4l[l];
+        const LayerPtrs& Lp = e->L[l];
+        const int hd = y.head_dim, F = y.ffn_dim, QKV = g4_qkv_dim(e, l), QD = g4_q_dim(e, l);
+        const bool own = owns_kv(e, l);
+        if ((rc = mxd_rmsnorm(e->bx, Lp.attn_norm, e->bxn, MXD_F16, T, D, eps, 0, ms))) return rc;
+        if ((rc = mxd_gemm_f16(Lp.wqkv, e->bxn, MXD_F16, e->bqkv, T, QKV, D, MXD_EPI_STORE, ws, wsb, ms))) return rc;
+        if ((rc = mxd_qk_norm_rope_kv(e->bqkv, own ? Lp.kc : nullptr, own ? Lp.vc : nullptr, Lp.q_norm,
+                                      own ? Lp.k_norm : nullptr, e->invf + (size_t)l * G4_FREQS, NH, own ? NKV : 0,
+                                      hd, y.rope_pairs, e->max_ctx, eps, pos0, T, nullptr, ms)))
+            return rc;
+        if ((rc = mxd_attention_prefill_window(e->bqkv, QKV, Lp.kc, Lp.vc, e->batt, QD, NH, NKV, hd, e->max_ctx, pos0,
+                                               T, y.sliding ? c.window : 0, 1.0f, ms)))
+            return rc;
+        if ((rc = mxd_gemm_f16(Lp.wo, e->batt, MXD_F32, e->btmp, T, D, QD, MXD_EPI_STORE, ws, wsb, ms))) return rc;
+        if ((rc = mxd_rmsnorm_add(e->btmp, Lp.post_attn_norm, e->bx, T, D, eps, 1.0f, ms))) return rc;
+        if ((rc = mxd_rmsnorm(e->bx, Lp.ffn_norm, e->bxn, MXD_F16, T, D, eps, 0, ms))) return rc;
+        if ((rc = mxd_gemm_gate_up_f16(Lp.wgate, Lp.wup, e->bxn, e->bh, T, F, D, MXD_ACT_GELU_TANH, ws, wsb, ms)))
+            return rc;
+        if ((rc = mxd_gemm_f16(Lp.wdown, e->bh, MXD_F32, e->btmp, T, D, F, MXD_EPI_STORE, ws, wsb, ms))) return rc;
+        if ((rc = mxd_rmsnorm_add(e->btmp, Lp.post_ffn_norm, e->bx, T, D, eps, 1.0f, ms))) return rc;
+        // the gate reads the un-normalized residual, rounded to fp16 (KG/main.swift:507)
+        if ((rc = mxd_gemm_f16(Lp.ple_gate, e->bx, MXD_F32, e->bpleg, T, P, D, MXD_EPI_STORE, ws, wsb, ms))) return rc;
+        if ((rc = mxd_ple_gate_act(e->bpleg, e->bple + (size_t)l * P, e->bpleg16, T, P, LP, ms))) return rc;
+        if ((rc = mxd_gemm_f16(Lp.ple_out, e->bpleg16, MXD_F16, e->btmp, T, D, P, MXD_EPI_STORE, ws, wsb, ms)))
+            return rc;
+        if ((rc = mxd_rmsnorm_add(e->btmp, Lp.post_ple_norm, e->bx, T, D, eps, y.layer_scalar, ms))) return rc;
+    }
+    if (!sample) return MXD_OK;
+    // Only the last row needs logits: it takes the decode path's head.
+    HIP_OK(hipMemcpyAsync(e->x, e->bx + (size_t)(T - 1) * D, (size_t)D * 4, hipMemcpyDeviceToDevice, s),
+           "mxd_engine_prefill");
+    if ((rc = mxd_matvec_f16_rmsnorm(e->embed, e->x, e->final_norm, eps, 0, e->logits, V, D, MXD_EPI_STORE, nullptr,
+                                     ms)))
+        return rc;
+    return mxd::argmax_dev(e->logits, e->tokens, V, pos0 + T, nullptr, false, e->am_ws, s);
+}
+
+// Split-K workspace of the chunk products for any chunk of 1 .. rows rows.
+size_t g4_prefill_ws_bytes(const mxd_engine* e, int rows) {
+    const mxd_gemma4_config& c = e->g4;
+    const int D = c.dim, P = c.ple_dim, LP = c.n_layers * c.ple_dim;
+    size_t m = 0;
+    for (int T = 1; T <= rows; ++T) {
+        m = max(m, mxd_gemm_f16_workspace_size(T, LP, D));
+        m = max(m, mxd_gemm_f16_workspace_size(T, P, D));
+        m = max(m, mxd_gemm_f16_workspace_size(T, D, P));
+        for (int l = 0; l < c.n_layers; ++l) {
+            const int F = e->g4l[l].ffn_dim;
+            m = max(m, mxd_gemm_f16_workspace_size(T, g4_qkv_dim(e, l), D));
+            m = max(m, mxd_gemm_f16_workspace_size(T, D, g4_q_dim(e, l)));
+            m = max(m, mxd_gemm_gate_up_f16_workspace_size(T, F, D));
+            m = max(m, mxd_gemm_f16_workspace_size(T, D, F));
+        }
+    }
+    return m;
+}
+
+}  // namespace
+
 int mxd_eng::g4_prefill(mxd_engine* e, int n) {
+    if (n > 1 && mxd::tunable("ENG_NO_GEMM", 0) != 1) {
+        for (int done = 0; done < n;) {
+            const int rows = min(e->max_rows, n - done);
+            if (int rc = g4_prefill_chunk(e, done, rows, done + rows == n)) return rc;
+            done += rows;
+        }
+        return MXD_OK;
+    }
     // Token by token through the decode step (the reference's --no-gemm
     // prefill, KG/main.swift:440-445).
     for (int p = 0; p < n; ++p)
@@ -214,6 +305,13 @@ extern "C" int mxd_engine_create_gemma4(const mxd_gemma4_config* cfg, int max_ct
     const size_t o_ple = take(LP * 4), o_pleproj = take(LP * 4), o_pleg = take(P * 4);
     const size_t o_invf = take((size_t)L * G4_FREQS * 4), o_tok = take(((size_t)max_ctx + 1) * 4), o_pos = take(4);
     const size_t o_aws = take(e->attn_ws_bytes), o_am = take(mxd_argmax_workspace_size(c.vocab)), o_step = take(4);
+    // prefill chunk buffers
+    const size_t B = (size_t)(e->max_rows = min(PREFILL_ROWS, max_ctx));
+    e->gm_ws_bytes = g4_prefill_ws_bytes(e, e->max_rows);
+    const size_t o_bx = take(B * D * 4), o_bxn = take(B * D * 2), o_bqkv = take(B * max_qkv * 4);
+    const size_t o_batt = take(B * max_q * 4), o_bh = take(B * max_f * 4), o_btmp = take(B * D * 4);
+    const size_t o_bple = take(B * LP * 4), o_bpleproj = take(B * LP * 4), o_bpleg = take(B * P * 4);
+    const size_t o_bpleg16 = take(B * P * 2), o_gws = take(max(e->gm_ws_bytes, (size_t)16));
     std::vector<size_t> o_kc(L, 0), o_vc(L, 0);
     for (int l = 0; l < L; ++l) {
         if (!owns_kv(e, l)) continue;
@@ -240,6 +338,17 @@ extern "C" int mxd_engine_create_gemma4(const mxd_gemma4_config* cfg, int max_ct
     e->attn_ws = a + o_aws;
     e->am_ws = a + o_am;
     e->step = reinterpret_cast<int32_t*>(a + o_step);
+    e->bx = reinterpret_cast<float*>(a + o_bx);
+    e->bxn = reinterpret_cast<uint16_t*>(a + o_bxn);
+    e->bqkv = reinterpret_cast<float*>(a + o_bqkv);
+    e->batt = reinterpret_cast<float*>(a + o_batt);
+    e->bh = reinterpret_cast<float*>(a + o_bh);
+    e->btmp = reinterpret_cast<float*>(a + o_btmp);
+    e->bple = reinterpret_cast<float*>(a + o_bple);
+    e->bpleproj = reinterpret_cast<float*>(a + o_bpleproj);
+    e->bpleg = reinterpret_cast<float*>(a + o_bpleg);
+    e->bpleg16 = reinterpret_cast<uint16_t*>(a + o_bpleg16);
+    e->gm_ws = a + o_gws;
     e->embed = wptr<uint16_t>(e, "embed");
     e->head = e->embed;
     e->final_norm = wptr<float>(e, "final_norm");

@@ -270,6 +270,15 @@ qk_norm_rope_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kcache, uint
     }
 }
 
+// Prefill's per-layer-embedding gate activation (KG/kernels.metal:451-461):
+// dst[t][i] = fp16(gelu_tanh(src[t][i]) * ple[t * ple_stride + i]), i < P.
+__global__ void __launch_bounds__(256) ple_gate_act_kernel(const float* __restrict__ src, const float* __restrict__ ple,
+                                                           uint16_t* __restrict__ dst, int P, int ple_stride) {
+    const int t = blockIdx.y, i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= P) return;
+    dst[(size_t)t * P + i] = mxd::f2h_bits(mxd::gelu_tanh(src[(size_t)t * P + i]) * ple[(size_t)t * ple_stride + i]);
+}
+
 }  // namespace
 
 namespace mxd {
@@ -406,4 +415,14 @@ extern "C" int mxd_qk_norm_rope_kv(float* qkv, uint16_t* kcache, uint16_t* vcach
                        mxd::as_stream(stream), qkv, kcache, vcache, q_w, k_w, inv_freq, n_heads, n_kv_heads, head_dim,
                        rope_pairs, max_ctx, eps, pos0, pos_dev);
     return mxd::check_launch("mxd_qk_norm_rope_kv");
+}
+
+extern "C" int mxd_ple_gate_act(const float* src, const float* ple, uint16_t* dst, int rows, int P, int ple_stride,
+                                mxd_stream_t stream) {
+    MXD_REQUIRE(src && ple && dst, MXD_ERR_INVALID_ARG, "mxd_ple_gate_act: null pointer");
+    MXD_REQUIRE(rows > 0 && P > 0 && ple_stride >= P, MXD_ERR_INVALID_ARG,
+                "mxd_ple_gate_act: rows=%d P=%d ple_stride=%d", rows, P, ple_stride);
+    hipLaunchKernelGGL(ple_gate_act_kernel, dim3((P + 255) / 256, rows), dim3(256), 0, mxd::as_stream(stream), src, ple,
+                       dst, P, ple_stride);
+    return mxd::check_launch("mxd_ple_gate_act");
 }

@@ -13,10 +13,18 @@ Tensor names (KL/convert_weights.py:56-69): embed, l<i>.attn_norm, l<i>.wqkv
 final_norm, and lm_head when the head is not tied. Norm weights are fp32,
 everything else fp16.
 
+A Gemma-4 file (KG/convert_weights.py:1-15) has the same layout; its header
+adds "engine": {"layers": [{head_dim, ffn_dim, sliding, kv_layer, rope_theta,
+rope_pairs, layer_scalar}]}, "config" is the checkpoint's text config, and the
+tensors are embed, ple_embed, ple_proj, ple_norm, per layer attn_norm, wqkv
+(q only on KV-shared layers), q_norm, k_norm (own K/V only), wo,
+post_attn_norm, ffn_norm, wgate, wup, wdown, post_ffn_norm, ple_gate,
+ple_out, post_ple_norm, and final_norm.
+
 The engine covers Gemma-1/2B-style and Llama-style decoders (Llama-3.2-1B
 included) with a tied or untied LM head, head_dim 64, 128 or 256, and plain or
-Llama-3-scaled RoPE; a file outside that raises ValueError naming what is
-unsupported.
+Llama-3-scaled RoPE, and Gemma-4 (E2B-style) text models; a file outside that
+raises ValueError naming what is unsupported.
 """
 
 from __future__ import annotations
@@ -28,7 +36,7 @@ from pathlib import Path
 
 import numpy as np
 
-from .engine import Engine, ModelShape
+from .engine import Engine, Gemma4Layer, Gemma4Shape, ModelShape
 
 ALIGN = 256
 PAGE = 16384
@@ -40,9 +48,10 @@ _LAYER_KINDS = ("attn_norm", "wqkv", "wo", "ffn_norm", "wgate", "wup", "wdown")
 # ---------------------------------------------------------------- file format
 
 
-def write_bin(path: str | os.PathLike, config: dict, tensors: dict[str, np.ndarray]) -> int:
+def write_bin(path: str | os.PathLike, config: dict, tensors: dict[str, np.ndarray], engine: dict | None = None) -> int:
     """Write `tensors` (name -> fp16/fp32 array, in the given order) and the
-    model config in the flat format. Returns the file size in bytes."""
+    model config (and a Gemma-4 file's "engine" facts) in the flat format.
+    Returns the file size in bytes."""
     arrays = []
     for name, arr in tensors.items():
         a = np.ascontiguousarray(arr)
@@ -56,7 +65,10 @@ def write_bin(path: str | os.PathLike, config: dict, tensors: dict[str, np.ndarr
             off = (off + ALIGN - 1) // ALIGN * ALIGN
             meta[name] = {"offset": off, "shape": list(a.shape), "dtype": str(a.dtype)}
             off += a.nbytes
-        header = json.dumps({"config": config, "tensors": meta}).encode()
+        head = {"config": config, "tensors": meta}
+        if engine is not None:
+            head = {"config": config, "engine": engine, "tensors": meta}
+        header = json.dumps(head).encode()
         if 8 + len(header) <= start:
             break
         start = (8 + len(header) + ALIGN - 1) // ALIGN * ALIGN
@@ -73,6 +85,12 @@ def write_bin(path: str | os.PathLike, config: dict, tensors: dict[str, np.ndarr
 
 def read_bin(path: str | os.PathLike) -> tuple[dict, dict[str, np.ndarray]]:
     """(config, {name: read-only array over a memory map of the file})."""
+    header, tensors = read_bin_full(path)
+    return header["config"], tensors
+
+
+def read_bin_full(path: str | os.PathLike) -> tuple[dict, dict[str, np.ndarray]]:
+    """(the whole JSON header, {name: read-only array over a memory map})."""
     size = os.path.getsize(path)
     with open(path, "rb") as f:
         head = f.read(8)
@@ -95,7 +113,7 @@ def read_bin(path: str | os.PathLike) -> tuple[dict, dict[str, np.ndarray]]:
         if off < 8 + hlen or off + nb > size:
             raise ValueError(f"{path}: tensor {name} [{off}, {off + nb}) lies outside the data region")
         tensors[name] = mm[off : off + nb].view(dt).reshape(shape)
-    return header["config"], tensors
+    return header, tensors
 
 
 # ---------------------------------------------------------------- config
@@ -156,15 +174,60 @@ def tensor_names(n_layers: int, tied: bool = True) -> list[str]:
     return names if tied else names + ["lm_head"]
 
 
+def is_gemma4(config: dict) -> bool:
+    """A Gemma-4 config: model_type gemma4 / gemma4_text, or a text_config of one."""
+    mt = str(config.get("model_type", ""))
+    return mt.startswith("gemma4") or str((config.get("text_config") or {}).get("model_type", "")).startswith("gemma4")
+
+
+def gemma4_shape(config: dict, engine: dict | None = None) -> Gemma4Shape:
+    """Gemma4Shape of a text config; the per-layer facts from a file's "engine"
+    header when given (KG/main.swift:86-101), else resolved from the config
+    (layer scalars 1)."""
+    text = config.get("text_config", config)
+    layers = None
+    if engine is not None:
+        try:
+            layers = tuple(Gemma4Layer(int(y["head_dim"]), int(y["ffn_dim"]), bool(y["sliding"]), int(y["kv_layer"]),
+                                       int(y["rope_pairs"]), float(y["rope_theta"]),
+                                       float(y.get("layer_scalar", 1.0))) for y in engine["layers"])
+        except (KeyError, TypeError) as err:
+            raise ValueError(f"engine header: bad layer entry ({err})") from None
+        if len(layers) != int(text["num_hidden_layers"]):
+            raise ValueError(f"engine header has {len(layers)} layers for num_hidden_layers "
+                             f"{text['num_hidden_layers']}")
+    return Gemma4Shape.from_hf(text, layers)
+
+
+def gemma4_tensor_names(shape: Gemma4Shape) -> list[str]:
+    """Tensor names of a Gemma-4 file, in the reference converter's order
+    (KG/convert_weights.py:98-121)."""
+    names = ["embed", "ple_embed", "ple_proj", "ple_norm"]
+    for i, y in enumerate(shape.layers):
+        own = y.kv_layer == i
+        names += [f"l{i}.{k}" for k in ("attn_norm", "wqkv", "q_norm") + (("k_norm",) if own else ()) +
+                  ("wo", "post_attn_norm", "ffn_norm", "wgate", "wup", "wdown", "post_ffn_norm", "ple_gate",
+                   "ple_out", "post_ple_norm")]
+    return names + ["final_norm"]
+
+
 # ---------------------------------------------------------------- engine
 
 
 def load_engine(path: str | os.PathLike, max_ctx: int = 4096) -> Engine:
     """An Engine holding the file's weights (every tensor checked for name,
     dtype and size before the first upload)."""
-    config, tensors = read_bin(path)
-    shape = shape_from_config(config)
-    extra = sorted(set(tensors) - set(tensor_names(shape.n_layers, shape.tie_embeddings)))
+    header, tensors = read_bin_full(path)
+    config = header["config"]
+    if "engine" in header or is_gemma4(config):
+        if "engine" not in header:
+            raise ValueError(f"{path}: a Gemma-4 file needs the 'engine' header (KG/convert_weights.py)")
+        shape = gemma4_shape(config, header["engine"])
+        names = gemma4_tensor_names(shape)
+    else:
+        shape = shape_from_config(config)
+        names = tensor_names(shape.n_layers, shape.tie_embeddings)
+    extra = sorted(set(tensors) - set(names))
     if extra:
         raise ValueError(f"{path}: tensors the engine does not use: {', '.join(extra[:8])}")
     e = Engine(shape, max_ctx)
@@ -206,7 +269,9 @@ def convert_hf(src: str | os.PathLike, out: str | os.PathLike) -> int:
 
     src = Path(src)
     config = json.loads((src / "config.json").read_text())
-    shape = shape_from_config(config)  # reject what the engine cannot run before converting
+    gemma4 = is_gemma4(config)
+    # reject what the engine cannot run before converting
+    shape = gemma4_shape(config) if gemma4 else shape_from_config(config)
     files = sorted(src.glob("*.safetensors"))
     if not files:
         raise FileNotFoundError(f"no *.safetensors in {src}")
@@ -228,6 +293,8 @@ def convert_hf(src: str | os.PathLike, out: str | os.PathLike) -> int:
             raise ValueError(f"{name} overflows fp16 (max |w| = {m})")
         return a.astype(np.float16)
 
+    if gemma4:
+        return _convert_gemma4(config, shape, where, get, f16, out)
     out_t: dict[str, np.ndarray] = {"embed": f16("embed", get("model.embed_tokens.weight"))}
     for i in range(int(config["num_hidden_layers"])):
         p = f"model.layers.{i}."
@@ -243,6 +310,50 @@ def convert_hf(src: str | os.PathLike, out: str | os.PathLike) -> int:
     if not shape.tie_embeddings:
         out_t["lm_head"] = f16("lm_head", get("lm_head.weight"))
     return write_bin(out, config, out_t)
+
+
+def _convert_gemma4(config: dict, shape: Gemma4Shape, where: dict, get, f16, out) -> int:
+    """The text model of a Gemma-4 checkpoint as KG/convert_weights.py:73-144
+    writes it: the per-layer facts in the "engine" header (layer_scalar read
+    from the checkpoint), q|k|v fused (q only on KV-shared layers), norms fp32,
+    the rest fp16. Tensors live under model.language_model. (the multimodal
+    checkpoint) or model. (a text-only one)."""
+    text = config.get("text_config", config)
+    if not text.get("tie_word_embeddings", True):
+        raise ValueError("the Gemma-4 LM head is the tied embedding (tie_word_embeddings false is not supported)")
+    pre = "model.language_model." if "model.language_model.embed_tokens.weight" in where else "model."
+    f32 = lambda name: get(pre + name).astype(np.float32)  # noqa: E731
+    out_t: dict[str, np.ndarray] = {
+        "embed": f16("embed", get(pre + "embed_tokens.weight")),
+        "ple_embed": f16("ple_embed", get(pre + "embed_tokens_per_layer.weight")),
+        "ple_proj": f16("ple_proj", get(pre + "per_layer_model_projection.weight")),
+        "ple_norm": f32("per_layer_projection_norm.weight"),
+    }
+    layers = []
+    for i, y in enumerate(shape.layers):
+        p = f"layers.{i}."
+        own = y.kv_layer == i
+        scalar = float(get(pre + p + "layer_scalar").reshape(-1)[0])
+        layers.append({"head_dim": y.head_dim, "ffn_dim": y.ffn_dim, "sliding": y.sliding, "kv_layer": y.kv_layer,
+                       "rope_theta": y.rope_theta, "rope_pairs": y.rope_pairs, "layer_scalar": scalar})
+        out_t[f"l{i}.attn_norm"] = f32(p + "input_layernorm.weight")
+        qkv = [get(pre + p + f"self_attn.{n}_proj.weight") for n in ("qkv" if own else "q")]
+        out_t[f"l{i}.wqkv"] = f16(f"l{i}.wqkv", np.concatenate(qkv, axis=0))
+        out_t[f"l{i}.q_norm"] = f32(p + "self_attn.q_norm.weight")
+        if own:
+            out_t[f"l{i}.k_norm"] = f32(p + "self_attn.k_norm.weight")
+        out_t[f"l{i}.wo"] = f16(f"l{i}.wo", get(pre + p + "self_attn.o_proj.weight"))
+        out_t[f"l{i}.post_attn_norm"] = f32(p + "post_attention_layernorm.weight")
+        out_t[f"l{i}.ffn_norm"] = f32(p + "pre_feedforward_layernorm.weight")
+        out_t[f"l{i}.wgate"] = f16(f"l{i}.wgate", get(pre + p + "mlp.gate_proj.weight"))
+        out_t[f"l{i}.wup"] = f16(f"l{i}.wup", get(pre + p + "mlp.up_proj.weight"))
+        out_t[f"l{i}.wdown"] = f16(f"l{i}.wdown", get(pre + p + "mlp.down_proj.weight"))
+        out_t[f"l{i}.post_ffn_norm"] = f32(p + "post_feedforward_layernorm.weight")
+        out_t[f"l{i}.ple_gate"] = f16(f"l{i}.ple_gate", get(pre + p + "per_layer_input_gate.weight"))
+        out_t[f"l{i}.ple_out"] = f16(f"l{i}.ple_out", get(pre + p + "per_layer_projection.weight"))
+        out_t[f"l{i}.post_ple_norm"] = f32(p + "post_per_layer_input_norm.weight")
+    out_t["final_norm"] = f32("norm.weight")
+    return write_bin(out, text, out_t, engine={"layers": layers})
 
 
 def main(argv=None) -> int:

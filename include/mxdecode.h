@@ -260,6 +260,13 @@ int mxd_rmsnorm_add(const float* src, const float* w, float* x, int rows, int D,
 int mxd_ple_combine(const float* proj, float* ple, const float* w, int rows, int n_layers, int P,
                     float proj_scale, float eps, mxd_stream_t stream);
 
+/* Prefill's gate activation of the per-layer inputs: dst[t][i] =
+ * fp16(gelu_tanh(src[t][i]) * ple[t * ple_stride + i]) for rows t, i < P (ple
+ * points at the layer's slice of the per-layer-input rows). Replaces
+ * ple_gate_act (KG/kernels.metal:451-461; host KG/main.swift:530-539). */
+int mxd_ple_gate_act(const float* src, const float* ple, uint16_t* dst, int rows, int P, int ple_stride,
+                     mxd_stream_t stream);
+
 /* qkv rows [q n_heads*hd | k n_kv_heads*hd | v n_kv_heads*hd] fp32 (row r at
  * position pos0 + r, or *pos_dev + r): per-head RMSNorm of q (weight q_w),
  * k (k_w) and v (no weight), HF rotate_half RoPE on q and k over the rotation
@@ -437,6 +444,10 @@ int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_engine** out
  * the layers that own them. mxd_engine_get_logits returns softcapped logits
  * (--dump-logits, KG/main.swift:657-662). */
 int mxd_engine_create_gemma4(const mxd_gemma4_config* cfg, int max_ctx, mxd_engine** out);
+/* (Its prefill runs chunks of up to 256 rows through the matrix-core
+ * * products as encodePrefillChunk does, KG/main.swift:486-520: activations
+ * rounded to fp16 before each product, the per-layer inputs' gate through
+ * mxd_ple_gate_act; ENG_NO_GEMM = 1 steps the decode path instead.) */
 int mxd_engine_destroy(mxd_engine* e);
 /* Weight tensors by index / name: "embed", "final_norm", "l<i>.attn_norm",
  * "l<i>.wqkv" (rows q|k|v), "l<i>.wo", "l<i>.ffn_norm", "l<i>.wgate",

@@ -168,6 +168,11 @@ def make_weights(cfg: G4Config, seed: int, std: float = 0.02, qk_norm_scale: flo
     return w
 
 
+def _h(v, half: bool):
+    """v rounded to fp16 (and back to fp32) when half, else unchanged."""
+    return np.asarray(v).astype(F16).astype(F32) if half else v
+
+
 def rmsnorm_w(x, w, eps):
     """x * rsqrt(mean(x^2) + eps) * w (w None: no weight), fp64."""
     x = np.asarray(x, dtype=F64)
@@ -189,26 +194,29 @@ class G4Decoder:
         self.invf = [cfg.inv_freq(l) for l in range(cfg.n_layers)]
         self.tokens = np.zeros(max_ctx + 1, np.int32)
 
-    def ple(self, tok: int, x: np.ndarray) -> np.ndarray:
+    def ple(self, tok: int, x: np.ndarray, half_acts: bool = False) -> np.ndarray:
         """Per-layer inputs [L, P] of a token (KG/main.swift:398-401, ple_combine
         KG/kernels.metal:132-149)."""
         c, w = self.cfg, self.w
         L, P = c.n_layers, c.ple_dim
         tok_part = (w["ple_embed"][tok].astype(F64) * F32(math.sqrt(P))).astype(F32).reshape(L, P)
-        proj = ops.matvec(w["ple_proj"], x).astype(F32).reshape(L, P)
+        proj = ops.matvec(w["ple_proj"], _h(x, half_acts)).astype(F32).reshape(L, P)
         normed = rmsnorm_w(proj.astype(F64) * F32(c.dim ** -0.5), w["ple_norm"], c.eps)
         return ((normed + tok_part.astype(F64)) * (2.0 ** -0.5)).astype(F32)
 
-    def forward(self, pos: int) -> np.ndarray:
-        """Logits (fp32, before the softcap) for tokens[pos] at position pos."""
+    def forward(self, pos: int, half_acts: bool = False) -> np.ndarray:
+        """Logits (fp32, before the softcap) for tokens[pos] at position pos.
+        half_acts: the activations that enter a product are rounded to fp16
+        first, as the reference's batched prefill chunk stores them
+        (xnHalf / attHalf / hidHalf / plegHalf, KG/main.swift:486-520)."""
         c, w = self.cfg, self.w
         D, NH = c.dim, c.n_heads
         tok = int(self.tokens[pos])
         x = ops.embed(w["embed"], tok, float(F32(math.sqrt(D)))).astype(F32)
-        ple = self.ple(tok, x)
+        ple = self.ple(tok, x, half_acts)
         for l, lay in enumerate(c.layers):
             hd, own = lay.head_dim, lay.kv_layer == l
-            xn = rmsnorm_w(x, w[f"l{l}.attn_norm"], c.eps).astype(F32)
+            xn = _h(rmsnorm_w(x, w[f"l{l}.attn_norm"], c.eps).astype(F32), half_acts)
             qkv = ops.matvec(w[f"l{l}.wqkv"], xn).astype(F32)
             q = rmsnorm_w(qkv[: NH * hd].reshape(NH, hd), w[f"l{l}.q_norm"], c.eps).astype(F32)
             q = ops.rope(q, pos, self.invf[l]).astype(F32)
@@ -220,13 +228,14 @@ class G4Decoder:
             kc, vc = self.k[lay.kv_layer], self.v[lay.kv_layer]
             att = ops.attention(q.reshape(-1), kc[None, start : pos + 1], vc[None, start : pos + 1], pos + 1 - start,
                                 NH, 1.0).astype(F32)
-            a = ops.matvec(w[f"l{l}.wo"], att)
+            a = ops.matvec(w[f"l{l}.wo"], _h(att, half_acts))
             x = (x.astype(F64) + rmsnorm_w(a.astype(F32), w[f"l{l}.post_attn_norm"], c.eps)).astype(F32)
-            xn = rmsnorm_w(x, w[f"l{l}.ffn_norm"], c.eps).astype(F32)
+            xn = _h(rmsnorm_w(x, w[f"l{l}.ffn_norm"], c.eps).astype(F32), half_acts)
             h = ops.gate_up(w[f"l{l}.wgate"], w[f"l{l}.wup"], xn, "gelu_tanh").astype(F32)
-            m = ops.matvec(w[f"l{l}.wdown"], h)
+            m = ops.matvec(w[f"l{l}.wdown"], _h(h, half_acts))
             x = (x.astype(F64) + rmsnorm_w(m.astype(F32), w[f"l{l}.post_ffn_norm"], c.eps)).astype(F32)
-            g = (ops.gelu_tanh(ops.matvec(w[f"l{l}.ple_gate"], x).astype(F32)) * ple[l]).astype(F32)
+            gi = ops.matvec(w[f"l{l}.ple_gate"], _h(x, half_acts)).astype(F32)
+            g = _h((ops.gelu_tanh(gi) * ple[l]).astype(F32), half_acts)
             p = ops.matvec(w[f"l{l}.ple_out"], g)
             x = ((x.astype(F64) + rmsnorm_w(p.astype(F32), w[f"l{l}.post_ple_norm"], c.eps)) * lay.layer_scalar
                  ).astype(F32)

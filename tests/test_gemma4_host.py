@@ -76,3 +76,61 @@ def test_engine_rejects_bad_layers():
         Engine(Gemma4Shape(base.dim, 3, 1, base.vocab, base.ple_dim, base.ple_vocab, base.window, L), 64)
     with pytest.raises(_lib.MxdValueError, match="max_ctx"):
         Engine(base, 48)
+
+
+def _g4_snapshot(d, cfg, w, multimodal: bool):
+    """A local HF checkpoint directory of the oracle's weights: a text-only
+    Gemma4ForCausalLM layout, or the multimodal one (text model under
+    model.language_model., config under text_config)."""
+    import json
+
+    import numpy as np
+    import torch
+    from safetensors.torch import save_file
+
+    from tests import gemma4_hf
+
+    text = gemma4_hf.text_config(cfg)
+    sd = gemma4_hf.hf_state(cfg, w, "model.language_model." if multimodal else "model.")
+    d.mkdir(parents=True, exist_ok=True)
+    save_file({k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in sd.items()}, str(d / "model.safetensors"))
+    config = {"model_type": "gemma4", "text_config": text} if multimodal else text
+    (d / "config.json").write_text(json.dumps(config))
+    return text
+
+
+@pytest.mark.parametrize("multimodal", [False, True])
+def test_convert_gemma4_checkpoint(tmp_path, multimodal):
+    """The converter writes the reference's Gemma-4 file (KG/convert_weights.py):
+    the text config, the resolved per-layer facts with the checkpoint's layer
+    scalars, and every tensor bit for bit; the loader reads the shape back."""
+    import numpy as np
+
+    from gemmagemini4hackathon2026_10_2425_amd import weights as W
+
+    cfg = g4.G4_TINY
+    w = g4.make_weights(cfg, 5)
+    text = _g4_snapshot(tmp_path / "snap", cfg, w, multimodal)
+    W.convert_hf(tmp_path / "snap", tmp_path / "g4.bin")
+    header, t = W.read_bin_full(tmp_path / "g4.bin")
+    assert header["config"] == text
+    assert [y["layer_scalar"] for y in header["engine"]["layers"]] == \
+           [float(np.float32(y.layer_scalar)) for y in cfg.layers]
+    shape = W.gemma4_shape(header["config"], header["engine"])
+    assert _layers_equal(shape.layers, cfg.layers)
+    assert [y.layer_scalar for y in shape.layers] == [float(np.float32(y.layer_scalar)) for y in cfg.layers]
+    assert list(t) == W.gemma4_tensor_names(shape)
+    assert sorted(t) == sorted(w)
+    for name, a in w.items():
+        assert t[name].dtype == a.dtype and np.array_equal(t[name].view(np.uint8), a.view(np.uint8)), name
+
+
+def test_gemma4_file_needs_engine_header(tmp_path):
+    import numpy as np
+
+    from gemmagemini4hackathon2026_10_2425_amd import weights as W
+    from tests import gemma4_hf
+
+    W.write_bin(tmp_path / "x.bin", gemma4_hf.text_config(g4.G4_TINY), {"embed": np.zeros((4, 4), np.float16)})
+    with pytest.raises(ValueError, match="engine"):
+        W.load_engine(tmp_path / "x.bin", 64)

@@ -541,6 +541,23 @@ def test_gemma4_matches_hf_gemma4():
     assert min(margins) > 0.01
 
 
+def test_gemma4_half_activation_prefill():
+    """The prefill mode (activations rounded to fp16 before each product, as
+    the reference's chunk stores them) stays within the 1e-2 contract of
+    transformers' fp64 logits, and does round: it moves the logits by more
+    than fp32 storage alone does."""
+    g4, z, prompt = _g4_golden()
+    cfg = g4.G4_TINY
+    w = g4.make_weights(cfg, int(z["seed"]), qk_norm_scale=float(z["qk_norm_scale"]))
+    d = g4.G4Decoder(cfg, w, 64, fp16_kv=False)
+    d.tokens[: len(prompt)] = prompt
+    errs = []
+    for pos in range(len(prompt)):
+        ref = z["logits"][pos]
+        errs.append(np.abs(d.softcap(d.forward(pos, half_acts=True)) - ref).max() / np.abs(ref).max())
+    assert max(errs) < 1e-2 and max(errs) > 1e-4
+
+
 def test_gemma4_e2b_layer_facts():
     """The E2B per-layer facts as the reference's converter resolves them
     (KG/convert_weights.py engine_config, KG/PLAN.md:25-44)."""
