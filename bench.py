@@ -199,6 +199,34 @@ def gemv_size_fit_leg(steps: int, warmup: int, dev) -> dict:
     }
 
 
+def launch_floor_leg(steps: int, warmup: int, dev) -> dict:
+    """The fixed cost of one kernel on this system, without HBM traffic:
+    graph-replayed back-to-back launches of a one-workgroup kernel
+    (mxd_f32_to_f16 of 256 values: one load and one store per thread), and of
+    the fp16 matvec with a single 4096-wide row (one workgroup, 8 KB of
+    weights: the matvec's own start-up, first HBM round trip and drain).
+    Per-launch period in the graph, and the same launches stream-ordered."""
+    import torch
+
+    from gemmagemini4hackathon2026_10_2425_amd import ops
+
+    cap = torch.cuda.Stream()
+    src = torch.zeros(256, dtype=torch.float32, device=dev)
+    dst = torch.empty(256, dtype=torch.float16, device=dev)
+    W = ops.fill_normal((1, 4096), torch.float16, 7, 400, 0.02, dev)
+    x = ops.fill_normal((4096,), torch.float16, 7, 401, 1.0, dev)
+    y = torch.empty(1, dtype=torch.float32, device=dev)
+    out = {}
+    for name, args in (("tiny_kernel", ("mxd_f32_to_f16", src.data_ptr(), dst.data_ptr(), 256)),
+                       ("matvec_1x4096", ("mxd_matvec_f16", W.data_ptr(), x.data_ptr(), 1, y.data_ptr(), 1, 4096, 0,
+                                          None))):
+        g = _bound(*args, cap.cuda_stream)
+        e = _bound(*args, _stream())
+        out[name] = {"graph_us": _graph_time(g, cap, steps * 10, warmup) * 1e3,
+                     "stream_us": _events_time(e, steps * 10, warmup) * 1e3}
+    return out
+
+
 def gemv_q8_leg(steps: int, warmup: int, dev) -> dict:
     import numpy as np
     import torch
@@ -430,7 +458,7 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="gemv_f16",
-                    choices=["gemv_f16", "gemv_q8", "gemv_size_fit", "attention", "decode", "decode_4096",
+                    choices=["gemv_f16", "gemv_q8", "gemv_size_fit", "launch_floor", "attention", "decode", "decode_4096",
                              "decode_streaming", "decode_llama32_1b", "decode_gemma4_e2b", "prefill", "ragged_layer",
                              "copy"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -454,6 +482,7 @@ def main(argv=None) -> int:
     detail = {}
     if args.workload != "gemv_f16":
         legs = {"gemv_q8": lambda: gemv_q8_leg(args.steps, args.warmup, dev),
+                "launch_floor": lambda: launch_floor_leg(args.steps, args.warmup, dev),
                 "gemv_size_fit": lambda: gemv_size_fit_leg(args.steps, args.warmup, dev),
                 "attention": lambda: attention_leg(args.steps, args.warmup, dev),
                 "decode": decode_leg,
@@ -472,6 +501,7 @@ def main(argv=None) -> int:
     if not args.no_detail:
         log("fp16 GEMV size fit leg")
         detail["gemv_f16_size_fit"] = gemv_size_fit_leg(args.steps, args.warmup, dev)
+        detail["launch_floor"] = launch_floor_leg(args.steps, args.warmup, dev)
         torch.cuda.empty_cache()
         log("int8 GEMV leg")
         detail["gemv_q8b32"] = gemv_q8_leg(args.steps, args.warmup, dev)
