@@ -107,6 +107,7 @@ struct mxd_engine {
     uint16_t *ple_embed = nullptr, *ple_proj = nullptr;
     float* ple_norm = nullptr;
     float *tmp = nullptr, *ple = nullptr, *pleproj = nullptr, *pleg = nullptr;
+    float* x2 = nullptr;  // the second residual buffer (x and x2 alternate)
     float *btmp = nullptr, *bple = nullptr, *bpleproj = nullptr, *bpleg = nullptr;
     uint16_t* bpleg16 = nullptr;
 

@@ -26,6 +26,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <utility>
+
 using namespace mxd_eng;
 
 namespace {
@@ -129,14 +131,43 @@ int mxd_eng::g4_step(mxd_engine* e, int pos, int32_t* pos_dev, bool sample) {
         return rc;
     if ((rc = mxd_matvec_f16(e->ple_proj, e->x, MXD_F32, e->pleproj, L * P, D, MXD_EPI_STORE, nullptr, ms))) return rc;
     if ((rc = mxd_ple_combine(e->pleproj, e->ple, e->ple_norm, 1, L, P, 1.0f / sqrtf((float)D), eps, ms))) return rc;
+    // Each sandwich norm's residual add, x = (x + rmsnorm(tmp) * w) * post, is
+    // folded into the product that reads x next (the *_residual entry
+    // points); the updated residual goes to the other of two buffers, since
+    // the product's other workgroups still read the current one. With
+    // ENG_G4_RESADD = 2 the adds run as their own launches instead.
+    const bool fold = mxd::tunable("ENG_G4_RESADD", 1) != 2;
+    float* xc = e->x;                 // the current residual
+    float* xo = e->x2;                // the other buffer
+    const float* pend_w = nullptr;    // a residual add pending on tmp (fold mode)
+    float pend_post = 1.0f;
+    // y (op)= W . [rmsnorm](x) after the pending add, if any.
+    auto product = [&](const uint16_t* W, const float* norm_w, float* y, int M, int K, int epi,
+                       const float* aux) -> int {
+        if (!pend_w) {
+            if (norm_w) return mxd_matvec_f16_rmsnorm(W, xc, norm_w, eps, 0, y, M, K, epi, aux, ms);
+            return mxd_matvec_f16(W, xc, MXD_F32, y, M, K, epi, aux, ms);
+        }
+        const int r = mxd_matvec_f16_residual(W, xc, e->tmp, pend_w, pend_post, xo, norm_w, eps, 0, y, M, K, epi, aux,
+                                              ms);
+        std::swap(xc, xo);
+        pend_w = nullptr;
+        return r;
+    };
+    auto residual_add = [&](const float* w, float post) -> int {
+        if (fold) {
+            pend_w = w;
+            pend_post = post;
+            return MXD_OK;
+        }
+        return mxd_rmsnorm_add(e->tmp, w, xc, 1, D, eps, post, ms);
+    };
     for (int l = 0; l < L; ++l) {
         const mxd_gemma4_layer& y = e->g4l[l];
         const LayerPtrs& Lp = e->L[l];
         const int hd = y.head_dim, F = y.ffn_dim;
         const bool own = owns_kv(e, l);
-        if ((rc = mxd_matvec_f16_rmsnorm(Lp.wqkv, e->x, Lp.attn_norm, eps, 0, e->qkv, g4_qkv_dim(e, l), D,
-                                         MXD_EPI_STORE, nullptr, ms)))
-            return rc;
+        if ((rc = product(Lp.wqkv, Lp.attn_norm, e->qkv, g4_qkv_dim(e, l), D, MXD_EPI_STORE, nullptr))) return rc;
         if ((rc = mxd_qk_norm_rope_kv(e->qkv, own ? Lp.kc : nullptr, own ? Lp.vc : nullptr, Lp.q_norm,
                                       own ? Lp.k_norm : nullptr, e->invf + (size_t)l * G4_FREQS, NH, own ? NKV : 0,
                                       hd, y.rope_pairs, e->max_ctx, eps, pos, 1, pos_dev, ms)))
@@ -145,22 +176,25 @@ int mxd_eng::g4_step(mxd_engine* e, int pos, int32_t* pos_dev, bool sample) {
                                        y.sliding ? c.window : 0, 1.0f, e->attn_ws, e->attn_ws_bytes, ms)))
             return rc;
         if ((rc = mxd_matvec_f16(Lp.wo, e->att, MXD_F32, e->tmp, D, NH * hd, MXD_EPI_STORE, nullptr, ms))) return rc;
-        if ((rc = mxd_rmsnorm_add(e->tmp, Lp.post_attn_norm, e->x, 1, D, eps, 1.0f, ms))) return rc;
-        if ((rc = mxd_gate_up_rmsnorm(Lp.wgate, Lp.wup, e->x, Lp.ffn_norm, eps, 0, e->h, F, D, MXD_ACT_GELU_TANH, ms)))
-            return rc;
+        if ((rc = residual_add(Lp.post_attn_norm, 1.0f))) return rc;
+        if (pend_w) {
+            rc = mxd_gate_up_residual(Lp.wgate, Lp.wup, xc, e->tmp, pend_w, pend_post, xo, Lp.ffn_norm, eps, 0, e->h,
+                                      F, D, MXD_ACT_GELU_TANH, ms);
+            std::swap(xc, xo);
+            pend_w = nullptr;
+        } else {
+            rc = mxd_gate_up_rmsnorm(Lp.wgate, Lp.wup, xc, Lp.ffn_norm, eps, 0, e->h, F, D, MXD_ACT_GELU_TANH, ms);
+        }
+        if (rc) return rc;
         if ((rc = mxd_matvec_f16(Lp.wdown, e->h, MXD_F32, e->tmp, D, F, MXD_EPI_STORE, nullptr, ms))) return rc;
-        if ((rc = mxd_rmsnorm_add(e->tmp, Lp.post_ffn_norm, e->x, 1, D, eps, 1.0f, ms))) return rc;
-        if ((rc = mxd_matvec_f16(Lp.ple_gate, e->x, MXD_F32, e->pleg, P, D, MXD_EPI_GELU_MUL, e->ple + (size_t)l * P,
-                                 ms)))
-            return rc;
+        if ((rc = residual_add(Lp.post_ffn_norm, 1.0f))) return rc;
+        if ((rc = product(Lp.ple_gate, nullptr, e->pleg, P, D, MXD_EPI_GELU_MUL, e->ple + (size_t)l * P))) return rc;
         if ((rc = mxd_matvec_f16(Lp.ple_out, e->pleg, MXD_F32, e->tmp, D, P, MXD_EPI_STORE, nullptr, ms))) return rc;
-        if ((rc = mxd_rmsnorm_add(e->tmp, Lp.post_ple_norm, e->x, 1, D, eps, y.layer_scalar, ms))) return rc;
+        if ((rc = residual_add(Lp.post_ple_norm, y.layer_scalar))) return rc;
     }
     if (!sample) return MXD_OK;
     // tied LM head; argmax on the raw logits (the softcap is monotonic, KG/main.swift:378-391)
-    if ((rc = mxd_matvec_f16_rmsnorm(e->embed, e->x, e->final_norm, eps, 0, e->logits, V, D, MXD_EPI_STORE, nullptr,
-                                     ms)))
-        return rc;
+    if ((rc = product(e->embed, e->final_norm, e->logits, V, D, MXD_EPI_STORE, nullptr))) return rc;
     return mxd::argmax_dev(e->logits, e->tokens, V, pos + 1, pos_dev, pos_dev != nullptr, e->am_ws, s,
                            pos_dev ? e->htokens_dev : nullptr);
 }
@@ -300,7 +334,7 @@ extern "C" int mxd_engine_create_gemma4(const mxd_gemma4_config* cfg, int max_ct
         off += align256(bytes);
         return o;
     };
-    const size_t o_x = take(D * 4), o_tmp = take(D * 4), o_qkv = take((size_t)max_qkv * 4);
+    const size_t o_x = take(D * 4), o_x2 = take(D * 4), o_tmp = take(D * 4), o_qkv = take((size_t)max_qkv * 4);
     const size_t o_att = take((size_t)max_q * 4), o_h = take((size_t)max_f * 4), o_logits = take((size_t)c.vocab * 4);
     const size_t o_ple = take(LP * 4), o_pleproj = take(LP * 4), o_pleg = take(P * 4);
     const size_t o_invf = take((size_t)L * G4_FREQS * 4), o_tok = take(((size_t)max_ctx + 1) * 4), o_pos = take(4);
@@ -324,6 +358,7 @@ extern "C" int mxd_engine_create_gemma4(const mxd_gemma4_config* cfg, int max_ct
 
     char* a = e->abase;
     e->x = reinterpret_cast<float*>(a + o_x);
+    e->x2 = reinterpret_cast<float*>(a + o_x2);
     e->tmp = reinterpret_cast<float*>(a + o_tmp);
     e->qkv = reinterpret_cast<float*>(a + o_qkv);
     e->att = reinterpret_cast<float*>(a + o_att);

@@ -22,6 +22,7 @@ namespace {
 // (gate, up).
 template <int WF, typename XT, int NMAT, int OP, int NR, int NW>
 __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
+    if constexpr (std::is_same<XT, float>::value && OP != EPI_ROPE_KV) residual_prologue<NW>(a);
     constexpr int EPL = WT<WF>::EPL;
     constexpr int CH = 64 * EPL;
     constexpr int U = (8 / (NR * NMAT)) > 0 ? (8 / (NR * NMAT)) : 1;
@@ -200,8 +201,12 @@ __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int RS_MAX_CHUNKS = 64;  // 16 waves x 4 chunks
 
+// Dynamic LDS of a launch: the residual prologue's x' (K floats).
+size_t dyn_lds(const GemvArgs& a) { return a.rsrc ? (size_t)a.K * sizeof(float) : 0; }
+
 template <int WF, typename XT, int NMAT, int OP, int NW, int RS_CPW>
 __global__ void __launch_bounds__(NW * 64) gemv_rows_kernel(GemvArgs a) {
+    if constexpr (std::is_same<XT, float>::value) residual_prologue<NW>(a);
     constexpr int EPL = WT<WF>::EPL;
     constexpr int CH = 64 * EPL;
     const int lane = threadIdx.x & 63;
@@ -298,12 +303,13 @@ int launch_rows_k(const GemvArgs& a, int wg_per_cu, hipStream_t s) {
     auto kern = gemv_rows_kernel<WF, XT, NMAT, OP, NW, CPW>;
     // A persistent grid must fit on the GPU at once: cap by the occupancy the
     // kernel's registers and LDS allow.
+    const size_t dyn = dyn_lds(a);
     int fit = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&fit, kern, NW * 64, 0) != hipSuccess || fit < 1) fit = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&fit, kern, NW * 64, dyn) != hipSuccess || fit < 1) fit = 1;
     if (wg_per_cu > fit) wg_per_cu = fit;
     int grid = 256 * wg_per_cu;
     if (grid > a.M) grid = a.M;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), 0, s, a);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), dyn, s, a);
     return mxd::check_launch("matvec");
 }
 
@@ -337,6 +343,7 @@ constexpr int SW_MAX_ROWS = 256;
 
 template <int WF, typename XT, int NMAT, int OP, int NW, int CPW>
 __global__ void __launch_bounds__(NW * 64) gemv_sweep_kernel(GemvArgs a) {
+    if constexpr (std::is_same<XT, float>::value) residual_prologue<NW>(a);
     constexpr int EPL = WT<WF>::EPL;
     constexpr int CH = 64 * EPL;
     __shared__ float part[SW_MAX_ROWS][NMAT][NW];
@@ -434,14 +441,15 @@ __global__ void __launch_bounds__(NW * 64) gemv_sweep_kernel(GemvArgs a) {
 template <int WF, typename XT, int NMAT, int OP, int NW, int CPW>
 int launch_sweep_k(const GemvArgs& a, int wg_per_cu, hipStream_t s) {
     auto kern = gemv_sweep_kernel<WF, XT, NMAT, OP, NW, CPW>;
+    const size_t dyn = dyn_lds(a);
     int fit = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&fit, kern, NW * 64, 0) != hipSuccess || fit < 1) fit = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&fit, kern, NW * 64, dyn) != hipSuccess || fit < 1) fit = 1;
     if (wg_per_cu > fit) wg_per_cu = fit;
     int grid = 256 * wg_per_cu;
     const int min_grid = (a.M + SW_MAX_ROWS - 1) / SW_MAX_ROWS;  // LDS holds SW_MAX_ROWS rows per workgroup
     if (grid < min_grid) grid = min_grid;
     if (grid > a.M) grid = a.M;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), 0, s, a);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), dyn, s, a);
     return mxd::check_launch("matvec");
 }
 
@@ -485,11 +493,12 @@ void pick_tiling(int M, int nch, bool q8, bool x_half, bool norm, int& nr, int& 
 template <int WF, typename XT, int NMAT, int OP, int NR>
 int launch_nw(const GemvArgs& a, int nw, hipStream_t s) {
     const dim3 grid((a.M + NR - 1) / NR);
+    const size_t dyn = dyn_lds(a);
     switch (nw) {
-        case 1: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 1>), grid, dim3(64), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 2>), grid, dim3(128), 0, s, a); break;
-        case 4: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 4>), grid, dim3(256), 0, s, a); break;
-        case 8: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 8>), grid, dim3(512), 0, s, a); break;
+        case 1: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 1>), grid, dim3(64), dyn, s, a); break;
+        case 2: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 2>), grid, dim3(128), dyn, s, a); break;
+        case 4: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 4>), grid, dim3(256), dyn, s, a); break;
+        case 8: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 8>), grid, dim3(512), dyn, s, a); break;
         default: return mxd::fail(MXD_ERR_INVALID_ARG, "matvec: MV_NW must be 1, 2, 4 or 8 (got %d)", nw);
     }
     return mxd::check_launch("matvec");
@@ -706,6 +715,59 @@ extern "C" int mxd_gate_up_rmsnorm(const uint16_t* Wg, const uint16_t* Wu, const
     a.nw = norm_w;
     a.eps = eps;
     a.plus_one = plus_one;
+    return launch_act<MXD_W_F16, float>(a, act, mxd::as_stream(stream));
+}
+
+namespace {
+
+int check_residual(const char* fn, const float* x, const float* res_src, const float* res_w, const float* x_out) {
+    MXD_REQUIRE(res_src && res_w && x_out, MXD_ERR_INVALID_ARG, "%s: null residual pointer", fn);
+    MXD_REQUIRE(x_out != x && x_out != res_src, MXD_ERR_INVALID_ARG, "%s: x_out must not alias x or res_src", fn);
+    MXD_REQUIRE(aligned16(res_src) && aligned16(res_w) && aligned16(x_out), MXD_ERR_UNSUPPORTED,
+                "%s: residual pointers must be 16-byte aligned", fn);
+    return MXD_OK;
+}
+
+}  // namespace
+
+extern "C" int mxd_matvec_f16_residual(const uint16_t* W, const float* x, const float* res_src, const float* res_w,
+                                       float res_post, float* x_out, const float* norm_w, float eps, int plus_one,
+                                       float* y, int M, int K, int epilogue, const float* aux, mxd_stream_t stream) {
+    const char* fn = "mxd_matvec_f16_residual";
+    if (norm_w) {
+        if (int rc = check_norm(fn, W, x, norm_w, y, M, K)) return rc;
+    } else {
+        if (int rc = check_common(fn, W, x, y, M, K)) return rc;
+        MXD_REQUIRE(K % 8 == 0, MXD_ERR_UNSUPPORTED, "%s: K=%d must be a multiple of 8", fn, K);
+    }
+    if (int rc = check_residual(fn, x, res_src, res_w, x_out)) return rc;
+    MXD_REQUIRE(epilogue != MXD_EPI_GELU_MUL || aux, MXD_ERR_INVALID_ARG, "%s: GELU_MUL needs aux", fn);
+    GemvArgs a{{W, nullptr}, {nullptr, nullptr}, x, y, aux, M, K};
+    a.nw = norm_w;
+    a.eps = eps;
+    a.plus_one = plus_one;
+    a.rsrc = res_src;
+    a.rw = res_w;
+    a.rpost = res_post;
+    a.rout = x_out;
+    return launch_epi<MXD_W_F16, float>(a, epilogue, mxd::as_stream(stream));
+}
+
+extern "C" int mxd_gate_up_residual(const uint16_t* Wg, const uint16_t* Wu, const float* x, const float* res_src,
+                                    const float* res_w, float res_post, float* x_out, const float* norm_w, float eps,
+                                    int plus_one, float* h, int F, int K, int act, mxd_stream_t stream) {
+    const char* fn = "mxd_gate_up_residual";
+    if (int rc = check_norm(fn, Wg, x, norm_w, h, F, K)) return rc;
+    MXD_REQUIRE(Wu && aligned16(Wu), MXD_ERR_INVALID_ARG, "%s: Wu null or not 16-byte aligned", fn);
+    if (int rc = check_residual(fn, x, res_src, res_w, x_out)) return rc;
+    GemvArgs a{{Wg, Wu}, {nullptr, nullptr}, x, h, nullptr, F, K};
+    a.nw = norm_w;
+    a.eps = eps;
+    a.plus_one = plus_one;
+    a.rsrc = res_src;
+    a.rw = res_w;
+    a.rpost = res_post;
+    a.rout = x_out;
     return launch_act<MXD_W_F16, float>(a, act, mxd::as_stream(stream));
 }
 

@@ -43,6 +43,15 @@ struct GemvArgs {
     // fp32 x rounded to nearest-even fp16 on load (the batched products'
     // fp32-activation mode, below their matrix-core threshold)
     int xr16 = 0;
+    // Residual prologue (a sandwich norm's residual add folded into the next
+    // product): the product's x is x' = (x + rsrc * rsqrt(mean(rsrc^2) + eps)
+    // * rw) * rpost, formed by every workgroup in dynamic LDS (K floats) and
+    // written to rout by workgroup 0 (rout != x: the other workgroups still
+    // read x).
+    const float* rsrc = nullptr;
+    const float* rw = nullptr;
+    float rpost = 1.0f;
+    float* rout = nullptr;
 };
 
 constexpr int MERGE_MAX_SPLITS = 8;
@@ -241,6 +250,32 @@ __device__ __forceinline__ float block_rms_scale(const float* x, int K, float ep
 #pragma unroll
     for (int w = 1; w < NW; ++w) tot += nred[w];
     return rsqrtf(tot / (float)K + eps);
+}
+
+// The residual prologue (GemvArgs::rsrc): forms x' in dynamic LDS and points
+// a.x at it. Every thread of the workgroup calls it before any x load.
+template <int NW>
+__device__ __forceinline__ void residual_prologue(GemvArgs& a) {
+    if (!a.rsrc) return;
+    extern __shared__ __attribute__((aligned(16))) float gemv_dyn_x[];
+    const int K = a.K;
+    const float scale = block_rms_scale<NW>(a.rsrc, K, a.eps);
+    const float* x = static_cast<const float*>(a.x);
+    const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && a.rout != nullptr;
+    for (int k = threadIdx.x * 4; k < K; k += NW * 64 * 4) {
+        const f4_t xv = *reinterpret_cast<const f4_t*>(x + k);
+        const f4_t sv = *reinterpret_cast<const f4_t*>(a.rsrc + k);
+        const f4_t wv = *reinterpret_cast<const f4_t*>(a.rw + k);
+        f4_t v;
+        v.x = (xv.x + sv.x * scale * wv.x) * a.rpost;
+        v.y = (xv.y + sv.y * scale * wv.y) * a.rpost;
+        v.z = (xv.z + sv.z * scale * wv.z) * a.rpost;
+        v.w = (xv.w + sv.w * scale * wv.w) * a.rpost;
+        *reinterpret_cast<f4_t*>(gemv_dyn_x + k) = v;
+        if (writer) *reinterpret_cast<f4_t*>(a.rout + k) = v;
+    }
+    __syncthreads();
+    a.x = gemv_dyn_x;
 }
 
 }  // namespace

@@ -377,6 +377,36 @@ def rmsnorm_add(src, w, x, eps: float, post: float = 1.0) -> torch.Tensor:
     return x
 
 
+def matvec_f16_residual(W, x, res_src, res_w, x_out, eps: float, res_post: float = 1.0, norm_w=None, y=None,
+                        epilogue: str = "store", aux=None) -> torch.Tensor:
+    """x_out = (x + rmsnorm(res_src) * res_w) * res_post, then y (op)= W . x_out
+    (W . rmsnorm(x_out) * norm_w with norm_w), in one launch."""
+    _on_gpu(W, x, res_src, res_w, x_out)
+    M, K = W.shape
+    _need(W.dtype == torch.float16 and x.dtype == torch.float32 and x.numel() == K,
+          "matvec_f16_residual: W fp16 [M, K], x float32 [K]")
+    _need(res_src.numel() == K and res_w.numel() == K and x_out.numel() == K, "matvec_f16_residual: vectors of K")
+    if y is None:
+        _need(epilogue != "add", "matvec_f16_residual: epilogue 'add' needs y")
+        y = torch.empty(M, dtype=torch.float32, device=W.device)
+    call("mxd_matvec_f16_residual", _ptr(W), _ptr(x), _ptr(res_src), _ptr(res_w), float(res_post), _ptr(x_out),
+         _ptr(norm_w), float(eps), 0, _ptr(y), M, K, _EPI[epilogue], _ptr(aux), _stream())
+    return y
+
+
+def gate_up_residual(Wg, Wu, x, res_src, res_w, x_out, norm_w, eps: float, res_post: float = 1.0,
+                     act: str = "gelu_tanh", h=None) -> torch.Tensor:
+    """x_out = (x + rmsnorm(res_src) * res_w) * res_post, then
+    h = act(Wg . n) * (Wu . n) with n = rmsnorm(x_out) * norm_w, in one launch."""
+    _on_gpu(Wg, Wu, x, res_src, res_w, x_out, norm_w)
+    F, K = Wg.shape
+    _need(Wu.shape == Wg.shape and Wg.dtype == torch.float16, "gate_up_residual: Wg, Wu fp16 [F, K]")
+    h = torch.empty(F, dtype=torch.float32, device=Wg.device) if h is None else h
+    call("mxd_gate_up_residual", _ptr(Wg), _ptr(Wu), _ptr(x), _ptr(res_src), _ptr(res_w), float(res_post), _ptr(x_out),
+         _ptr(norm_w), float(eps), 0, _ptr(h), F, K, _ACT[act], _stream())
+    return h
+
+
 def ple_combine(proj, ple, w, n_layers: int, dim: int, eps: float) -> torch.Tensor:
     """ple = (rmsnorm(proj / sqrt(dim)) * w + ple) / sqrt(2) over each of the
     n_layers slices of len(w) values per row (proj, ple float32 [rows, n_layers * P])."""

@@ -121,6 +121,20 @@ int mxd_matvec_f16_rmsnorm(const uint16_t* W, const float* x, const float* norm_
 int mxd_gate_up_rmsnorm(const uint16_t* Wg, const uint16_t* Wu, const float* x, const float* norm_w, float eps,
                         int plus_one, float* h, int F, int K, int act, mxd_stream_t stream);
 
+/* The same products after a sandwich norm's residual add: with
+ * x' = (x + res_src * rsqrt(mean(res_src^2) + eps) * res_w) * res_post (the
+ * mxd_rmsnorm_add of res_src into x), y (op)= W · rmsnorm(x') (norm_w NULL:
+ * W · x'), or h = act(Wg · rmsnorm(x')) * (Wu · rmsnorm(x')). Every
+ * workgroup forms x' itself; one of them writes it to x_out, which must not
+ * alias x or res_src (x' is the next residual). Fuses Gemma-4's rmsnorm_add
+ * into the product that follows it (KG/main.swift:405-422). */
+int mxd_matvec_f16_residual(const uint16_t* W, const float* x, const float* res_src, const float* res_w,
+                            float res_post, float* x_out, const float* norm_w, float eps, int plus_one, float* y,
+                            int M, int K, int epilogue, const float* aux, mxd_stream_t stream);
+int mxd_gate_up_residual(const uint16_t* Wg, const uint16_t* Wu, const float* x, const float* res_src,
+                         const float* res_w, float res_post, float* x_out, const float* norm_w, float eps,
+                         int plus_one, float* h, int F, int K, int act, mxd_stream_t stream);
+
 /* [q | k | v] = Wqkv · rmsnorm(x) (norm_w NULL: no norm), then RoPE on q and k
  * at pos and the K/V append, in the projection's epilogue: q (rotated, fp32,
  * n_heads*head_dim) goes to `q`, k and v (fp16) to the tiled caches. Fuses

@@ -80,6 +80,49 @@ def test_ple_combine(dev, rng, rows, L, P, D):
     _close(got.reshape(rows, L, P), want, 1e-6)
 
 
+@pytest.mark.parametrize("M,K", [(2560, 1536), (256, 1536), (65536, 1536), (1024, 256), (6144, 1536)])
+@pytest.mark.parametrize("norm", [True, False])
+def test_matvec_residual(dev, rng, M, K, norm):
+    """The sandwich norm's residual add folded into the next product: x_out =
+    (x + rmsnorm(src) * w) * post, y = W . rmsnorm(x_out) * nw (or W . x_out
+    with the gelu * aux epilogue); every tiling the shape selects, the LM-head
+    sweep included."""
+    ops = _ops()
+    x = rng.standard_normal(K, dtype=np.float32)
+    src = rng.standard_normal(K, dtype=np.float32) * 3
+    w = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    W = (rng.standard_normal((M, K), dtype=np.float32) * 0.02).astype(np.float16)
+    aux = rng.standard_normal(M, dtype=np.float32)
+    xw = (x.astype(np.float64) + g4.rmsnorm_w(src, w, 1e-6)) * 0.7
+    xo = torch.empty(K, dtype=torch.float32, device=dev)
+    if norm:
+        y = ops.matvec_f16_residual(_t(W, dev), _t(x, dev), _t(src, dev), _t(w, dev), xo, 1e-6, 0.7, _t(nw, dev))
+        want = ref.matvec(W, g4.rmsnorm_w(xw, nw, 1e-6))
+    else:
+        y = ops.matvec_f16_residual(_t(W, dev), _t(x, dev), _t(src, dev), _t(w, dev), xo, 1e-6, 0.7,
+                                    epilogue="gelu_mul", aux=_t(aux, dev))
+        want = ref.gelu_tanh(ref.matvec(W, xw)) * aux
+    _close(xo.cpu().numpy(), xw, 1e-6)
+    _close(y.cpu().numpy(), want, 1e-5)
+
+
+@pytest.mark.parametrize("F,K", [(6144, 1536), (512, 256)])
+def test_gate_up_residual(dev, rng, F, K):
+    ops = _ops()
+    x = rng.standard_normal(K, dtype=np.float32)
+    src = rng.standard_normal(K, dtype=np.float32)
+    w = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    Wg = (rng.standard_normal((F, K), dtype=np.float32) * 0.02).astype(np.float16)
+    Wu = (rng.standard_normal((F, K), dtype=np.float32) * 0.02).astype(np.float16)
+    xo = torch.empty(K, dtype=torch.float32, device=dev)
+    h = ops.gate_up_residual(_t(Wg, dev), _t(Wu, dev), _t(x, dev), _t(src, dev), _t(w, dev), xo, _t(nw, dev), 1e-6)
+    xw = x.astype(np.float64) + g4.rmsnorm_w(src, w, 1e-6)
+    _close(xo.cpu().numpy(), xw, 1e-6)
+    _close(h.cpu().numpy(), ref.gate_up(Wg, Wu, g4.rmsnorm_w(xw, nw, 1e-6), "gelu_tanh"), 1e-5)
+
+
 def _tile_rows(tiles, pos, which):
     """Cache rows [n_kv, hd] at position pos of the tiled layout."""
     ops = _ops()
@@ -185,6 +228,19 @@ def test_attention_prefill_window(dev, rng, hd, window):
 # ---------------------------------------------------------------- engine
 
 
+@pytest.fixture(params=["folded", "separate"])
+def g4_resadd(request):
+    """The sandwich norms' residual adds folded into the next product (the
+    default) or as their own launches (ENG_G4_RESADD=2)."""
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
+    _lib.set_tunable("ENG_G4_RESADD", 2 if request.param == "separate" else 1)
+    try:
+        yield request.param
+    finally:
+        _lib.set_tunable("ENG_G4_RESADD", 0)
+
+
 def _shape(cfg: g4.G4Config):
     from gemmagemini4hackathon2026_10_2425_amd.engine import Gemma4Layer, Gemma4Shape
 
@@ -225,7 +281,7 @@ def test_gemma4_engine_weights_are_the_generator(dev):
             assert np.array_equal(got.view(np.uint8), w.view(np.uint8)), name
 
 
-def test_gemma4_engine_matches_oracle_every_position(dev):
+def test_gemma4_engine_matches_oracle_every_position(dev, g4_resadd):
     """Softcapped logits after every step of prompt + greedy continuation, the
     positions past the sliding window (16) included."""
     cfg = g4.G4_TINY
@@ -301,7 +357,7 @@ def test_gemma4_engine_prefill_chunks(dev):
         _close(e.logits(), oracle.softcap(raw), 2e-3)
 
 
-def test_gemma4_engine_decode_graph_equals_steps(dev):
+def test_gemma4_engine_decode_graph_equals_steps(dev, g4_resadd):
     cfg = g4.G4_TINY
     prompt = [5, 17, 999, 3, 250]
     with _engine(cfg, 64, 3, 0.25) as a, _engine(cfg, 64, 3, 0.25) as b:
