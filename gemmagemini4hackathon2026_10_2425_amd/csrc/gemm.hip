@@ -120,6 +120,15 @@ __device__ __forceinline__ h8_t q8x8_to_h8(uint32_t lo, uint32_t hi) {
     return h8_t{a[0].x, a[0].y, a[1].x, a[1].y, a[2].x, a[2].y, a[3].x, a[3].y};
 }
 
+// Eight dequantised weights fp16(q * s): the int8 values are exact in fp16,
+// and each product is rounded once (packed fp16 multiplies), so the matrix
+// cores accumulate the scaled weights directly.
+__device__ __forceinline__ h8_t q8x8_scaled(uint32_t lo, uint32_t hi, _Float16 s) {
+    const h8_t q = q8x8_to_h8(lo, hi);
+    const h8_t sv = {s, s, s, s, s, s, s, s};
+    return q * sv;
+}
+
 // The runtime-loop form (any chunk count): activations in registers two
 // chunks ahead, a register ring of two chunks of weights and scales.
 template <int NMAT, int OP, bool XF32>
@@ -191,20 +200,19 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_loop_kernel(GemmArgs a) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
-    const f32x16_t zero = acc[0];
 
     // One chunk (ci = chunk index within the split, par = ci & 1, also the LDS
     // buffer holding it).
     auto chunk = [&](const int ci, const int par) {
         const bool more = c0 + ci + 1 < c1;
         if (c0 + ci + 2 < c1) load_x(xv[par], ci + 2);
-        float sc[4];
+        _Float16 sc[4];
         {
             const u2_t sv = sr[par];
-            sc[0] = mxd::h2f((uint16_t)(sv.x & 0xFFFFu));
-            sc[1] = mxd::h2f((uint16_t)(sv.x >> 16));
-            sc[2] = mxd::h2f((uint16_t)(sv.y & 0xFFFFu));
-            sc[3] = mxd::h2f((uint16_t)(sv.y >> 16));
+            sc[0] = mxd::as_h2(sv.x).x;
+            sc[1] = mxd::as_h2(sv.x).y;
+            sc[2] = mxd::as_h2(sv.y).x;
+            sc[3] = mxd::as_h2(sv.y).y;
         }
         const bool refill = c0 + ci + 2 < c1;
         if (refill) sr[par] = *reinterpret_cast<const u2_t*>(sp + 4 * (ci + 2));
@@ -214,25 +222,16 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_q8_loop_kernel(GemmArgs a) {
             if (refill)
                 wr[par][j] = *reinterpret_cast<const u4_t*>(
                     wp + (size_t)(ci + 2) * GM2_CK + 32 * j);
-            const h8_t w0 = q8x8_to_h8(w.x, w.y), w1 = q8x8_to_h8(w.z, w.w);
+            const h8_t w0 = q8x8_scaled(w.x, w.y, sc[j]), w1 = q8x8_scaled(w.z, w.w, sc[j]);
             const int kx = 32 * j + 16 * h;
             const h8_t x00 = *reinterpret_cast<const h8_t*>(&xs[par][mc][kx]);
             const h8_t x01 = *reinterpret_cast<const h8_t*>(&xs[par][mc][kx + 8]);
             const h8_t x10 = *reinterpret_cast<const h8_t*>(&xs[par][32 + mc][kx]);
             const h8_t x11 = *reinterpret_cast<const h8_t*>(&xs[par][32 + mc][kx + 8]);
-            f32x16_t t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x00, w0, zero, 0, 0, 0);
-            f32x16_t t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, zero, 0, 0, 0);
-            t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, t0, 0, 0, 0);
-            t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, t1, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                acc[0][r] = fmaf(sc[j], t0[r], acc[0][r]);
-                acc[1][r] = fmaf(sc[j], t1[r], acc[1][r]);
-            }
-            // One block's products live at a time: the empty asm consumes the
-            // accumulators here, so the scaling cannot be sunk below the next
-            // block's MFMAs (which would keep all four blocks' products live).
-            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x00, w0, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, acc[1], 0, 0, 0);
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, acc[1], 0, 0, 0);
         }
         if (more) store_x(xv[par ^ 1], par ^ 1);
         __syncthreads();
@@ -408,21 +407,18 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
-    const f32x16_t zero = acc[0];
-    f32x16_t tp[2] = {zero, zero};  // int8: the previous block's unscaled products
-    float sp = 0.0f;                // and its scale
 
     static_for<0, NCH>([&](auto cic) {
         constexpr int ci = decltype(cic)::value;
         constexpr int par = ci & 1;
         const _Float16(*xcur)[GM2_CK] = xs[par];
-        float sc[4];
+        _Float16 sc[4];
         if constexpr (Q8) {
             const u2_t sv2 = *reinterpret_cast<const u2_t*>(&ss[wave][mc][4 * ci]);
-            sc[0] = mxd::h2f((uint16_t)(sv2.x & 0xFFFFu));
-            sc[1] = mxd::h2f((uint16_t)(sv2.x >> 16));
-            sc[2] = mxd::h2f((uint16_t)(sv2.y & 0xFFFFu));
-            sc[3] = mxd::h2f((uint16_t)(sv2.y >> 16));
+            sc[0] = mxd::as_h2(sv2.x).x;
+            sc[1] = mxd::as_h2(sv2.x).y;
+            sc[2] = mxd::as_h2(sv2.y).x;
+            sc[3] = mxd::as_h2(sv2.y).y;
         }
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (ci + 2 < NCH) load_x(ic<ci + 2>{});
@@ -432,8 +428,8 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
             h8_t w0, w1;
             if constexpr (Q8) {
                 const u4_t w = wr[par][j];
-                w0 = q8x8_to_h8(w.x, w.y);
-                w1 = q8x8_to_h8(w.z, w.w);
+                w0 = q8x8_scaled(w.x, w.y, sc[j]);
+                w1 = q8x8_scaled(w.z, w.w, sc[j]);
             } else {
                 __builtin_memcpy(&w0, &wr[par][2 * j], 16);
                 __builtin_memcpy(&w1, &wr[par][2 * j + 1], 16);
@@ -446,44 +442,17 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
             const h8_t x01 = *reinterpret_cast<const h8_t*>(&xcur[mc][8 * ((p0 + 1) ^ sw)]);
             const h8_t x10 = *reinterpret_cast<const h8_t*>(&xcur[32 + mc][8 * (p0 ^ sw)]);
             const h8_t x11 = *reinterpret_cast<const h8_t*>(&xcur[32 + mc][8 * ((p0 + 1) ^ sw)]);
-            if constexpr (Q8) {
-                f32x16_t t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x00, w0, zero, 0, 0, 0);
-                f32x16_t t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, zero, 0, 0, 0);
-                t0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, t0, 0, 0, 0);
-                t1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, t1, 0, 0, 0);
-                // Software pipeline: the previous block's products are scaled
-                // while this block's MFMAs run (they do not depend on each
-                // other), so the matrix core and the VALU overlap in one wave.
-                if (ci > 0 || j > 0) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        acc[0][r] = fmaf(sp, tp[0][r], acc[0][r]);
-                        acc[1][r] = fmaf(sp, tp[1][r], acc[1][r]);
-                    }
-                }
-                tp[0] = t0;
-                tp[1] = t1;
-                sp = sc[j];
-            } else {
-                acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x00, w0, acc[0], 0, 0, 0);
-                acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, acc[1], 0, 0, 0);
-                acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, acc[0], 0, 0, 0);
-                acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, acc[1], 0, 0, 0);
-            }
-            if constexpr (!Q8) asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x00, w0, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, acc[1], 0, 0, 0);
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, acc[1], 0, 0, 0);
+            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
         }
         if constexpr (ci + 1 < NCH) {
             store_x(ic<ci + 1>{});
             __syncthreads();
         }
     });
-    if constexpr (Q8) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            acc[0][r] = fmaf(sp, tp[0][r], acc[0][r]);
-            acc[1][r] = fmaf(sp, tp[1][r], acc[1][r]);
-        }
-    }
 
     const int wr_out = row0 + mc;
     auto brow = [&](int t, int r) { return b0 + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3); };

@@ -15,7 +15,9 @@ KL/kernels.metal:361-365), the projections and the residual to fp32, K/V to
 the caches' dtype (fp16 as on the device). Caches here are per sequence in the
 reference's layout [n_kv, ctx, hd].
 
-Pins (tests/test_oracle.py): dequant by closed forms; gemm_q8b32 row by row
+Pins (tests/test_oracle.py): dequant by closed forms (its fp16 mode within
+half an fp16 ulp of each exact weight, and equal to numpy's own fp16
+rounding of it); gemm_q8b32 row by row
 against ops.matvec_q8b32 and against math.fsum brute force; gate_up_rows row
 by row against ops.gate_up_q8b32; layer_step on a ragged, staggered batch
 against each sequence stepped alone, and, without the fp16 activation
@@ -71,25 +73,29 @@ def synthetic_layer(cfg: LayerConfig, seed: int, std: float = 0.02) -> dict:
     return W
 
 
-def dequant(q: np.ndarray, s: np.ndarray) -> np.ndarray:
-    """fp64 weights q * s (exact: an fp16 scale times an int8 fits in fp64)."""
+def dequant(q: np.ndarray, s: np.ndarray, f16: bool = False) -> np.ndarray:
+    """fp64 weights q * s (exact: an fp16 scale times an int8 fits in fp64);
+    f16: each product rounded to fp16 (nearest even), the weights the batched
+    matrix-core products feed their fp16 MFMAs."""
     M, K = q.shape
-    return (q.reshape(M, K // 32, 32).astype(F64) * s.astype(F64)[:, :, None]).reshape(M, K)
+    w = (q.reshape(M, K // 32, 32).astype(F64) * s.astype(F64)[:, :, None]).reshape(M, K)
+    return w.astype(F16).astype(F64) if f16 else w
 
 
-def gemm_q8b32(q: np.ndarray, s: np.ndarray, X: np.ndarray) -> np.ndarray:
+def gemm_q8b32(q: np.ndarray, s: np.ndarray, X: np.ndarray, f16_weights: bool = False) -> np.ndarray:
     """Y[b] = matvec_q8b32(q, s, X[b]) for every row b, in fp64 (one
-    dequantisation, one BLAS product)."""
-    return np.asarray(X, dtype=F64) @ dequant(q, s).T
+    dequantisation, one BLAS product); f16_weights: with the dequantised
+    weights rounded to fp16 (the matrix-core path, from 16 rows)."""
+    return np.asarray(X, dtype=F64) @ dequant(q, s, f16_weights).T
 
 
-def gate_up_rows(qg, sg, qu, su, X, act: str) -> np.ndarray:
-    g, u = gemm_q8b32(qg, sg, X), gemm_q8b32(qu, su, X)
+def gate_up_rows(qg, sg, qu, su, X, act: str, f16_weights: bool = False) -> np.ndarray:
+    g, u = gemm_q8b32(qg, sg, X, f16_weights), gemm_q8b32(qu, su, X, f16_weights)
     return (ops.gelu_tanh(g) if act == "gelu_tanh" else ops.silu(g)) * u
 
 
 def layer_step(cfg: LayerConfig, W: dict, X: np.ndarray, kcaches: list, vcaches: list,
-               seq_lens: np.ndarray, half_acts: bool = True) -> np.ndarray:
+               seq_lens: np.ndarray, half_acts: bool = True, f16_weights: bool = False) -> np.ndarray:
     """One decode step of the layer for every sequence; returns the new residual
     rows (fp32 [B, D]) and appends each sequence's k, v to its caches (rounded
     to the caches' dtype).
@@ -98,7 +104,9 @@ def layer_step(cfg: LayerConfig, W: dict, X: np.ndarray, kcaches: list, vcaches:
     s fp16) pairs. kcaches[b], vcaches[b]: [n_kv, ctx_b, hd], ctx_b >=
     seq_lens[b]. half_acts=False skips the three fp16 roundings of the
     products' activation operands (then, with fp64 caches, the step is the
-    layer's exact arithmetic up to the fp32 storage of its outputs)."""
+    layer's exact arithmetic up to the fp32 storage of its outputs);
+    f16_weights rounds the dequantised weights to fp16 (the matrix-core
+    products of a batch of at least 16 rows)."""
     B = X.shape[0]
     NH, NKV, hd = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
     H = F16 if half_acts else F32
@@ -106,13 +114,14 @@ def layer_step(cfg: LayerConfig, W: dict, X: np.ndarray, kcaches: list, vcaches:
     scale = 1.0 / math.sqrt(hd)
     X = np.asarray(X, dtype=F32)
     xn = ops.rmsnorm(X, W["attn_norm"], cfg.eps, cfg.plus_one).astype(H)
-    qkv = gemm_q8b32(*W["wqkv"], xn).astype(F32)
+    fw = f16_weights
+    qkv = gemm_q8b32(*W["wqkv"], xn, fw).astype(F32)
     att = np.empty((B, NH * hd), dtype=F32)
     for b in range(B):
         pos = int(seq_lens[b]) - 1
         q = ops.rope_kv(qkv[b], kcaches[b], vcaches[b], invf, NH, NKV, pos).astype(F32)
         att[b] = ops.attention(q, kcaches[b], vcaches[b], pos + 1, NH, scale)
-    x1 = (X.astype(F64) + gemm_q8b32(*W["wo"], att.astype(H))).astype(F32)
+    x1 = (X.astype(F64) + gemm_q8b32(*W["wo"], att.astype(H), fw)).astype(F32)
     xn2 = ops.rmsnorm(x1, W["ffn_norm"], cfg.eps, cfg.plus_one).astype(H)
-    h = gate_up_rows(*W["wgate"], *W["wup"], xn2, cfg.act).astype(F32).astype(H)
-    return (x1.astype(F64) + gemm_q8b32(*W["wdown"], h)).astype(F32)
+    h = gate_up_rows(*W["wgate"], *W["wup"], xn2, cfg.act, fw).astype(F32).astype(H)
+    return (x1.astype(F64) + gemm_q8b32(*W["wdown"], h, fw)).astype(F32)

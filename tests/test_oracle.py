@@ -426,6 +426,24 @@ def test_batch_dequant_closed_forms():
     assert not d[1, :32].any() and np.all(d[1, 32:] == -127 * 0.25)
 
 
+def test_batch_dequant_f16_rounds_each_weight(rng):
+    """The fp16-weight mode: every weight within half an fp16 ulp of q * s
+    (relative 2^-11 for normal values), exact where q * s is representable
+    (q * 2^k, |q| <= 127 < 2^11), and a product of it is within
+    2^-11 * sum |w x| of the exact one."""
+    q = rng.integers(-127, 128, (40, 256)).astype(np.int8)
+    s = (np.abs(rng.standard_normal((40, 8))) * 1e-3 + 1e-4).astype(np.float16)
+    exact, rounded = ob.dequant(q, s), ob.dequant(q, s, f16=True)
+    nz = exact != 0
+    assert np.all(np.abs(rounded - exact)[nz] <= np.abs(exact)[nz] * 2.0**-11)
+    pow2 = np.full((1, 8), 0.0078125, np.float16)  # 2^-7: every product exact in fp16
+    assert np.array_equal(ob.dequant(q[:1], pow2, f16=True), ob.dequant(q[:1], pow2))
+    X = rng.standard_normal((5, 256)).astype(np.float16)
+    d = ob.gemm_q8b32(q, s, X, True) - ob.gemm_q8b32(q, s, X)
+    bound = 2.0**-11 * (np.abs(X.astype(np.float64)) @ np.abs(exact).T)
+    assert np.all(np.abs(d) <= bound * (1 + 1e-9))
+
+
 def test_batch_gemm_q8b32_rows_equal_matvec(rng):
     W = rng.standard_normal((23, 320)).astype(np.float32) * 0.02
     q, s = ops.quantize_q8b32(W)
