@@ -20,9 +20,9 @@ namespace {
 
 // NMAT == 1: OP is an MXD_EPI_* or EPI_ROPE_KV; NMAT == 2: OP is an MXD_ACT_*
 // (gate, up).
-template <int WF, typename XT, int NMAT, int OP, int NR, int NW>
+template <int WF, typename XT, int NMAT, int OP, int NR, int NW, bool RES = false>
 __global__ void __launch_bounds__(NW * 64) gemv_kernel(GemvArgs a) {
-    if constexpr (std::is_same<XT, float>::value && OP != EPI_ROPE_KV) residual_prologue<NW>(a);
+    if constexpr (RES) residual_prologue<NW>(a);
     constexpr int EPL = WT<WF>::EPL;
     constexpr int CH = 64 * EPL;
     constexpr int U = (8 / (NR * NMAT)) > 0 ? (8 / (NR * NMAT)) : 1;
@@ -204,9 +204,9 @@ constexpr int RS_MAX_CHUNKS = 64;  // 16 waves x 4 chunks
 // Dynamic LDS of a launch: the residual prologue's x' (K floats).
 size_t dyn_lds(const GemvArgs& a) { return a.rsrc ? (size_t)a.K * sizeof(float) : 0; }
 
-template <int WF, typename XT, int NMAT, int OP, int NW, int RS_CPW>
+template <int WF, typename XT, int NMAT, int OP, int NW, int RS_CPW, bool RES = false>
 __global__ void __launch_bounds__(NW * 64) gemv_rows_kernel(GemvArgs a) {
-    if constexpr (std::is_same<XT, float>::value) residual_prologue<NW>(a);
+    if constexpr (RES) residual_prologue<NW>(a);
     constexpr int EPL = WT<WF>::EPL;
     constexpr int CH = 64 * EPL;
     const int lane = threadIdx.x & 63;
@@ -298,9 +298,16 @@ __global__ void __launch_bounds__(NW * 64) gemv_rows_kernel(GemvArgs a) {
     }
 }
 
-template <int WF, typename XT, int NMAT, int OP, int NW, int CPW>
-int launch_rows_k(const GemvArgs& a, int wg_per_cu, hipStream_t s) {
-    auto kern = gemv_rows_kernel<WF, XT, NMAT, OP, NW, CPW>;
+// Whether a launch takes the residual prologue (fp16 weights, fp32 x only:
+// the kernels without it keep their x in the global address space).
+template <int WF, typename XT, int OP>
+constexpr bool res_capable() {
+    return WF == MXD_W_F16 && std::is_same<XT, float>::value && OP != EPI_ROPE_KV;
+}
+
+template <int WF, typename XT, int NMAT, int OP, int NW, int CPW, bool RES>
+int launch_rows_kr(const GemvArgs& a, int wg_per_cu, hipStream_t s) {
+    auto kern = gemv_rows_kernel<WF, XT, NMAT, OP, NW, CPW, RES>;
     // A persistent grid must fit on the GPU at once: cap by the occupancy the
     // kernel's registers and LDS allow.
     const size_t dyn = dyn_lds(a);
@@ -311,6 +318,14 @@ int launch_rows_k(const GemvArgs& a, int wg_per_cu, hipStream_t s) {
     if (grid > a.M) grid = a.M;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), dyn, s, a);
     return mxd::check_launch("matvec");
+}
+
+template <int WF, typename XT, int NMAT, int OP, int NW, int CPW>
+int launch_rows_k(const GemvArgs& a, int wg_per_cu, hipStream_t s) {
+    if constexpr (res_capable<WF, XT, OP>()) {
+        if (a.rsrc) return launch_rows_kr<WF, XT, NMAT, OP, NW, CPW, true>(a, wg_per_cu, s);
+    }
+    return launch_rows_kr<WF, XT, NMAT, OP, NW, CPW, false>(a, wg_per_cu, s);
 }
 
 template <int WF, typename XT, int NMAT, int OP>
@@ -341,9 +356,9 @@ int launch_rows(const GemvArgs& a, int nw, int cpw, int wg_per_cu, hipStream_t s
 // ---------------------------------------------------------------------------
 constexpr int SW_MAX_ROWS = 256;
 
-template <int WF, typename XT, int NMAT, int OP, int NW, int CPW>
+template <int WF, typename XT, int NMAT, int OP, int NW, int CPW, bool RES = false>
 __global__ void __launch_bounds__(NW * 64) gemv_sweep_kernel(GemvArgs a) {
-    if constexpr (std::is_same<XT, float>::value) residual_prologue<NW>(a);
+    if constexpr (RES) residual_prologue<NW>(a);
     constexpr int EPL = WT<WF>::EPL;
     constexpr int CH = 64 * EPL;
     __shared__ float part[SW_MAX_ROWS][NMAT][NW];
@@ -438,9 +453,9 @@ __global__ void __launch_bounds__(NW * 64) gemv_sweep_kernel(GemvArgs a) {
     }
 }
 
-template <int WF, typename XT, int NMAT, int OP, int NW, int CPW>
-int launch_sweep_k(const GemvArgs& a, int wg_per_cu, hipStream_t s) {
-    auto kern = gemv_sweep_kernel<WF, XT, NMAT, OP, NW, CPW>;
+template <int WF, typename XT, int NMAT, int OP, int NW, int CPW, bool RES>
+int launch_sweep_kr(const GemvArgs& a, int wg_per_cu, hipStream_t s) {
+    auto kern = gemv_sweep_kernel<WF, XT, NMAT, OP, NW, CPW, RES>;
     const size_t dyn = dyn_lds(a);
     int fit = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&fit, kern, NW * 64, dyn) != hipSuccess || fit < 1) fit = 1;
@@ -451,6 +466,14 @@ int launch_sweep_k(const GemvArgs& a, int wg_per_cu, hipStream_t s) {
     if (grid > a.M) grid = a.M;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), dyn, s, a);
     return mxd::check_launch("matvec");
+}
+
+template <int WF, typename XT, int NMAT, int OP, int NW, int CPW>
+int launch_sweep_k(const GemvArgs& a, int wg_per_cu, hipStream_t s) {
+    if constexpr (res_capable<WF, XT, OP>()) {
+        if (a.rsrc) return launch_sweep_kr<WF, XT, NMAT, OP, NW, CPW, true>(a, wg_per_cu, s);
+    }
+    return launch_sweep_kr<WF, XT, NMAT, OP, NW, CPW, false>(a, wg_per_cu, s);
 }
 
 template <int WF, typename XT, int NMAT, int OP>
@@ -490,18 +513,26 @@ void pick_tiling(int M, int nch, bool q8, bool x_half, bool norm, int& nr, int& 
     nw = mxd::tunable("MV_NW", nw);
 }
 
-template <int WF, typename XT, int NMAT, int OP, int NR>
-int launch_nw(const GemvArgs& a, int nw, hipStream_t s) {
+template <int WF, typename XT, int NMAT, int OP, int NR, bool RES>
+int launch_nwr(const GemvArgs& a, int nw, hipStream_t s) {
     const dim3 grid((a.M + NR - 1) / NR);
     const size_t dyn = dyn_lds(a);
     switch (nw) {
-        case 1: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 1>), grid, dim3(64), dyn, s, a); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 2>), grid, dim3(128), dyn, s, a); break;
-        case 4: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 4>), grid, dim3(256), dyn, s, a); break;
-        case 8: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 8>), grid, dim3(512), dyn, s, a); break;
+        case 1: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 1, RES>), grid, dim3(64), dyn, s, a); break;
+        case 2: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 2, RES>), grid, dim3(128), dyn, s, a); break;
+        case 4: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 4, RES>), grid, dim3(256), dyn, s, a); break;
+        case 8: hipLaunchKernelGGL((gemv_kernel<WF, XT, NMAT, OP, NR, 8, RES>), grid, dim3(512), dyn, s, a); break;
         default: return mxd::fail(MXD_ERR_INVALID_ARG, "matvec: MV_NW must be 1, 2, 4 or 8 (got %d)", nw);
     }
     return mxd::check_launch("matvec");
+}
+
+template <int WF, typename XT, int NMAT, int OP, int NR>
+int launch_nw(const GemvArgs& a, int nw, hipStream_t s) {
+    if constexpr (res_capable<WF, XT, OP>()) {
+        if (a.rsrc) return launch_nwr<WF, XT, NMAT, OP, NR, true>(a, nw, s);
+    }
+    return launch_nwr<WF, XT, NMAT, OP, NR, false>(a, nw, s);
 }
 
 template <int WF, typename XT, int NMAT, int OP>
