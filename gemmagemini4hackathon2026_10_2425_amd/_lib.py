@@ -117,6 +117,8 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_matvec_gate_up": (c_int, [c_int, P, P, P, P, P, c_int, P, c_int, c_int, c_int, P]),
     "mxd_matvec_f16_rmsnorm": (c_int, [P, P, P, c_float, c_int, P, c_int, c_int, c_int, P, P]),
     "mxd_matvec_f16_attn_merge": (c_int, [P, P, c_int, c_int, c_int, c_int, c_int, P, P, c_int, c_int, P, P]),
+    "mxd_matvec_f16_attn_merge_window": (c_int, [P, P, c_int, c_int, c_int, c_int, c_int, P, c_int, P, c_int, c_int, P,
+                                                 P]),
     "mxd_matvec_f16_residual": (c_int, [P, P, P, P, c_float, P, P, c_float, c_int, P, c_int, c_int, c_int, P, P]),
     "mxd_gate_up_residual": (c_int, [P, P, P, P, P, c_float, P, P, c_float, c_int, P, c_int, c_int, c_int, P]),
     "mxd_gate_up_rmsnorm": (c_int, [P, P, P, P, c_float, c_int, P, c_int, c_int, c_int, P]),
@@ -131,6 +133,8 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_attention_noalloc_max_scratch": (c_size_t, []),
     "mxd_attention_noalloc": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, P]),
     "mxd_attention_split": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, c_int, P, c_size_t, P]),
+    "mxd_attention_split_window": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_int, c_float, c_int, P,
+                                           c_size_t, P]),
     "mxd_attention_prefill": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, P]),
     "mxd_attention_window": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_int, c_float, P, c_size_t,
                                      P]),

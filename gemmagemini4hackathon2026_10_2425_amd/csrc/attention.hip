@@ -569,14 +569,23 @@ extern "C" int mxd_attention_split(const float* q, const uint16_t* kcache, const
                                    int n_kv_heads, int head_dim, int max_ctx, int n_keys, const int32_t* pos_dev,
                                    float scale, int n_splits, float* partials, size_t partial_bytes,
                                    mxd_stream_t stream) {
+    return mxd_attention_split_window(q, kcache, vcache, n_heads, n_kv_heads, head_dim, max_ctx, n_keys, pos_dev, 0,
+                                      scale, n_splits, partials, partial_bytes, stream);
+}
+
+extern "C" int mxd_attention_split_window(const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                                          int n_heads, int n_kv_heads, int head_dim, int max_ctx, int n_keys,
+                                          const int32_t* pos_dev, int window, float scale, int n_splits,
+                                          float* partials, size_t partial_bytes, mxd_stream_t stream) {
+    MXD_REQUIRE(window >= 0, MXD_ERR_INVALID_ARG, "mxd_attention_split: window=%d", window);
     MXD_REQUIRE(q && kcache && vcache && partials, MXD_ERR_INVALID_ARG, "mxd_attention_split: null pointer");
     MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, MXD_ERR_INVALID_ARG,
                 "mxd_attention_split: n_heads=%d must be a positive multiple of n_kv_heads=%d", n_heads, n_kv_heads);
     const int G = n_heads / n_kv_heads;
     MXD_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, MXD_ERR_UNSUPPORTED,
                 "mxd_attention_split: group size %d (n_heads / n_kv_heads) must be 1, 2, 4 or 8", G);
-    MXD_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, MXD_ERR_UNSUPPORTED, "mxd_attention_split: head_dim %d (64, 128 or 256)",
-                head_dim);
+    MXD_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512, MXD_ERR_UNSUPPORTED,
+                "mxd_attention_split: head_dim %d (64, 128, 256 or 512)", head_dim);
     MXD_REQUIRE(max_ctx > 0 && max_ctx % 32 == 0, MXD_ERR_UNSUPPORTED,
                 "mxd_attention_split: max_ctx=%d must be a positive multiple of 32", max_ctx);
     MXD_REQUIRE(pos_dev || (n_keys >= 1 && n_keys <= max_ctx), MXD_ERR_INVALID_ARG,
@@ -606,9 +615,10 @@ extern "C" int mxd_attention_split(const float* q, const uint16_t* kcache, const
     a.n_splits = n_splits;
     a.qscale = scale * LOG2E;
     a.partials_only = true;
+    a.window = window;
     hipStream_t s = mxd::as_stream(stream);
     const dim3 grid(n_splits, n_kv_heads);
-    with_head_dim(head_dim, [&](auto hd) { launch_split<decltype(hd)::value>(grid, s, a); });
+    with_head_dim<true>(head_dim, [&](auto hd) { launch_split<decltype(hd)::value>(grid, s, a); });
     return mxd::check_launch("mxd_attention_split");
 }
 

@@ -108,6 +108,9 @@ struct mxd_engine {
     float* ple_norm = nullptr;
     float *tmp = nullptr, *ple = nullptr, *pleproj = nullptr, *pleg = nullptr;
     float* x2 = nullptr;  // the second residual buffer (x and x2 alternate)
+    // per layer: splits of the attention whose partials the o projection
+    // merges (0: the attention with its own output, then the o projection)
+    std::vector<int> g4_splits;
     float *btmp = nullptr, *bple = nullptr, *bpleproj = nullptr, *bpleg = nullptr;
     uint16_t* bpleg16 = nullptr;
 

@@ -172,10 +172,23 @@ int mxd_eng::g4_step(mxd_engine* e, int pos, int32_t* pos_dev, bool sample) {
                                       own ? Lp.k_norm : nullptr, e->invf + (size_t)l * G4_FREQS, NH, own ? NKV : 0,
                                       hd, y.rope_pairs, e->max_ctx, eps, pos, 1, pos_dev, ms)))
             return rc;
-        if ((rc = mxd_attention_window(e->qkv, Lp.kc, Lp.vc, e->att, NH, NKV, hd, e->max_ctx, pos + 1, pos_dev,
-                                       y.sliding ? c.window : 0, 1.0f, e->attn_ws, e->attn_ws_bytes, ms)))
-            return rc;
-        if ((rc = mxd_matvec_f16(Lp.wo, e->att, MXD_F32, e->tmp, D, NH * hd, MXD_EPI_STORE, nullptr, ms))) return rc;
+        const int window = y.sliding ? c.window : 0;
+        if (const int S = e->g4_splits[l]) {
+            // the splits' partials, merged by the o projection as it loads them
+            float* part = static_cast<float*>(e->attn_ws);
+            if ((rc = mxd_attention_split_window(e->qkv, Lp.kc, Lp.vc, NH, NKV, hd, e->max_ctx, pos + 1, pos_dev,
+                                                 window, 1.0f, S, part, e->attn_ws_bytes, ms)))
+                return rc;
+            if ((rc = mxd_matvec_f16_attn_merge_window(Lp.wo, part, S, NH, hd, e->max_ctx, pos + 1, pos_dev, window,
+                                                       e->tmp, D, MXD_EPI_STORE, nullptr, ms)))
+                return rc;
+        } else {
+            if ((rc = mxd_attention_window(e->qkv, Lp.kc, Lp.vc, e->att, NH, NKV, hd, e->max_ctx, pos + 1, pos_dev,
+                                           window, 1.0f, e->attn_ws, e->attn_ws_bytes, ms)))
+                return rc;
+            if ((rc = mxd_matvec_f16(Lp.wo, e->att, MXD_F32, e->tmp, D, NH * hd, MXD_EPI_STORE, nullptr, ms)))
+                return rc;
+        }
         if ((rc = residual_add(Lp.post_attn_norm, 1.0f))) return rc;
         if (pend_w) {
             rc = mxd_gate_up_residual(Lp.wgate, Lp.wup, xc, e->tmp, pend_w, pend_post, xo, Lp.ffn_norm, eps, 0, e->h,
@@ -322,11 +335,23 @@ extern "C" int mxd_engine_create_gemma4(const mxd_gemma4_config* cfg, int max_ct
     const size_t D = c.dim, P = c.ple_dim, LP = (size_t)L * P;
     int max_qkv = 0, max_q = 0, max_f = 0;
     e->attn_ws_bytes = 0;
+    // The decode attention leaves its splits' partials for the o projection
+    // to merge when a layer sees at most 8 x 4 blocks (one 32-key block per
+    // wave, 2 to 8 splits; ENG_ATT_FOLD = 2: never), as the Gemma-2B step
+    // does; sliding layers see at most window + 32 keys of the cache.
+    e->g4_splits.assign(L, 0);
     for (int l = 0; l < L; ++l) {
+        const mxd_gemma4_layer& y = e->g4l[l];
         max_qkv = max(max_qkv, g4_qkv_dim(e, l));
         max_q = max(max_q, g4_q_dim(e, l));
-        max_f = max(max_f, e->g4l[l].ffn_dim);
-        e->attn_ws_bytes = max(e->attn_ws_bytes, mxd_attention_workspace_size(NH, NKV, e->g4l[l].head_dim, max_ctx));
+        max_f = max(max_f, y.ffn_dim);
+        e->attn_ws_bytes = max(e->attn_ws_bytes, mxd_attention_workspace_size(NH, NKV, y.head_dim, max_ctx));
+        const int keys = y.sliding && c.window > 0 ? min(max_ctx, c.window + 32) : max_ctx;
+        const int S = ((keys + 31) / 32 + 3) / 4;
+        if (S >= 2 && S <= 8 && mxd::tunable("ENG_ATT_FOLD", 1) != 2) {
+            e->g4_splits[l] = S;
+            e->attn_ws_bytes = max(e->attn_ws_bytes, (size_t)S * NH * (y.head_dim + 2) * sizeof(float));
+        }
     }
     size_t off = 0;
     auto take = [&](size_t bytes) {

@@ -846,7 +846,16 @@ extern "C" int mxd_qkv_rope_kv(const uint16_t* Wqkv, const float* x, const float
 extern "C" int mxd_matvec_f16_attn_merge(const uint16_t* W, const float* partials, int n_splits, int n_heads,
                                          int head_dim, int max_ctx, int n_keys, const int32_t* pos_dev, float* y,
                                          int M, int epilogue, const float* aux, mxd_stream_t stream) {
+    return mxd_matvec_f16_attn_merge_window(W, partials, n_splits, n_heads, head_dim, max_ctx, n_keys, pos_dev, 0, y,
+                                            M, epilogue, aux, stream);
+}
+
+extern "C" int mxd_matvec_f16_attn_merge_window(const uint16_t* W, const float* partials, int n_splits, int n_heads,
+                                                int head_dim, int max_ctx, int n_keys, const int32_t* pos_dev,
+                                                int window, float* y, int M, int epilogue, const float* aux,
+                                                mxd_stream_t stream) {
     const int K = n_heads * head_dim;
+    MXD_REQUIRE(window >= 0, MXD_ERR_INVALID_ARG, "mxd_matvec_f16_attn_merge: window=%d", window);
     if (int rc = check_common("mxd_matvec_f16_attn_merge", W, partials, y, M, K)) return rc;
     MXD_REQUIRE(n_splits >= 1 && n_splits <= MERGE_MAX_SPLITS, MXD_ERR_UNSUPPORTED,
                 "mxd_matvec_f16_attn_merge: n_splits=%d outside [1, %d]", n_splits, MERGE_MAX_SPLITS);
@@ -866,6 +875,7 @@ extern "C" int mxd_matvec_f16_attn_merge(const uint16_t* W, const float* partial
     a.max_ctx = max_ctx;
     a.n_keys = n_keys;
     a.pos_dev = pos_dev;
+    a.mwindow = window;
     // Row tiles (every workgroup merges the x it reads, so fewer, taller
     // tiles read fewer partials): 8 rows from 2048 rows on.
     int nr, nw;

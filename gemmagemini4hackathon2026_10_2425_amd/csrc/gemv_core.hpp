@@ -40,6 +40,7 @@ struct GemvArgs {
     const float* mpo = nullptr;
     const float* mpml = nullptr;
     int msplits = 0, n_keys = 0;
+    int mwindow = 0;  // the producer's sliding window (0: all keys)
     // fp32 x rounded to nearest-even fp16 on load (the batched products'
     // fp32-activation mode, below their matrix-core threshold)
     int xr16 = 0;
@@ -61,7 +62,8 @@ constexpr int MERGE_MAX_SPLITS = 8;
 __device__ __forceinline__ int merge_active(const GemvArgs& a) {
     int n = a.pos_dev ? a.pos_dev[0] + 1 : a.n_keys;
     n = max(0, min(n, a.max_ctx));
-    return max(1, min(a.msplits, (n + 31) / 32));
+    const int lo = a.mwindow > 0 ? max(0, n - a.mwindow) : 0;  // blocks before the window hold none
+    return max(1, min(a.msplits, (n + 31) / 32 - lo / 32));
 }
 
 // Internal epilogue: rows are rotated in (i, i + hd/2) pairs and q goes back

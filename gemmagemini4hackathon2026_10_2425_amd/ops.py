@@ -303,7 +303,7 @@ def attention(q, kcache, vcache, n_keys: int, n_heads: int, scale: float | None 
 
 
 def attention_split(q, kcache, vcache, n_keys: int, n_heads: int, n_splits: int, scale: float | None = None,
-                    partials=None, pos_dev=None) -> torch.Tensor:
+                    partials=None, pos_dev=None, window: int = 0) -> torch.Tensor:
     """The split half of attention without its merge: a float32 buffer of
     n_splits unnormalised partials, O [n_splits, n_heads, hd] then (max, sum)
     [n_splits, n_heads, 2] (log2-domain scores), for matvec_f16_attn_merge."""
@@ -315,14 +315,14 @@ def attention_split(q, kcache, vcache, n_keys: int, n_heads: int, n_splits: int,
     partials = torch.empty(n, dtype=torch.float32, device=q.device) if partials is None else partials
     _need(partials.dtype == torch.float32 and partials.numel() >= n, f"attention_split: partials float32 [{n}]")
     call(
-        "mxd_attention_split", _ptr(q), _ptr(kcache), _ptr(vcache), n_heads, n_kv, hd, max_ctx, int(n_keys),
-        _ptr(pos_dev), float(scale), int(n_splits), _ptr(partials), partials.numel() * 4, _stream(),
+        "mxd_attention_split_window", _ptr(q), _ptr(kcache), _ptr(vcache), n_heads, n_kv, hd, max_ctx, int(n_keys),
+        _ptr(pos_dev), int(window), float(scale), int(n_splits), _ptr(partials), partials.numel() * 4, _stream(),
     )
     return partials
 
 
 def matvec_f16_attn_merge(W, partials, n_splits: int, n_heads: int, head_dim: int, max_ctx: int, n_keys: int,
-                          y=None, epilogue: str = "store", pos_dev=None) -> torch.Tensor:
+                          y=None, epilogue: str = "store", pos_dev=None, window: int = 0) -> torch.Tensor:
     """y (op)= W . x with x the log-sum-exp merge of attention_split's partials."""
     _on_gpu(W, partials)
     M, K = W.shape
@@ -332,8 +332,8 @@ def matvec_f16_attn_merge(W, partials, n_splits: int, n_heads: int, head_dim: in
         _need(epilogue == "store", "matvec_f16_attn_merge: epilogue 'add' needs y")
         y = torch.empty(M, dtype=torch.float32, device=W.device)
     call(
-        "mxd_matvec_f16_attn_merge", _ptr(W), _ptr(partials), int(n_splits), n_heads, head_dim, max_ctx,
-        int(n_keys), _ptr(pos_dev), _ptr(y), M, _EPI[epilogue], None, _stream(),
+        "mxd_matvec_f16_attn_merge_window", _ptr(W), _ptr(partials), int(n_splits), n_heads, head_dim, max_ctx,
+        int(n_keys), _ptr(pos_dev), int(window), _ptr(y), M, _EPI[epilogue], None, _stream(),
     )
     return y
 

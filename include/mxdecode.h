@@ -154,6 +154,10 @@ int mxd_qkv_rope_kv(const uint16_t* Wqkv, const float* x, const float* norm_w, f
 int mxd_matvec_f16_attn_merge(const uint16_t* W, const float* partials, int n_splits, int n_heads,
                               int head_dim, int max_ctx, int n_keys, const int32_t* n_keys_dev, float* y,
                               int M, int epilogue, const float* aux, mxd_stream_t stream);
+/* The merge of mxd_attention_split_window's partials (the same window). */
+int mxd_matvec_f16_attn_merge_window(const uint16_t* W, const float* partials, int n_splits, int n_heads,
+                                     int head_dim, int max_ctx, int n_keys, const int32_t* pos_dev, int window,
+                                     float* y, int M, int epilogue, const float* aux, mxd_stream_t stream);
 
 /* ---- normalisation, embedding, casts ------------------------------------ */
 
@@ -233,6 +237,14 @@ int mxd_attention_split(const float* q, const uint16_t* kcache, const uint16_t* 
                         int n_kv_heads, int head_dim, int max_ctx, int n_keys, const int32_t* n_keys_dev,
                         float scale, int n_splits, float* partials, size_t partial_bytes,
                         mxd_stream_t stream);
+/* The same over a sliding window: the blocks dealt to the splits start at the
+ * window's first block, and the active splits count the attended blocks
+ * (min(n_splits, ceil(n_keys / 32) - start / 32), start = max(0, n_keys -
+ * window)). Merge with mxd_matvec_f16_attn_merge_window at the same window. */
+int mxd_attention_split_window(const float* q, const uint16_t* kcache, const uint16_t* vcache, int n_heads,
+                               int n_kv_heads, int head_dim, int max_ctx, int n_keys, const int32_t* n_keys_dev,
+                               int window, float scale, int n_splits, float* partials, size_t partial_bytes,
+                               mxd_stream_t stream);
 
 /* Causal attention of a prefill chunk: `rows` queries at positions pos0 ..
  * pos0 + rows - 1 (their keys and values already in the caches), query t over

@@ -212,6 +212,28 @@ def test_attention_window_ignores_keys_before_start(dev, rng):
     _close(out.cpu().numpy(), _window_ref(q, kc, vc, L, nh, window), 1e-3)
 
 
+@pytest.mark.parametrize("nh,hd", [(8, 256), (8, 512), (4, 64)])
+@pytest.mark.parametrize("L,window,S", [(40, 16, 2), (300, 160, 2), (600, 512, 5), (1000, 512, 8), (200, 0, 3),
+                                        (1, 512, 4)])
+def test_attention_split_window_merged_by_o_projection(dev, rng, nh, hd, L, window, S):
+    """The windowed split attention's partials (blocks dealt from the
+    window's first block) merged by the o projection as it loads them: Wo .
+    attention over the last `window` keys; the key count read on the device
+    gives the same result."""
+    ops = _ops()
+    M, max_ctx = 512, max(64, (L + 31) // 32 * 32)
+    q, kc, vc = _attn_case(rng, nh, 1, hd, L, max_ctx)
+    Wo = (rng.standard_normal((M, nh * hd), dtype=np.float32) * 0.02).astype(np.float16)
+    qd, kd, vd, wd = _t(q, dev), _t(ops.to_tiles(kc, "k"), dev), _t(ops.to_tiles(vc, "v"), dev), _t(Wo, dev)
+    part = ops.attention_split(qd, kd, vd, L, nh, S, scale=1.0, window=window)
+    got = ops.matvec_f16_attn_merge(wd, part, S, nh, hd, max_ctx, L, window=window).cpu().numpy()
+    _close(got, ref.matvec(Wo, _window_ref(q, kc, vc, L, nh, window)), 1e-3)
+    pos = torch.tensor([L - 1], dtype=torch.int32, device=dev)
+    part2 = ops.attention_split(qd, kd, vd, 0, nh, S, scale=1.0, window=window, pos_dev=pos)
+    got2 = ops.matvec_f16_attn_merge(wd, part2, S, nh, hd, max_ctx, 0, window=window, pos_dev=pos).cpu().numpy()
+    assert np.array_equal(got, got2)
+
+
 @pytest.mark.parametrize("hd,window", [(128, 16), (512, 0), (256, 48)])
 def test_attention_prefill_window(dev, rng, hd, window):
     ops = _ops()
@@ -301,6 +323,54 @@ def test_gemma4_engine_matches_oracle_every_position(dev, g4_resadd):
             else:
                 e.set_tokens([prompt[pos + 1]], pos + 1)
         assert e.tokens(len(prompt), len(greedy)) == greedy
+
+
+@pytest.mark.parametrize("fold", ["merged", "separate"])
+def test_gemma4_engine_long_context_window(dev, fold):
+    """A window of 160 keys at max_ctx 320: the sliding layers' attention runs
+    as 2 splits whose partials the o projection merges (ENG_ATT_FOLD=2: the
+    attention with its own output), the full layers as 3. A 250-token prompt
+    stepped through the decode path (past the window), then 12 graph-replayed
+    steps: the softcapped logits of the prompt's last position and of every
+    replayed step within 2e-3 of the oracle, the same greedy tokens, and the
+    replayed steps equal eager ones bit for bit."""
+    import dataclasses
+
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
+    cfg = dataclasses.replace(g4.G4_TINY, window=160)
+    _, seed, qk, _, _ = _golden()
+    prompt = np.random.default_rng(7).integers(0, cfg.vocab, 250).tolist()
+    oracle = g4.G4Decoder(cfg, g4.make_weights(cfg, seed, qk_norm_scale=qk), 320)
+    oracle.tokens[: len(prompt)] = prompt
+    for pos in range(len(prompt)):
+        raw = oracle.forward(pos)
+    oracle.tokens[len(prompt)] = ref.argmax(raw)
+    _lib.set_tunable("ENG_ATT_FOLD", 2 if fold == "separate" else 1)
+    try:
+        with _engine(cfg, 320, seed, qk) as a, _engine(cfg, 320, seed, qk) as b:
+            _lib.set_tunable("ENG_NO_GEMM", 1)
+            try:
+                for e in (a, b):
+                    e.set_tokens(prompt)
+                    e.prefill(len(prompt))
+            finally:
+                _lib.set_tunable("ENG_NO_GEMM", 0)
+            _close(a.logits(), oracle.softcap(raw), 2e-3)
+            assert a.token(len(prompt)) == int(oracle.tokens[len(prompt)])
+            for pos in range(len(prompt), len(prompt) + 12):
+                raw = oracle.forward(pos)
+                oracle.tokens[pos + 1] = ref.argmax(raw)
+                a.decode(pos, 1)
+                b.step(pos)
+                got = a.logits()
+                _close(got, oracle.softcap(raw), 2e-3)
+                assert np.array_equal(got, b.logits()), f"pos {pos}: graph and eager steps differ"
+            n = len(prompt)
+            assert a.tokens(n, 13) == [int(t) for t in oracle.tokens[n : n + 13]]
+            assert b.tokens(n, 13) == a.tokens(n, 13)
+    finally:
+        _lib.set_tunable("ENG_ATT_FOLD", 0)
 
 
 def test_gemma4_engine_generate_matches_transformers(dev):
