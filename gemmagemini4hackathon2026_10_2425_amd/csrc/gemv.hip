@@ -577,17 +577,29 @@ int launch(const GemvArgs& a, hipStream_t s) {
     if (algo == 1) {
         MXD_REQUIRE(nch <= RS_MAX_CHUNKS, MXD_ERR_UNSUPPORTED, "matvec: row streaming needs K <= %d",
                     RS_MAX_CHUNKS * CH);
-        // Long rows: 16 waves, or 14 where that covers the row's chunks with
-        // fewer idle waves (K = 14336: 28 fp16 chunks as 14 x 2 instead of
-        // 16 x 2; 4096 x 14336 fp16 measured 18.9 against 19.3 us).
-        int nw_long = 16;
-        if (nch > 8 && ((nch + 13) / 14) * 14 - nch < ((nch + 15) / 16) * 16 - nch && (nch + 13) / 14 <= 2) nw_long = 14;
-        const int nw = mxd::tunable("MV_RS_NW", rows_glu ? 8 : nch <= 4 ? 4 : nch <= 8 ? 8 : nw_long);
+        // Long rows: 16 waves, or 14 where 14 waves cover the row's chunks
+        // exactly (K = 14336: 28 fp16 chunks as 14 x 2 instead of 16 x 2;
+        // 4096 x 14336 fp16 measured 18.9 against 19.3 us). Where neither
+        // covers it exactly, 16 (Gemma-4-E2B down, 1536 x 12288: 8.60 against
+        // 9.08 us as 14 x 2; 1536 x 6144: 5.52 against 5.62 as 14 x 1).
+        const int nw_long = nch % 14 == 0 && nch <= 28 ? 14 : 16;
+        // Rows of 3 chunks (K = 1536) keep every wave busy with 4 waves; the
+        // gate/up pair then runs 8 workgroups per CU (E2B, 12288 x 1536 x 2
+        // with the residual prologue: 15.79 against 18.33 us as 8 waves x 4
+        // per CU; 6144 rows: 10.21 against 11.05).
+        const bool glu3 = rows_glu && nch <= 3;
+        const int nw = mxd::tunable("MV_RS_NW", rows_glu && !glu3 ? 8 : nch <= 4 ? 4 : nch <= 8 ? 8 : nw_long);
         int cpw = (nch + nw - 1) / nw;
         cpw = cpw <= 1 ? 1 : cpw <= 2 ? 2 : 4;
         MXD_REQUIRE(nw * cpw >= nch, MXD_ERR_UNSUPPORTED,
                     "matvec: row streaming with %d waves covers at most %d chunks", nw, nw * 4);
-        const int wg_per_cu = mxd::tunable("MV_RS_WGCU", rows_glu ? 4 : nw >= 16 ? 2 : 32 / nw);
+        // The residual prologue is per workgroup (it reads three K-vectors
+        // and reduces them before the first row), so a single short-row
+        // matrix with it takes 4 workgroups per CU instead of 8 (E2B q|k|v,
+        // 2560 x 1536: 5.80 against 6.50 us; q, 2048 x 1536: 5.62 against 6.38).
+        const int wg_small = a.rsrc && nw == 4 ? 4 : 32 / nw;
+        const int wg_per_cu =
+            mxd::tunable("MV_RS_WGCU", glu3 ? 8 : rows_glu ? 4 : nw >= 16 ? 2 : wg_small);
         return launch_rows<WF, XT, NMAT, OP>(a, nw, cpw, wg_per_cu, s);
     }
     if (algo == 2) {
