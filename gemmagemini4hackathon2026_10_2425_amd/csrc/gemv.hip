@@ -206,7 +206,6 @@ size_t dyn_lds(const GemvArgs& a) { return a.rsrc ? (size_t)a.K * sizeof(float) 
 
 template <int WF, typename XT, int NMAT, int OP, int NW, int RS_CPW, bool RES = false>
 __global__ void __launch_bounds__(NW * 64) gemv_rows_kernel(GemvArgs a) {
-    if constexpr (RES) residual_prologue<NW>(a);
     constexpr int EPL = WT<WF>::EPL;
     constexpr int CH = 64 * EPL;
     const int lane = threadIdx.x & 63;
@@ -220,17 +219,10 @@ __global__ void __launch_bounds__(NW * 64) gemv_rows_kernel(GemvArgs a) {
     int col[RS_CPW];
     bool ok[RS_CPW];
     XFrag<XT, EPL> xf[RS_CPW];
-    const float nscale = a.nw ? block_rms_scale<NW>(static_cast<const float*>(a.x), K, a.eps) : 1.0f;
 #pragma unroll
     for (int j = 0; j < RS_CPW; ++j) {
         col[j] = (wave + j * NW) * CH + lane * EPL;
         ok[j] = (wave + j * NW) < nch && col[j] < K;
-        if (ok[j]) {
-            if (a.nw)
-                xf[j].load_norm(a.x, a.nw, col[j], nscale, a.plus_one);
-            else
-                xf[j].load(a.x, col[j], a.xr16);
-        }
     }
 
     __shared__ float red[2][NW][NMAT];
@@ -249,8 +241,28 @@ __global__ void __launch_bounds__(NW * 64) gemv_rows_kernel(GemvArgs a) {
             }
     };
 
+    auto load_x = [&]() {
+        const float nscale = a.nw ? block_rms_scale<NW>(static_cast<const float*>(a.x), K, a.eps) : 1.0f;
+#pragma unroll
+        for (int j = 0; j < RS_CPW; ++j) {
+            if (ok[j]) {
+                if (a.nw)
+                    xf[j].load_norm(a.x, a.nw, col[j], nscale, a.plus_one);
+                else
+                    xf[j].load(a.x, col[j], a.xr16);
+            }
+        }
+    };
     int row = blockIdx.x;
-    if (row < M) issue(row);
+    if constexpr (RES) {
+        // the first row's weights in flight before the prologue's round trip
+        if (row < M) issue(row);
+        residual_prologue<NW>(a);
+        load_x();
+    } else {
+        load_x();
+        if (row < M) issue(row);
+    }
     int buf = 0;
     for (; row < M; row += gridDim.x) {
         float acc[NMAT];
@@ -358,7 +370,6 @@ constexpr int SW_MAX_ROWS = 256;
 
 template <int WF, typename XT, int NMAT, int OP, int NW, int CPW, bool RES = false>
 __global__ void __launch_bounds__(NW * 64) gemv_sweep_kernel(GemvArgs a) {
-    if constexpr (RES) residual_prologue<NW>(a);
     constexpr int EPL = WT<WF>::EPL;
     constexpr int CH = 64 * EPL;
     __shared__ float part[SW_MAX_ROWS][NMAT][NW];
@@ -376,13 +387,17 @@ __global__ void __launch_bounds__(NW * 64) gemv_sweep_kernel(GemvArgs a) {
     for (int j = 0; j < CPW; ++j) {
         col[j] = (wave + j * NW) * CH + lane * EPL;
         ok[j] = (wave + j * NW) < nch && col[j] < K;
-        if (ok[j]) {
-            if (a.nw)
-                xf[j].load_norm(a.x, a.nw, col[j], 1.0f, a.plus_one);
-            else
-                xf[j].load(a.x, col[j], a.xr16);
-        }
     }
+    auto load_x = [&]() {
+#pragma unroll
+        for (int j = 0; j < CPW; ++j)
+            if (ok[j]) {
+                if (a.nw)
+                    xf[j].load_norm(a.x, a.nw, col[j], 1.0f, a.plus_one);
+                else
+                    xf[j].load(a.x, col[j], a.xr16);
+            }
+    };
 
     auto issue = [&](u4_t (&wv)[CPW][NMAT], uint16_t (&sv)[CPW][NMAT], int row) {
 #pragma unroll
@@ -420,7 +435,15 @@ __global__ void __launch_bounds__(NW * 64) gemv_sweep_kernel(GemvArgs a) {
 
     u4_t wa[CPW][NMAT], wb[CPW][NMAT];
     uint16_t sa[CPW][NMAT], sb[CPW][NMAT];
-    if (nrows > 0) issue(wa, sa, b);
+    if constexpr (RES) {
+        // the first row's weights in flight before the prologue's round trip
+        if (nrows > 0) issue(wa, sa, b);
+        residual_prologue<NW>(a);
+        load_x();
+    } else {
+        load_x();
+        if (nrows > 0) issue(wa, sa, b);
+    }
     for (int i = 0; i < nrows; i += 2) {
         if (i + 1 < nrows) issue(wb, sb, b + (i + 1) * G);
         consume(wa, sa, i);
@@ -889,7 +912,9 @@ extern "C" int mxd_matvec_f16_attn_merge_window(const uint16_t* W, const float* 
     a.pos_dev = pos_dev;
     a.mwindow = window;
     // Row tiles (every workgroup merges the x it reads, so fewer, taller
-    // tiles read fewer partials): 8 rows from 2048 rows on.
+    // tiles read fewer partials): 8 rows from 2048 rows on, 4 from 1024
+    // (Gemma-4-E2B, 1536 rows: decode 519 -> 538 tok/s against 2-row tiles;
+    // 8-row tiles, 192 workgroups, 534).
     int nr, nw;
     pick_tiling(M, (K + 511) / 512, false, false, false, nr, nw);
     hipStream_t s = mxd::as_stream(stream);
@@ -902,7 +927,9 @@ extern "C" int mxd_matvec_f16_attn_merge_window(const uint16_t* W, const float* 
             default: return mxd::fail(MXD_ERR_INVALID_ARG, "mxd_matvec_f16_attn_merge: unknown epilogue %d", epilogue);
         }
     };
-    if (M >= 2048) return go(std::integral_constant<int, 8>{});
-    if (M >= 256) return go(std::integral_constant<int, 2>{});
+    const int nrm = mxd::tunable("MV_MERGE_NR", M >= 2048 ? 8 : M >= 1024 ? 4 : M >= 256 ? 2 : 1);
+    if (nrm >= 8) return go(std::integral_constant<int, 8>{});
+    if (nrm >= 4) return go(std::integral_constant<int, 4>{});
+    if (nrm >= 2) return go(std::integral_constant<int, 2>{});
     return go(std::integral_constant<int, 1>{});
 }

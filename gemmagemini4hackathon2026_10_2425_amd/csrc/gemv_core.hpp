@@ -255,19 +255,21 @@ __device__ __forceinline__ float block_rms_scale(const float* x, int K, float ep
 }
 
 // The residual prologue (GemvArgs::rsrc): forms x' in dynamic LDS and points
-// a.x at it. Every thread of the workgroup calls it before any x load.
+// a.x at it. Every thread of the workgroup calls it before any x load; the
+// kernels issue their first weight loads before it, so the prologue's round
+// trip overlaps them. For K up to 4096 x (NW / 4) it loads src, x and w in one
+// pass and keeps them in registers through the rms reduction (the sum of
+// squares in the same per-thread order as block_rms_scale).
 template <int NW>
 __device__ __forceinline__ void residual_prologue(GemvArgs& a) {
     if (!a.rsrc) return;
     extern __shared__ __attribute__((aligned(16))) float gemv_dyn_x[];
+    constexpr int T = NW * 64;
+    constexpr int IT = 4096 / (T * 4) > 0 ? 4096 / (T * 4) : 1;  // f4 per thread held in registers
     const int K = a.K;
-    const float scale = block_rms_scale<NW>(a.rsrc, K, a.eps);
     const float* x = static_cast<const float*>(a.x);
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && a.rout != nullptr;
-    for (int k = threadIdx.x * 4; k < K; k += NW * 64 * 4) {
-        const f4_t xv = *reinterpret_cast<const f4_t*>(x + k);
-        const f4_t sv = *reinterpret_cast<const f4_t*>(a.rsrc + k);
-        const f4_t wv = *reinterpret_cast<const f4_t*>(a.rw + k);
+    auto finish = [&](int k, const f4_t& xv, const f4_t& sv, const f4_t& wv, float scale) {
         f4_t v;
         v.x = (xv.x + sv.x * scale * wv.x) * a.rpost;
         v.y = (xv.y + sv.y * scale * wv.y) * a.rpost;
@@ -275,6 +277,45 @@ __device__ __forceinline__ void residual_prologue(GemvArgs& a) {
         v.w = (xv.w + sv.w * scale * wv.w) * a.rpost;
         *reinterpret_cast<f4_t*>(gemv_dyn_x + k) = v;
         if (writer) *reinterpret_cast<f4_t*>(a.rout + k) = v;
+    };
+    if (K <= IT * T * 4) {
+        __shared__ float nred[NW];
+        f4_t xv[IT], sv[IT], wv[IT];
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < IT; ++i) {
+            const int k = (threadIdx.x + i * T) * 4;
+            if (k < K) {
+                sv[i] = *reinterpret_cast<const f4_t*>(a.rsrc + k);
+                xv[i] = *reinterpret_cast<const f4_t*>(x + k);
+                wv[i] = *reinterpret_cast<const f4_t*>(a.rw + k);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < IT; ++i) {
+            const int k = (threadIdx.x + i * T) * 4;
+            if (k < K) {
+                const f4_t t = sv[i];
+                ss = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, fmaf(t.w, t.w, ss))));
+            }
+        }
+        ss = mxd::wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) nred[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        float tot = nred[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) tot += nred[w];
+        const float scale = rsqrtf(tot / (float)K + a.eps);
+#pragma unroll
+        for (int i = 0; i < IT; ++i) {
+            const int k = (threadIdx.x + i * T) * 4;
+            if (k < K) finish(k, xv[i], sv[i], wv[i], scale);
+        }
+    } else {
+        const float scale = block_rms_scale<NW>(a.rsrc, K, a.eps);
+        for (int k = threadIdx.x * 4; k < K; k += T * 4)
+            finish(k, *reinterpret_cast<const f4_t*>(x + k), *reinterpret_cast<const f4_t*>(a.rsrc + k),
+                   *reinterpret_cast<const f4_t*>(a.rw + k), scale);
     }
     __syncthreads();
     a.x = gemv_dyn_x;
