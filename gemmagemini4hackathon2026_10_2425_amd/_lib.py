@@ -125,6 +125,7 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_qkv_rope_kv": (c_int, [P, P, P, c_float, c_int, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P,
                                 P]),
     "mxd_rmsnorm": (c_int, [P, P, P, c_int, c_int, c_int, c_float, c_int, P]),
+    "mxd_rmsnorm_residual_sum": (c_int, [P, P, c_int, P, P, c_int, c_int, c_int, c_float, c_int, P]),
     "mxd_embed": (c_int, [P, P, c_int, c_int, P, c_int, c_float, c_int, P]),
     "mxd_f32_to_f16": (c_int, [P, P, c_size_t, P]),
     "mxd_rope_kv": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P]),
@@ -148,11 +149,14 @@ SIGNATURES: dict[str, tuple] = {
     "mxd_argmax_workspace_size": (c_size_t, [c_int]),
     "mxd_argmax": (c_int, [P, P, c_int, c_int, P, c_size_t, P]),
     "mxd_rope_kv_paged": (c_int, [P, P, P, c_int, P, c_int, c_int, c_int, P, c_int, P, c_int, P]),
+    "mxd_rope_kv_paged_sum": (c_int, [P, c_int, P, P, P, c_int, P, c_int, c_int, c_int, P, c_int, P, c_int, P]),
     "mxd_attention_paged_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "mxd_attention_paged": (c_int, [P, c_int, P, P, c_int, P, c_int, P, c_int, P, c_int, c_int, c_int, c_int, c_int,
                                     c_float, P, c_size_t, P]),
     "mxd_gemm_q8b32_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "mxd_gemm_q8b32": (c_int, [P, P, P, c_int, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
+    "mxd_gemm_q8b32_partials_size": (c_size_t, [c_int, c_int, c_int]),
+    "mxd_gemm_q8b32_partials": (c_int, [P, P, P, c_int, P, c_size_t, c_int, c_int, c_int, P, P]),
     "mxd_gemm_gate_up_q8b32_workspace_size": (c_size_t, [c_int, c_int, c_int]),
     "mxd_gemm_gate_up_q8b32": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, P, c_size_t, P]),
     "mxd_gemm_f16_workspace_size": (c_size_t, [c_int, c_int, c_int]),

@@ -22,6 +22,7 @@ include/mxdecode.h.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from dataclasses import dataclass
 
@@ -195,6 +196,62 @@ def gemm_q8b32(Wq, scales, X, Y=None, epilogue: str = "store", workspace=None) -
     return Y
 
 
+def gemm_q8b32_partials_bytes(n_rows: int, M: int, K: int) -> int:
+    """Bytes gemm_q8b32_partials leaves for these sizes (0: not a matrix-core product)."""
+    return query("mxd_gemm_q8b32_partials_size", n_rows, M, K)
+
+
+def gemm_q8b32_partials(Wq, scales, X, part) -> int:
+    """The K-split partial products of gemm_q8b32 (store) left unsummed in
+    part (fp32, at least gemm_q8b32_partials_bytes); returns their count.
+    rope_kv_paged_sum and rmsnorm_residual_sum add them as they load them.
+    Needs B >= 16 and K % 128 == 0."""
+    ops._on_gpu(Wq, scales, X, part)
+    M, K = Wq.shape
+    _need(Wq.dtype == torch.int8 and scales.dtype == torch.float16 and tuple(scales.shape) == (M, K // 32),
+          "gemm_q8b32_partials: int8 Wq [M, K] and fp16 scales [M, K/32]")
+    _need(X.dtype in (torch.float16, torch.float32) and X.dim() == 2 and X.shape[1] == K and X.is_contiguous(),
+          "gemm_q8b32_partials: X fp16 or fp32 [B, K]")
+    _need(part.is_contiguous() and part.dtype == torch.float32, "gemm_q8b32_partials: part fp32")
+    n = ctypes.c_int(0)
+    call("mxd_gemm_q8b32_partials", Wq.data_ptr(), scales.data_ptr(), X.data_ptr(), ops._xdtype(X), part.data_ptr(),
+         part.numel() * 4, X.shape[0], M, K, ctypes.byref(n), ops._stream())
+    return n.value
+
+
+def rope_kv_paged_sum(part, n_splits: int, qkv, kpool, vpool, inv_freq_t, n_heads: int, n_kv_heads: int, page_table,
+                      seq_lens) -> None:
+    """rope_kv_paged over the sum of n_splits partials of the q|k|v product
+    (part as gemm_q8b32_partials leaves it): the rotated q goes to qkv, k and v
+    to the pages."""
+    ops._on_gpu(part, qkv, kpool, vpool, inv_freq_t, page_table, seq_lens)
+    n_pages, n_kv, page, hd = kpool.shape
+    _need(page == PAGE and n_kv == n_kv_heads and tuple(vpool.shape) == tuple(kpool.shape),
+          "rope_kv_paged_sum: pools [n_pages, n_kv, 16, hd]")
+    B = seq_lens.numel()
+    row = (n_heads + 2 * n_kv_heads) * hd
+    _need(qkv.dtype == torch.float32 and qkv.numel() == B * row, "rope_kv_paged_sum: qkv float32 [B, (NH + 2 NKV) hd]")
+    _need(part.dtype == torch.float32 and part.numel() >= n_splits * B * row, "rope_kv_paged_sum: part too small")
+    _need(page_table.dtype == torch.int32 and page_table.dim() == 2 and page_table.shape[0] == B,
+          "rope_kv_paged_sum: page_table int32 [B, max_pages]")
+    call("mxd_rope_kv_paged_sum", part.data_ptr(), n_splits, qkv.data_ptr(), kpool.data_ptr(), vpool.data_ptr(),
+         n_pages, inv_freq_t.data_ptr(), n_heads, n_kv_heads, hd, page_table.data_ptr(), page_table.shape[1],
+         seq_lens.data_ptr(), B, ops._stream())
+
+
+def rmsnorm_residual_sum(X, part, n_splits: int, w, eps: float, plus_one: bool, y) -> None:
+    """X += the sum of n_splits partials of a product with X's shape (part as
+    gemm_q8b32_partials leaves it), then y = rmsnorm(X) (fp16 or fp32 y)."""
+    ops._on_gpu(X, part, w, y)
+    B, D = X.shape
+    _need(X.dtype == torch.float32 and X.is_contiguous(), "rmsnorm_residual_sum: X fp32 [B, D]")
+    _need(part.dtype == torch.float32 and part.numel() >= n_splits * B * D, "rmsnorm_residual_sum: part too small")
+    _need(y.is_contiguous() and y.numel() == B * D and y.dtype in (torch.float16, torch.float32),
+          "rmsnorm_residual_sum: y fp16 or fp32 [B, D]")
+    call("mxd_rmsnorm_residual_sum", X.data_ptr(), part.data_ptr(), n_splits, w.data_ptr(), y.data_ptr(),
+         _lib.MXD_F16 if y.dtype == torch.float16 else _lib.MXD_F32, B, D, float(eps), int(plus_one), ops._stream())
+
+
 def gemm_gate_up_q8b32(Wg, sg, Wu, su, X, act: str = "silu", H=None, workspace=None) -> torch.Tensor:
     """H[b] = act(Wg . X[b]) * (Wu . X[b]); X fp16 [B, K], H fp32 [B, F]."""
     ops._on_gpu(Wg, sg, Wu, su, X)
@@ -248,9 +305,15 @@ class RaggedLayerQ8:
     batch: rmsnorm -> qkv -> rope_kv_paged -> attention_paged -> o (+x) ->
     rmsnorm -> gate/up (SwiGLU) -> down (+x), the reference's per-layer order
     (KL/main.swift:321-347). Workspaces and activations are allocated once
-    for batches of up to max_batch rows; step() allocates nothing."""
+    for batches of up to max_batch rows; step() allocates nothing.
 
-    def __init__(self, shape: LayerShape, weights: dict, max_batch: int, max_keys: int, device="cuda"):
+    From 16 rows on (fold_sums, the default) the qkv and o products leave
+    their K-split partials unsummed and the next op adds them as it loads
+    them (rope_kv_paged_sum, rmsnorm_residual_sum): two launches fewer per
+    step, with results bit-identical to the summing products."""
+
+    def __init__(self, shape: LayerShape, weights: dict, max_batch: int, max_keys: int, device="cuda",
+                 fold_sums: bool = True):
         self.s, self.dev, self.max_keys = shape, torch.device(device), max_keys
         s = shape
         D, F, QD = s.dim, s.ffn_dim, s.n_heads * s.head_dim
@@ -274,6 +337,15 @@ class RaggedLayerQ8:
             "wdown": gemm_workspace(B, D, F, False, self.dev),
             "attn": attention_paged_workspace(s.n_heads, s.n_kv_heads, s.head_dim, B, max_keys, self.dev),
         }
+        self.fold_sums = fold_sums
+        if fold_sums:
+            # partial buffers sized for every batch the matrix cores take
+            # (the split count depends on the batch)
+            rows = range(16, max(B, 16) + 1)
+            qb = max(gemm_q8b32_partials_bytes(b, s.qkv_dim, D) for b in rows)
+            ob = max(gemm_q8b32_partials_bytes(b, D, QD) for b in rows)
+            self.part_qkv = torch.empty(max(qb // 4, 4), dtype=torch.float32, device=self.dev)
+            self.part_o = torch.empty(max(ob // 4, 4), dtype=torch.float32, device=self.dev)
 
     def step(self, X: torch.Tensor, kpool, vpool, page_table, seq_lens) -> None:
         """X: fp32 [B, D] residual rows, updated in place; kpool / vpool this
@@ -281,15 +353,25 @@ class RaggedLayerQ8:
         s, B = self.s, X.shape[0]
         D, F, QD = s.dim, s.ffn_dim, s.n_heads * s.head_dim
         xn, qkv, att, h = self.xn[:B], self.qkv[:B], self.att[:B], self.h[:B]
+        fold = self.fold_sums and gemm_q8b32_partials_bytes(B, s.qkv_dim, D) > 0
         ops.rmsnorm(X, self.attn_norm, s.eps, s.plus_one, y=xn, out_dtype=torch.float16)
-        gemm_q8b32(*self.W["wqkv"], xn, qkv, workspace=self.ws["wqkv"])
-        rope_kv_paged(qkv, kpool, vpool, self.invf, s.n_heads, s.n_kv_heads, page_table, seq_lens)
+        if fold:
+            n = gemm_q8b32_partials(*self.W["wqkv"], xn, self.part_qkv)
+            rope_kv_paged_sum(self.part_qkv, n, qkv, kpool, vpool, self.invf, s.n_heads, s.n_kv_heads, page_table,
+                              seq_lens)
+        else:
+            gemm_q8b32(*self.W["wqkv"], xn, qkv, workspace=self.ws["wqkv"])
+            rope_kv_paged(qkv, kpool, vpool, self.invf, s.n_heads, s.n_kv_heads, page_table, seq_lens)
         attention_paged(qkv, kpool, vpool, page_table, seq_lens, s.n_heads, self.max_keys, q_stride=s.qkv_dim,
                         out=att, workspace=self.ws["attn"])
         # the fp32 attention output and hidden rows are rounded to fp16 as the
         # products load them (the reference's attHalf / hidHalf casts)
-        gemm_q8b32(*self.W["wo"], att, X, "add", workspace=self.ws["wo"])
-        ops.rmsnorm(X, self.ffn_norm, s.eps, s.plus_one, y=xn, out_dtype=torch.float16)
+        if fold:
+            n = gemm_q8b32_partials(*self.W["wo"], att, self.part_o)
+            rmsnorm_residual_sum(X, self.part_o, n, self.ffn_norm, s.eps, s.plus_one, xn)
+        else:
+            gemm_q8b32(*self.W["wo"], att, X, "add", workspace=self.ws["wo"])
+            ops.rmsnorm(X, self.ffn_norm, s.eps, s.plus_one, y=xn, out_dtype=torch.float16)
         gemm_gate_up_q8b32(*self.W["wgate"], *self.W["wup"], xn, s.act, h, workspace=self.ws["glu"])
         gemm_q8b32(*self.W["wdown"], h, X, "add", workspace=self.ws["wdown"])
 

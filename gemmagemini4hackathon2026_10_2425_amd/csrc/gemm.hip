@@ -569,13 +569,18 @@ size_t ws_bytes_for(int wf, int n_rows, int M, int K, int nmat) {
     return s > 1 ? (size_t)s * n_rows * nmat * M * sizeof(float) : 0;
 }
 
+// With defer set, the K-split partials are the result: they go to ws as
+// [splits][n_rows][NMAT][M] (a single split stores its product there as
+// split 0) and the sum is left to the consumer.
 template <int WF, int NMAT, int OP, bool XF32 = false>
-int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char* fn) {
+int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char* fn, bool defer = false) {
     a.splits = pick_splits(WF, a.n_rows, a.M, a.K, NMAT);
-    const size_t need = a.splits > 1 ? (size_t)a.splits * a.n_rows * NMAT * a.M * sizeof(float) : 0;
+    const size_t need =
+        a.splits > 1 || defer ? (size_t)a.splits * a.n_rows * NMAT * a.M * sizeof(float) : 0;
     MXD_REQUIRE(need == 0 || (ws && ws_bytes >= need), MXD_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)",
                 fn, need, ws_bytes);
     a.part = static_cast<float*>(ws);
+    if (defer && a.splits == 1) a.Y = a.part;
     a.row_tiles = (a.M + GM_ROWS / NMAT - 1) / (GM_ROWS / NMAT);
     a.batch_tiles = (a.n_rows + GM_BATCH - 1) / GM_BATCH;
     const int pairs = a.row_tiles * a.splits;
@@ -594,7 +599,7 @@ int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char
             }
             break;
     }
-    if (a.splits > 1) {
+    if (a.splits > 1 && !defer) {
         const size_t n = (size_t)a.n_rows * a.M;
         const size_t nb = (n + 255) / 256;
         const unsigned blocks = (unsigned)(nb < 4096 ? nb : 4096);
@@ -671,6 +676,38 @@ extern "C" int mxd_gemm_q8b32(const int8_t* Wq, const uint16_t* scales, const vo
     if (epilogue == MXD_EPI_ADD)
         return launch_gemm<MXD_W_Q8B32, 1, MXD_EPI_ADD>(a, workspace, ws_bytes, s, "mxd_gemm_q8b32");
     return launch_gemm<MXD_W_Q8B32, 1, MXD_EPI_STORE>(a, workspace, ws_bytes, s, "mxd_gemm_q8b32");
+}
+
+extern "C" size_t mxd_gemm_q8b32_partials_size(int n_rows, int M, int K) {
+    if (n_rows <= 0 || M <= 0 || K <= 0 || K % 32 != 0 || !use_mfma(MXD_W_Q8B32, n_rows, K)) return 0;
+    return (size_t)pick_splits(MXD_W_Q8B32, n_rows, M, K, 1) * n_rows * M * sizeof(float);
+}
+
+extern "C" int mxd_gemm_q8b32_partials(const int8_t* Wq, const uint16_t* scales, const void* X, int x_dtype,
+                                       float* part, size_t part_bytes, int n_rows, int M, int K, int* n_splits,
+                                       mxd_stream_t stream) {
+    if (int rc = check_common(Wq, scales, X, part, n_rows, M, K, "mxd_gemm_q8b32_partials")) return rc;
+    MXD_REQUIRE(n_splits, MXD_ERR_INVALID_ARG, "mxd_gemm_q8b32_partials: n_splits is null");
+    MXD_REQUIRE(x_dtype == MXD_F16 || x_dtype == MXD_F32, MXD_ERR_INVALID_ARG, "mxd_gemm_q8b32_partials: x_dtype %d",
+                x_dtype);
+    MXD_REQUIRE(use_mfma(MXD_W_Q8B32, n_rows, K), MXD_ERR_UNSUPPORTED,
+                "mxd_gemm_q8b32_partials: n_rows=%d K=%d is not a matrix-core product (16+ rows, K %% 128 == 0)",
+                n_rows, K);
+    GemmArgs a{};
+    a.W[0] = a.W[1] = Wq;
+    a.S[0] = a.S[1] = scales;
+    a.X = static_cast<const uint16_t*>(X);
+    a.Xf = static_cast<const float*>(X);
+    a.Y = part;
+    a.n_rows = n_rows;
+    a.M = M;
+    a.K = K;
+    *n_splits = pick_splits(MXD_W_Q8B32, n_rows, M, K, 1);
+    hipStream_t s = mxd::as_stream(stream);
+    if (x_dtype == MXD_F32)
+        return launch_gemm<MXD_W_Q8B32, 1, MXD_EPI_STORE, true>(a, part, part_bytes, s, "mxd_gemm_q8b32_partials",
+                                                                 true);
+    return launch_gemm<MXD_W_Q8B32, 1, MXD_EPI_STORE>(a, part, part_bytes, s, "mxd_gemm_q8b32_partials", true);
 }
 
 extern "C" int mxd_gemm_gate_up_q8b32(const int8_t* Wg, const uint16_t* sg, const int8_t* Wu, const uint16_t* su,

@@ -1,6 +1,8 @@
 // RMSNorm, embedding lookup, fp32->fp16 cast, and RoPE with KV-cache append.
 // These move kilobytes per decode step; they are latency-bound, so each is a
 // single small launch with no host synchronisation.
+#include <type_traits>
+
 #include "internal.hpp"
 
 namespace {
@@ -61,6 +63,119 @@ rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w, YT* __r
     }
     float ss = 0.0f;
     for (int i = threadIdx.x; i < D; i += NORM_THREADS) ss = fmaf(xr[i], xr[i], ss);
+    ss = block_sum(ss, scratch);
+    const float scale = rsqrtf(ss / (float)D + eps);
+    for (int i = threadIdx.x; i < D; i += NORM_THREADS) {
+        const float wi = PLUS_ONE ? 1.0f + w[i] : w[i];
+        yr[i] = (YT)(xr[i] * scale * wi);
+    }
+}
+
+// The sum of the K-split partials at element e (split stride `stride`),
+// added in split order from zero: the same order as the products' own
+// reduction, so the result is bit-identical to the summed output. With NS > 0
+// (the split count known at compile time) every load is issued before the
+// first add, one round trip in all; NS == 0 takes the runtime count n.
+template <int NS, typename T>
+__device__ __forceinline__ T split_sum(const float* __restrict__ part, int n, size_t stride, size_t e) {
+    T t{};
+    if constexpr (NS == 0) {
+        for (int sp = 0; sp < n; ++sp) t += *reinterpret_cast<const T*>(part + sp * stride + e);
+    } else {
+        T v[NS];
+#pragma unroll
+        for (int sp = 0; sp < NS; ++sp) v[sp] = *reinterpret_cast<const T*>(part + sp * stride + e);
+#pragma unroll
+        for (int sp = 0; sp < NS; ++sp) t += v[sp];
+    }
+    return t;
+}
+
+// Calls f(std::integral_constant<int, NS>) with NS = n for 1 <= n <= 8 and
+// NS = 0 (a runtime count) otherwise.
+template <typename F>
+int with_splits(int n, F&& f) {
+    switch (n) {
+        case 1: return f(std::integral_constant<int, 1>{});
+        case 2: return f(std::integral_constant<int, 2>{});
+        case 3: return f(std::integral_constant<int, 3>{});
+        case 4: return f(std::integral_constant<int, 4>{});
+        case 5: return f(std::integral_constant<int, 5>{});
+        case 6: return f(std::integral_constant<int, 6>{});
+        case 7: return f(std::integral_constant<int, 7>{});
+        case 8: return f(std::integral_constant<int, 8>{});
+        default: return f(std::integral_constant<int, 0>{});
+    }
+}
+
+// x[r] += sum of the K-split partials of a product's row r (the residual add
+// the product would have done), then y[r] = rmsnorm(x[r]) as rmsnorm_kernel
+// computes it (same loads per thread and the same reduction order), one
+// workgroup per row. All of a thread's loads go out before its first add.
+template <typename YT, bool PLUS_ONE, int NS, int NC>
+__global__ void __launch_bounds__(NORM_THREADS)
+rmsnorm_residual_sum_kernel(float* __restrict__ x, const float* __restrict__ part, int n_splits, size_t stride,
+                            const float* __restrict__ w, YT* __restrict__ y, int D, float eps) {
+    __shared__ float scratch[NORM_THREADS / 64];
+    const size_t r0 = (size_t)blockIdx.x * D;
+    float* xr = x + r0;
+    YT* yr = y + r0;
+    // NC 16-byte groups per thread (NC * 4 * NORM_THREADS >= D): rmsnorm_kernel's
+    // cached loop, whose groups past D add exact zeros to the sum of squares.
+    // Loads past D read the row's first group instead (no masked blocks, so
+    // every load is issued before the first wait) and are then zeroed.
+    if (NC > 0 && D % 4 == 0 && D <= NC * 4 * NORM_THREADS) {
+        constexpr int NU = NC > 0 ? NC : 1;
+        constexpr int NP = NS > 0 ? NS : 1;
+        f4_t v[NU];
+        f4_t pv[NU][NP];
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            const int i = (threadIdx.x + u * NORM_THREADS) * 4;
+            const int ic = i < D ? i : 0;
+            v[u] = *reinterpret_cast<const f4_t*>(xr + ic);
+            if constexpr (NS > 0) {
+#pragma unroll
+                for (int sp = 0; sp < NS; ++sp) pv[u][sp] = *reinterpret_cast<const f4_t*>(part + sp * stride + r0 + ic);
+            } else {
+                pv[u][0] = split_sum<0, f4_t>(part, n_splits, stride, r0 + ic);
+            }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            const int i = (threadIdx.x + u * NORM_THREADS) * 4;
+            f4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int sp = 0; sp < NP; ++sp) acc += pv[u][sp];
+            const f4_t t = v[u] + acc;
+            v[u] = i < D ? t : f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            if (i < D) *reinterpret_cast<f4_t*>(xr + i) = t;
+        }
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+            ss = fmaf(v[u].x, v[u].x, fmaf(v[u].y, v[u].y, fmaf(v[u].z, v[u].z, fmaf(v[u].w, v[u].w, ss))));
+        ss = block_sum(ss, scratch);
+        const float scale = rsqrtf(ss / (float)D + eps);
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            const int i = (threadIdx.x + u * NORM_THREADS) * 4;
+            if (i < D) {
+                const f4_t wv = *reinterpret_cast<const f4_t*>(w + i);
+                const float xs[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+                const float ws[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) yr[i + e] = (YT)(xs[e] * scale * (PLUS_ONE ? 1.0f + ws[e] : ws[e]));
+            }
+        }
+        return;
+    }
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < D; i += NORM_THREADS) {
+        const float t = xr[i] + split_sum<NS, float>(part, n_splits, stride, r0 + i);
+        xr[i] = t;
+        ss = fmaf(t, t, ss);
+    }
     ss = block_sum(ss, scratch);
     const float scale = rsqrtf(ss / (float)D + eps);
     for (int i = threadIdx.x; i < D; i += NORM_THREADS) {
@@ -167,6 +282,79 @@ rope_kv_paged_kernel(float* __restrict__ qkv, uint16_t* __restrict__ kpool, uint
         vpool[slab + mxd::v_page_offset(r, p)] = mxd::f2h_bits(vv[p]);
         vpool[slab + mxd::v_page_offset(r, p + half_d)] = mxd::f2h_bits(vv[p + half_d]);
     }
+}
+
+// rope_kv_paged_kernel over the K-split partials of the q|k|v product (split
+// stride `stride` floats, rows of (n_heads + 2 n_kv) * hd): each value is the
+// partials' sum in split order (bit-identical to the summed product), the
+// rotated q goes to qkv (the only part of qkv the attention reads) and k, v
+// to the pages. A row whose position or page is out of range gets its q
+// unrotated, as rope_kv_paged leaves it. A thread's partial loads (its q or k
+// pair, and the v pair for a kv head) all go out before the first add.
+template <int NS>
+__global__ void __launch_bounds__(256)
+rope_kv_paged_sum_kernel(const float* __restrict__ part, int n_splits, size_t stride, float* __restrict__ qkv,
+                         uint16_t* __restrict__ kpool, uint16_t* __restrict__ vpool,
+                         const float* __restrict__ inv_freq, int n_heads, int n_kv, int hd,
+                         const int32_t* __restrict__ page_table, int max_pages, const int32_t* __restrict__ seq_lens,
+                         int n_pages) {
+    const int half_d = hd >> 1;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;  // pair index over heads
+    const int b = blockIdx.y;                              // sequence
+    const int h = i / half_d, p = i - h * half_d;
+    if (h >= n_heads + n_kv) return;
+    const bool kv = h >= n_heads;
+    const size_t row = (size_t)b * (n_heads + 2 * n_kv) * hd;
+    const size_t e0 = row + (size_t)h * hd + p;
+    const size_t v0 = row + (size_t)(h + n_kv) * hd + p;  // the v pair of kv head h - n_heads
+    float x0, x1, y0 = 0.0f, y1 = 0.0f;
+    if constexpr (NS > 0) {
+        // v0 lies inside the row for every head (h + n_kv < n_heads + 2 n_kv), so
+        // the v loads need no branch; q heads ignore them
+        float a[NS], c[NS], va[NS], vc[NS];
+#pragma unroll
+        for (int sp = 0; sp < NS; ++sp) {
+            a[sp] = part[sp * stride + e0];
+            c[sp] = part[sp * stride + e0 + half_d];
+            va[sp] = part[sp * stride + v0];
+            vc[sp] = part[sp * stride + v0 + half_d];
+        }
+        x0 = 0.0f, x1 = 0.0f;
+#pragma unroll
+        for (int sp = 0; sp < NS; ++sp) x0 += a[sp], x1 += c[sp], y0 += va[sp], y1 += vc[sp];
+    } else {
+        x0 = split_sum<0, float>(part, n_splits, stride, e0);
+        x1 = split_sum<0, float>(part, n_splits, stride, e0 + half_d);
+        if (kv) {
+            y0 = split_sum<0, float>(part, n_splits, stride, v0);
+            y1 = split_sum<0, float>(part, n_splits, stride, v0 + half_d);
+        }
+    }
+    const int pos = seq_lens[b] - 1;
+    const int phys = pos >= 0 && pos < max_pages * mxd::PAGE_KEYS ? page_table[(size_t)b * max_pages + (pos >> 4)] : -1;
+    if (phys < 0 || phys >= n_pages) {
+        if (!kv) {
+            qkv[e0] = x0;
+            qkv[e0 + half_d] = x1;
+        }
+        return;
+    }
+    const float ang = (float)pos * inv_freq[p];
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    const float ra = x0 * cs - x1 * sn;
+    const float rb = x1 * cs + x0 * sn;
+    if (!kv) {
+        qkv[e0] = ra;
+        qkv[e0 + half_d] = rb;
+        return;
+    }
+    const int kvh = h - n_heads, r = pos & (mxd::PAGE_KEYS - 1);
+    const size_t slab = ((size_t)phys * n_kv + kvh) * mxd::PAGE_KEYS * hd;
+    kpool[slab + mxd::k_page_offset(r, p)] = mxd::f2h_bits(ra);
+    kpool[slab + mxd::k_page_offset(r, p + half_d)] = mxd::f2h_bits(rb);
+    vpool[slab + mxd::v_page_offset(r, p)] = mxd::f2h_bits(y0);
+    vpool[slab + mxd::v_page_offset(r, p + half_d)] = mxd::f2h_bits(y1);
 }
 
 // ---- Gemma-4 operators --------------------------------------------------------
@@ -371,6 +559,71 @@ extern "C" int mxd_rope_kv_paged(float* qkv, uint16_t* kpool, uint16_t* vpool, i
                        qkv, kpool, vpool, inv_freq, n_heads, n_kv_heads, head_dim, page_table, max_pages, seq_lens,
                        n_pages);
     return mxd::check_launch("mxd_rope_kv_paged");
+}
+
+extern "C" int mxd_rope_kv_paged_sum(const float* part, int n_splits, float* qkv, uint16_t* kpool, uint16_t* vpool,
+                                     int n_pages, const float* inv_freq, int n_heads, int n_kv_heads, int head_dim,
+                                     const int32_t* page_table, int max_pages, const int32_t* seq_lens, int n_seqs,
+                                     mxd_stream_t stream) {
+    MXD_REQUIRE(part && qkv && kpool && vpool && inv_freq && page_table && seq_lens, MXD_ERR_INVALID_ARG,
+                "mxd_rope_kv_paged_sum: null pointer");
+    MXD_REQUIRE(n_splits >= 1, MXD_ERR_INVALID_ARG, "mxd_rope_kv_paged_sum: n_splits=%d", n_splits);
+    MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_seqs > 0 && n_seqs <= 65535 && n_pages > 0 && max_pages > 0,
+                MXD_ERR_INVALID_ARG, "mxd_rope_kv_paged_sum: n_heads=%d n_kv_heads=%d n_seqs=%d n_pages=%d max_pages=%d",
+                n_heads, n_kv_heads, n_seqs, n_pages, max_pages);
+    MXD_REQUIRE(head_dim > 0 && head_dim % 32 == 0, MXD_ERR_UNSUPPORTED,
+                "mxd_rope_kv_paged_sum: head_dim=%d must be a multiple of 32 (page slab layout)", head_dim);
+    const int pairs = (n_heads + n_kv_heads) * (head_dim / 2);
+    const size_t stride = (size_t)n_seqs * (n_heads + 2 * n_kv_heads) * head_dim;
+    return with_splits(n_splits, [&](auto ns) {
+        hipLaunchKernelGGL(rope_kv_paged_sum_kernel<decltype(ns)::value>, dim3((pairs + 255) / 256, n_seqs), dim3(256),
+                           0, mxd::as_stream(stream), part, n_splits, stride, qkv, kpool, vpool, inv_freq, n_heads,
+                           n_kv_heads, head_dim, page_table, max_pages, seq_lens, n_pages);
+        return mxd::check_launch("mxd_rope_kv_paged_sum");
+    });
+}
+
+extern "C" int mxd_rmsnorm_residual_sum(float* x, const float* part, int n_splits, const float* w, void* y,
+                                        int y_dtype, int rows, int D, float eps, int plus_one, mxd_stream_t stream) {
+    MXD_REQUIRE(x && part && w && y, MXD_ERR_INVALID_ARG, "mxd_rmsnorm_residual_sum: null pointer");
+    MXD_REQUIRE(n_splits >= 1, MXD_ERR_INVALID_ARG, "mxd_rmsnorm_residual_sum: n_splits=%d", n_splits);
+    MXD_REQUIRE(rows > 0 && D > 0, MXD_ERR_INVALID_ARG, "mxd_rmsnorm_residual_sum: rows=%d D=%d must be positive", rows,
+                D);
+    MXD_REQUIRE(((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(part) | reinterpret_cast<uintptr_t>(w)) &
+                 15) == 0,
+                MXD_ERR_UNSUPPORTED, "mxd_rmsnorm_residual_sum: x, part and w must be 16-byte aligned");
+    MXD_REQUIRE(y_dtype == MXD_F32 || y_dtype == MXD_F16, MXD_ERR_INVALID_ARG, "mxd_rmsnorm_residual_sum: y_dtype %d",
+                y_dtype);
+    hipStream_t s = mxd::as_stream(stream);
+    const dim3 grid(rows), block(NORM_THREADS);
+    const size_t stride = (size_t)rows * D;
+    // groups per thread of the cached loop: 4 up to D = 4096, 8 up to 8192
+    // (rmsnorm_kernel's range), else the plain two-pass loop
+    const int nc = D % 4 != 0 ? 0 : D <= 4 * 4 * NORM_THREADS ? 4 : D <= NORM_CACHE * 4 * NORM_THREADS ? 8 : 0;
+    auto go = [&](auto ns, auto ncc) {
+        constexpr int NS = decltype(ns)::value, NC = decltype(ncc)::value;
+        if (y_dtype == MXD_F32) {
+            if (plus_one)
+                hipLaunchKernelGGL((rmsnorm_residual_sum_kernel<float, true, NS, NC>), grid, block, 0, s, x, part,
+                                   n_splits, stride, w, (float*)y, D, eps);
+            else
+                hipLaunchKernelGGL((rmsnorm_residual_sum_kernel<float, false, NS, NC>), grid, block, 0, s, x, part,
+                                   n_splits, stride, w, (float*)y, D, eps);
+        } else {
+            if (plus_one)
+                hipLaunchKernelGGL((rmsnorm_residual_sum_kernel<_Float16, true, NS, NC>), grid, block, 0, s, x, part,
+                                   n_splits, stride, w, (_Float16*)y, D, eps);
+            else
+                hipLaunchKernelGGL((rmsnorm_residual_sum_kernel<_Float16, false, NS, NC>), grid, block, 0, s, x, part,
+                                   n_splits, stride, w, (_Float16*)y, D, eps);
+        }
+        return mxd::check_launch("mxd_rmsnorm_residual_sum");
+    };
+    return with_splits(n_splits, [&](auto ns) {
+        if (nc == 4) return go(ns, std::integral_constant<int, 4>{});
+        if (nc == 8) return go(ns, std::integral_constant<int, 8>{});
+        return go(ns, std::integral_constant<int, 0>{});
+    });
 }
 
 // ---- Gemma-4 entry points -------------------------------------------------------

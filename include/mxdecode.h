@@ -168,6 +168,15 @@ int mxd_matvec_f16_attn_merge_window(const uint16_t* W, const float* partials, i
 int mxd_rmsnorm(const float* x, const float* w, void* y, int y_dtype, int rows, int D, float eps,
                 int plus_one, mxd_stream_t stream);
 
+/* x[r] += the sum of a product's K-split partials for row r (part: n_splits x
+ * [rows][D], as mxd_gemm_q8b32_partials leaves them; summed in split order,
+ * bit-identical to mxd_gemm_q8b32 with MXD_EPI_ADD), then y = rmsnorm(x) as
+ * mxd_rmsnorm computes it. x, part, w 16-byte aligned. Fuses the residual
+ * add of gemm_f16_add (KL/kernels.metal:389-441) with the rmsnorm that
+ * follows it in the batched layer (KL/main.swift:422-428). */
+int mxd_rmsnorm_residual_sum(float* x, const float* part, int n_splits, const float* w, void* y, int y_dtype,
+                             int rows, int D, float eps, int plus_one, mxd_stream_t stream);
+
 /* x[r][i] = float(E[tokens[pos + r]][i]) * scale for r < rows. Replaces embed
  * (KL/kernels.metal:31-39) and embed_rows (KG/kernels.metal:34-42); the token
  * index is read on the device, so a sampled token feeds the next step without
@@ -344,6 +353,18 @@ int mxd_rope_kv_paged(float* qkv, uint16_t* kpool, uint16_t* vpool, int n_pages,
                       int n_heads, int n_kv_heads, int head_dim, const int32_t* page_table, int max_pages,
                       const int32_t* seq_lens, int n_seqs, mxd_stream_t stream);
 
+/* mxd_rope_kv_paged fused with the sum of the q|k|v product's K-split
+ * partials (part: n_splits x [n_seqs][(n_heads + 2 n_kv_heads) head_dim], as
+ * mxd_gemm_q8b32_partials leaves them): each value is the partials' sum in
+ * split order, bit-identical to mxd_gemm_q8b32's output, so the product needs
+ * no summing launch. Only the q part of qkv is written (rotated), which is all
+ * mxd_attention_paged reads of it. Fuses the reference's rope_kv
+ * (KL/kernels.metal:182-224) with the sum it takes for granted. */
+int mxd_rope_kv_paged_sum(const float* part, int n_splits, float* qkv, uint16_t* kpool, uint16_t* vpool,
+                          int n_pages, const float* inv_freq, int n_heads, int n_kv_heads, int head_dim,
+                          const int32_t* page_table, int max_pages, const int32_t* seq_lens, int n_seqs,
+                          mxd_stream_t stream);
+
 /* Workspace bytes mxd_attention_paged needs (max_keys bounds every seq_lens).
  * The size follows the schedule the call will use: up to 2048 sequences the
  * batch's (sequence, kv head, block) items are dealt evenly over the
@@ -377,6 +398,19 @@ size_t mxd_gemm_q8b32_workspace_size(int n_rows, int M, int K);
 int mxd_gemm_q8b32(const int8_t* Wq, const uint16_t* scales, const void* X, int x_dtype, float* Y,
                    int n_rows, int M, int K, int epilogue, void* workspace, size_t ws_bytes,
                    mxd_stream_t stream);
+
+/* Bytes of the K-split partials mxd_gemm_q8b32_partials leaves (0 below 16
+ * rows or when K % 128 != 0, where it does not apply). */
+size_t mxd_gemm_q8b32_partials_size(int n_rows, int M, int K);
+
+/* mxd_gemm_q8b32 (MXD_EPI_STORE) on the matrix cores with the K-split sum
+ * left to the consumer: part receives *n_splits partial products
+ * [n_splits][n_rows][M] (a single split is the product itself), which
+ * mxd_rope_kv_paged_sum and mxd_rmsnorm_residual_sum add as they load them.
+ * Needs n_rows >= 16 and K % 128 == 0. The reference's gemm_f16
+ * (KL/kernels.metal:376-441) with its reduction deferred to the next op. */
+int mxd_gemm_q8b32_partials(const int8_t* Wq, const uint16_t* scales, const void* X, int x_dtype, float* part,
+                            size_t part_bytes, int n_rows, int M, int K, int* n_splits, mxd_stream_t stream);
 
 /* Workspace bytes mxd_gemm_gate_up_q8b32 needs (0 when it does not split K). */
 size_t mxd_gemm_gate_up_q8b32_workspace_size(int n_rows, int F, int K);

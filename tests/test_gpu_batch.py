@@ -263,6 +263,109 @@ def test_gemm_gate_up_q8b32(dev, rng, rows, act):
             _lib.set_tunable("GM_SPLITS", 0)
 
 
+@pytest.mark.parametrize("rows,M,K,xdt", [(16, 6144, 4096, F16), (64, 4096, 4096, F32), (64, 4096, 14336, F32),
+                                           (37, 300, 1024, F16), (100, 257, 640, F32)])
+def test_gemm_q8b32_partials_sum_to_the_product(dev, rng, rows, M, K, xdt):
+    """The unsummed K-split partials, added in split order from zero, are
+    bit-identical to the summing product (store and add epilogues)."""
+    B = _bm()
+    q, s = _qweights(rng, M, K)
+    X = rng.standard_normal((rows, K), dtype=F32).astype(xdt)
+    qd, sd, Xd = _d(q, dev), _d(s, dev), _d(X, dev)
+    part = torch.empty(B.gemm_q8b32_partials_bytes(rows, M, K) // 4, dtype=torch.float32, device=dev)
+    n = B.gemm_q8b32_partials(qd, sd, Xd, part)
+    assert n >= 1 and part.numel() == n * rows * M
+    P = part.cpu().numpy().reshape(n, rows, M)
+    acc = np.zeros((rows, M), F32)
+    for sp in range(n):
+        acc = acc + P[sp]
+    assert np.array_equal(acc, B.gemm_q8b32(qd, sd, Xd).cpu().numpy())
+    base = rng.standard_normal((rows, M), dtype=F32)
+    Y = _d(base, dev)
+    B.gemm_q8b32(qd, sd, Xd, Y, "add")
+    assert np.array_equal(base + acc, Y.cpu().numpy())
+
+
+def test_gemm_q8b32_partials_rejects_small_batches(dev, rng):
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
+    B = _bm()
+    q, s = _qweights(rng, 64, 256)
+    X = _d(rng.standard_normal((15, 256), dtype=F32).astype(F16), dev)
+    assert B.gemm_q8b32_partials_bytes(15, 64, 256) == 0
+    with pytest.raises(_lib.MxdValueError):
+        B.gemm_q8b32_partials(_d(q, dev), _d(s, dev), X, torch.empty(64 * 15, dtype=torch.float32, device=dev))
+
+
+def test_ops_that_add_partials_match_the_summing_path(dev, rng):
+    """rope_kv_paged_sum and rmsnorm_residual_sum over a product's partials give
+    bit for bit what the summing product followed by rope_kv_paged / rmsnorm
+    gives (q, the appended k and v, the residual and the normed rows)."""
+    from gemmagemini4hackathon2026_10_2425_amd import ops
+
+    B = _bm()
+    nh, nkv, hd, D = 8, 2, 128, 1024
+    lens = [int(n) for n in np.random.default_rng(7).integers(1, 200, 18)] + [1, 16]  # 20 rows: matrix cores
+    rows, QKV = len(lens), (nh + 2 * nkv) * hd
+    invf = _d(ref.inv_freq(hd, 10000.0), dev)
+    seq = _d(np.array(lens, np.int32), dev)
+    q, s = _qweights(rng, QKV, D)
+    qd, sd = _d(q, dev), _d(s, dev)
+    xn = _d(rng.standard_normal((rows, D), dtype=F32).astype(F16), dev)
+    part = torch.empty(B.gemm_q8b32_partials_bytes(rows, QKV, D) // 4, dtype=torch.float32, device=dev)
+    n = B.gemm_q8b32_partials(qd, sd, xn, part)
+    caches = []
+    for _ in range(2):
+        table, n_pages = B.pack_ragged(lens, seed=9)
+        caches.append(B.PagedCache(1, nkv, hd, table, n_pages, device=dev))
+    qkv_a = torch.zeros((rows, QKV), dtype=torch.float32, device=dev)
+    B.rope_kv_paged_sum(part, n, qkv_a, caches[0].k[0], caches[0].v[0], invf, nh, nkv, caches[0].table, seq)
+    qkv_b = B.gemm_q8b32(qd, sd, xn)
+    B.rope_kv_paged(qkv_b, caches[1].k[0], caches[1].v[0], invf, nh, nkv, caches[1].table, seq)
+    torch.cuda.synchronize()
+    assert torch.equal(qkv_a[:, : nh * hd], qkv_b[:, : nh * hd])
+    assert torch.equal(caches[0].k, caches[1].k) and torch.equal(caches[0].v, caches[1].v)
+
+    qo, so = _qweights(rng, D, nh * hd)
+    att = _d(rng.standard_normal((rows, nh * hd), dtype=F32), dev)
+    w = _d((1.0 + 0.02 * rng.standard_normal(D)).astype(F32), dev)
+    X = rng.standard_normal((rows, D), dtype=F32)
+    part_o = torch.empty(B.gemm_q8b32_partials_bytes(rows, D, nh * hd) // 4, dtype=torch.float32, device=dev)
+    no = B.gemm_q8b32_partials(_d(qo, dev), _d(so, dev), att, part_o)
+    for plus_one, ydt in ((False, torch.float16), (True, torch.float32)):
+        Xa, Xb = _d(X, dev), _d(X, dev)
+        ya = torch.empty((rows, D), dtype=ydt, device=dev)
+        B.rmsnorm_residual_sum(Xa, part_o, no, w, 1e-5, plus_one, ya)
+        B.gemm_q8b32(_d(qo, dev), _d(so, dev), att, Xb, "add")
+        yb = ops.rmsnorm(Xb, w, 1e-5, plus_one, out_dtype=ydt)
+        assert torch.equal(Xa, Xb) and torch.equal(ya, yb)
+
+
+def test_ragged_layer_fold_sums_is_bit_exact(dev):
+    """The layer step with the qkv and o sums folded into the next ops equals
+    the step with summing products, bit for bit (residual rows and pools)."""
+    from gemmagemini4hackathon2026_10_2425_amd import ops
+
+    B = _bm()
+    shape = B.LayerShape(dim=512, n_heads=8, n_kv_heads=2, head_dim=128, ffn_dim=1024)
+    lens = [int(n) for n in np.random.default_rng(8).integers(1, 300, 24)]
+    W = B.random_layer_weights(shape, 8)
+    X = np.random.default_rng(8).standard_normal((len(lens), shape.dim), dtype=F32)
+    out = []
+    for fold in (True, False):
+        table, n_pages = B.pack_ragged(lens, seed=8)
+        cache = B.PagedCache(1, shape.n_kv_heads, shape.head_dim, table, n_pages, device=dev)
+        for pool, tid in ((cache.k, 1), (cache.v, 2)):
+            pool.copy_(ops.fill_normal(tuple(pool.shape), torch.float16, 8, tid, 1.0, dev))
+        layer = B.RaggedLayerQ8(shape, W, max_batch=len(lens), max_keys=max(lens), device=dev, fold_sums=fold)
+        Xd = _d(X, dev)
+        layer.step(Xd, cache.k[0], cache.v[0], cache.table, _d(np.array(lens, np.int32), dev))
+        torch.cuda.synchronize()
+        out.append((Xd.cpu(), cache.k.cpu(), cache.v.cpu()))
+    for a, b in zip(*out):
+        assert torch.equal(a, b)
+
+
 def _layer_parity(dev, shape, lens, seed):
     """Step a ragged batch through RaggedLayerQ8 and through the oracle; compare
     the new residual rows and every sequence's appended K/V."""
