@@ -254,8 +254,17 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
     {
         // One 32-key block per wave (4 waves per split) over the whole
         // context; folded into the o projection while that is at most 8
-        // splits (contexts of up to 1024 keys) and more than one.
-        const int splits = ((max_ctx + 31) / 32 + 3) / 4;
+        // splits (contexts of up to 1024 keys) and more than one. A folded
+        // attention takes at least ENG_ATT_SPLITS (default 6) splits: spread
+        // over more workgroups, the same blocks finish sooner (Gemma-2B at
+        // max_ctx 384, measured on MI355X: 858-859 tok/s with 6 or 8 splits
+        // against 849-850 with the 3 one block per wave needs).
+        // ENG_ATT_FOLD = 3 also folds longer contexts, as 8 splits (at
+        // max_ctx 4096: 861 against 814 tok/s at 129-384 keys, but 760
+        // against 816 at 3584-3840 keys, where each wave walks ~4 blocks).
+        int splits = ((max_ctx + 31) / 32 + 3) / 4;
+        if (mxd::tunable("ENG_ATT_FOLD", 1) == 3 && splits > 8) splits = 8;
+        if (splits >= 2 && splits <= 8) splits = max(splits, min(8, mxd::tunable("ENG_ATT_SPLITS", 6)));
         e->att_splits = splits >= 2 && splits <= 8 && mxd::tunable("ENG_ATT_FOLD", 1) != 2 ? splits : 0;
         const size_t need = (size_t)splits * c.n_heads * (c.head_dim + 2) * sizeof(float);
         if (e->att_splits && e->attn_ws_bytes < need) e->attn_ws_bytes = need;

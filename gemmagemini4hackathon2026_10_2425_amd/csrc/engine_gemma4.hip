@@ -338,7 +338,9 @@ extern "C" int mxd_engine_create_gemma4(const mxd_gemma4_config* cfg, int max_ct
     // The decode attention leaves its splits' partials for the o projection
     // to merge when a layer sees at most 8 x 4 blocks (one 32-key block per
     // wave, 2 to 8 splits; ENG_ATT_FOLD = 2: never), as the Gemma-2B step
-    // does; sliding layers see at most window + 32 keys of the cache.
+    // does, with at least ENG_ATT_SPLITS (default 6) splits (E2B at max_ctx
+    // 384: 541-542 tok/s against 537); sliding layers see at most
+    // window + 32 keys of the cache.
     e->g4_splits.assign(L, 0);
     for (int l = 0; l < L; ++l) {
         const mxd_gemma4_layer& y = e->g4l[l];
@@ -347,7 +349,8 @@ extern "C" int mxd_engine_create_gemma4(const mxd_gemma4_config* cfg, int max_ct
         max_f = max(max_f, y.ffn_dim);
         e->attn_ws_bytes = max(e->attn_ws_bytes, mxd_attention_workspace_size(NH, NKV, y.head_dim, max_ctx));
         const int keys = y.sliding && c.window > 0 ? min(max_ctx, c.window + 32) : max_ctx;
-        const int S = ((keys + 31) / 32 + 3) / 4;
+        int S = ((keys + 31) / 32 + 3) / 4;
+        if (S >= 2 && S <= 8) S = max(S, min(8, mxd::tunable("ENG_ATT_SPLITS", 6)));
         if (S >= 2 && S <= 8 && mxd::tunable("ENG_ATT_FOLD", 1) != 2) {
             e->g4_splits[l] = S;
             e->attn_ws_bytes = max(e->attn_ws_bytes, (size_t)S * NH * (y.head_dim + 2) * sizeof(float));
