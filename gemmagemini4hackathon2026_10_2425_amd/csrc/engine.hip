@@ -16,7 +16,7 @@
 // argmax advances, so the same graph serves every position.
 //
 // Prefill (prefill(n:useGemm:), KL/main.swift:357-372, 412-446) runs the
-// prompt in chunks of up to PREFILL_ROWS rows through the matrix-core
+// prompt in chunks of up to prefill_rows() rows through the matrix-core
 // products, the causal multi-query attention and row-batched norm / RoPE /
 // cast kernels, with the reference's fp16 activation points; the last row of
 // the last chunk goes through the decode path's LM head and argmax. The
@@ -288,7 +288,7 @@ extern "C" int mxd_engine_create(const mxd_model_config* cfg, int max_ctx, mxd_e
     const size_t o_invf = take((size_t)c.head_dim / 2 * 4), o_tok = take(((size_t)max_ctx + 1) * 4), o_pos = take(4);
     const size_t o_aws = take(e->attn_ws_bytes), o_am = take(mxd_argmax_workspace_size(c.vocab));
     const size_t o_abws = take(max(e->ab_ws_bytes, (size_t)16)), o_step = take(4);
-    const size_t B = (size_t)(e->max_rows = min(PREFILL_ROWS, max_ctx));
+    const size_t B = (size_t)(e->max_rows = min(prefill_rows(), max_ctx));
     e->gm_ws_bytes = prefill_ws_bytes(c, e->qkv_dim(), e->q_dim(), e->max_rows);
     const size_t o_bx = take(B * D * 4), o_bxn = take(B * D * 2), o_bqkv = take(B * e->qkv_dim() * 4);
     const size_t o_batt = take(B * e->q_dim() * 4);

@@ -368,7 +368,7 @@ extern "C" int mxd_engine_create_gemma4(const mxd_gemma4_config* cfg, int max_ct
     const size_t o_invf = take((size_t)L * G4_FREQS * 4), o_tok = take(((size_t)max_ctx + 1) * 4), o_pos = take(4);
     const size_t o_aws = take(e->attn_ws_bytes), o_am = take(mxd_argmax_workspace_size(c.vocab)), o_step = take(4);
     // prefill chunk buffers
-    const size_t B = (size_t)(e->max_rows = min(PREFILL_ROWS, max_ctx));
+    const size_t B = (size_t)(e->max_rows = min(prefill_rows(), max_ctx));
     e->gm_ws_bytes = g4_prefill_ws_bytes(e, e->max_rows);
     const size_t o_bx = take(B * D * 4), o_bxn = take(B * D * 2), o_bqkv = take(B * max_qkv * 4);
     const size_t o_batt = take(B * max_q * 4), o_bh = take(B * max_f * 4), o_btmp = take(B * D * 4);

@@ -519,11 +519,14 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a) {
     }
 }
 
-// int8 weights need whole 128-k chunks (the runtime loop takes any count);
-// fp16 weights run only the unrolled kernel, so K must split into chunks of
-// at least 4 (K % 512 == 0).
+// Both weight formats need whole 128-k chunks: int8 runs any chunk count
+// (the runtime loop takes the ones the unrolled kernel does not), fp16 runs
+// the unrolled kernel only, with 1 or 2 chunks per workgroup where 4 does not
+// divide the count (K = 128, 256, 384, ...: Gemma-4's per-layer-input
+// projection back to the model width has K = 256).
 bool use_mfma(int wf, int n_rows, int K) {
-    return n_rows >= mxd::tunable("GM_MIN_ROWS", 16) && K % (wf == MXD_W_F16 ? 4 * GM2_CK : GM2_CK) == 0;
+    (void)wf;
+    return n_rows >= mxd::tunable("GM_MIN_ROWS", 16) && K % GM2_CK == 0;
 }
 
 // Chunks per workgroup of the unrolled kernel: the largest of 32, 16, 8, 4
@@ -549,6 +552,7 @@ int pick_nch(int wf, int n_rows, int M, int K, int nmat) {
         if (tiles * (nck / nch) >= 128) return nch;
         best = nch;
     }
+    if (!best && wf == MXD_W_F16) best = nck % 2 == 0 ? 2 : 1;  // fp16 has no runtime loop
     return best;
 }
 
@@ -591,6 +595,16 @@ int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char
         case 8: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 8, XF32>), grid, dim3(GM_THREADS), 0, s, a); break;
         case 16: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 16, XF32>), grid, dim3(GM_THREADS), 0, s, a); break;
         case 32: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 32, XF32>), grid, dim3(GM_THREADS), 0, s, a); break;
+        case 2:
+        case 1:
+            if constexpr (WF == MXD_W_F16) {
+                if (nch == 2)
+                    hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 2, XF32>), grid, dim3(GM_THREADS), 0, s, a);
+                else
+                    hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 1, XF32>), grid, dim3(GM_THREADS), 0, s, a);
+                break;
+            }
+            [[fallthrough]];
         default:
             if constexpr (WF == MXD_W_Q8B32) {
                 hipLaunchKernelGGL((gemm_q8_loop_kernel<NMAT, OP, XF32>), grid, dim3(GM_THREADS), 0, s, a);
@@ -762,7 +776,7 @@ extern "C" int mxd_gemm_f16(const uint16_t* W, const void* X, int x_dtype, float
                 "mxd_gemm_f16: epilogue %d (store or add)", epilogue);
     MXD_REQUIRE(x_dtype == MXD_F16 || x_dtype == MXD_F32, MXD_ERR_INVALID_ARG, "mxd_gemm_f16: x_dtype %d", x_dtype);
     const size_t xesz = x_dtype == MXD_F32 ? 4 : 2;
-    if (!use_mfma(MXD_W_F16, n_rows, K)) {  // few rows or K % 512: one matvec per row (fp32 X rounded the same way)
+    if (!use_mfma(MXD_W_F16, n_rows, K)) {  // few rows or K % 128: one matvec per row (fp32 X rounded the same way)
         for (int b = 0; b < n_rows; ++b) {
             const void* xb = static_cast<const char*>(X) + (size_t)b * K * xesz;
             const int rc = x_dtype == MXD_F32

@@ -427,7 +427,7 @@ size_t mxd_gemm_f16_workspace_size(int n_rows, int M, int K);
 /* Y[b] (op)= W · X[b] for fp16 W [M][K] and the n_rows rows of X [n_rows][K]
  * (x_dtype MXD_F16, or MXD_F32 rounded to nearest-even fp16 as it is loaded);
  * Y fp32 [n_rows][M]; epilogue MXD_EPI_STORE or MXD_EPI_ADD; fp32
- * accumulation. From 16 rows on (and K % 512 == 0) this runs on the matrix
+ * accumulation. From 16 rows on (and K % 128 == 0) this runs on the matrix
  * cores; below, one matvec per row. Replaces gemm_f16 / gemm_f16_add
  * (KL/kernels.metal:376-441; host gemm KL/main.swift:397-410), the prefill
  * products; fp32 X folds the f32_to_f16 cast before them (KL/main.swift:448-454). */

@@ -108,21 +108,24 @@ def test_engine_steps_match_oracle(dev, cfg, attn_mode):
         assert e.tokens(0, n) == [int(t) for t in ref.tokens[:n]]
 
 
-PREFILL_ROWS = 256  # the engine's prefill chunk
+PREFILL_ROWS = 256  # the prefill chunk these tests set (ENG_PREFILL_ROWS), so prompts span chunks
+DEFAULT_PREFILL_ROWS = 1024  # the engine's default chunk
 
 
 @pytest.fixture(params=["batched", "tokenwise"])
 def prefill_mode(request):
-    """Batched prefill (default: matrix-core products, fp16 activation rows) or
-    token by token through the decode path (ENG_NO_GEMM, the reference's
-    --no-gemm); the oracle runs the same mode."""
+    """Batched prefill (default: matrix-core products, fp16 activation rows;
+    chunks of PREFILL_ROWS) or token by token through the decode path
+    (ENG_NO_GEMM, the reference's --no-gemm); the oracle runs the same mode."""
     from gemmagemini4hackathon2026_10_2425_amd import _lib
 
     _lib.set_tunable("ENG_NO_GEMM", 1 if request.param == "tokenwise" else 0)
+    _lib.set_tunable("ENG_PREFILL_ROWS", PREFILL_ROWS)
     try:
         yield request.param
     finally:
         _lib.set_tunable("ENG_NO_GEMM", 0)
+        _lib.set_tunable("ENG_PREFILL_ROWS", 0)
 
 
 # (config, prompt length, seed, weight std, embedding std). With every weight
@@ -147,27 +150,36 @@ def test_engine_generate_matches_oracle(dev, cfg, P, seed, std, embed_std, prefi
 
 
 @pytest.mark.parametrize("cfg", CONFIGS, ids=CONFIG_IDS)
-def test_engine_batched_prefill_logits(dev, cfg):
+@pytest.mark.parametrize("chunk", [PREFILL_ROWS, None], ids=["chunk256", "default-chunk"])
+def test_engine_batched_prefill_logits(dev, cfg, chunk):
     """The last prompt row's logits after a batched prefill equal the oracle's
     batched prefill (same fp16 activation points), for one chunk and for a
-    prompt split over two chunks, and the K/V it appended serve the next step."""
+    prompt split over two chunks (256-row chunks), and the K/V it appended
+    serve the next step."""
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
     seed, max_ctx = 13, 320
-    for P in (17, 270):
-        prompt = [int(t) for t in np.random.default_rng(P).integers(0, cfg.vocab, P)]
-        ref = om.OracleDecoder(cfg, om.make_weights(cfg, seed), max_ctx)
-        ref.tokens[:P] = prompt
-        done = 0
-        while done < P:
-            rows = min(PREFILL_ROWS, P - done)
-            want = ref.prefill_chunk(done, rows, sample=done + rows == P)
-            done += rows
-        with _engine(cfg, max_ctx, seed) as e:
-            e.set_tokens(prompt)
-            e.prefill(P)
-            assert rel_err(e.logits(), want) <= 1e-3, f"P {P}"
-            assert e.token(P) == int(ref.tokens[P])
-            e.step(P)
-            assert rel_err(e.logits(), ref.forward(P)) <= 1e-3, f"step after prefill, P {P}"
+    rows_per_chunk = chunk or DEFAULT_PREFILL_ROWS
+    _lib.set_tunable("ENG_PREFILL_ROWS", chunk or 0)
+    try:
+        for P in (17, 270):
+            prompt = [int(t) for t in np.random.default_rng(P).integers(0, cfg.vocab, P)]
+            ref = om.OracleDecoder(cfg, om.make_weights(cfg, seed), max_ctx)
+            ref.tokens[:P] = prompt
+            done = 0
+            while done < P:
+                rows = min(rows_per_chunk, P - done)
+                want = ref.prefill_chunk(done, rows, sample=done + rows == P)
+                done += rows
+            with _engine(cfg, max_ctx, seed) as e:
+                e.set_tokens(prompt)
+                e.prefill(P)
+                assert rel_err(e.logits(), want) <= 1e-3, f"P {P}"
+                assert e.token(P) == int(ref.tokens[P])
+                e.step(P)
+                assert rel_err(e.logits(), ref.forward(P)) <= 1e-3, f"step after prefill, P {P}"
+    finally:
+        _lib.set_tunable("ENG_PREFILL_ROWS", 0)
 
 
 def test_graph_decode_equals_eager_steps(dev, attn_mode):

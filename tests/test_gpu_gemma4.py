@@ -410,10 +410,14 @@ def test_gemma4_engine_prefill_logits(dev):
         _close(e.logits(), gold["logits"][-1], 2e-3)
 
 
-def test_gemma4_engine_prefill_chunks(dev):
-    """A prompt of two chunks (256 + 44 rows, far past the window of 16): the
-    second chunk attends to the first's cached keys; the last row's logits
-    match the oracle run with the prefill's fp16 activation points."""
+@pytest.mark.parametrize("chunk", [256, 0], ids=["chunk256", "default-chunk"])
+def test_gemma4_engine_prefill_chunks(dev, chunk):
+    """A prompt of 300 rows, far past the window of 16, as two chunks (256 +
+    44 rows: the second attends to the first's cached keys) and as one (the
+    default 1024-row chunk); the last row's logits match the oracle run with
+    the prefill's fp16 activation points."""
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
     cfg = g4.G4_TINY
     _, seed, qk, _, _ = _golden()
     prompt = np.random.default_rng(5).integers(0, cfg.vocab, 300).tolist()
@@ -421,10 +425,14 @@ def test_gemma4_engine_prefill_chunks(dev):
     oracle.tokens[: len(prompt)] = prompt
     for pos in range(len(prompt)):
         raw = oracle.forward(pos, half_acts=True)
-    with _engine(cfg, 320, seed, qk) as e:
-        e.set_tokens(prompt)
-        e.prefill(len(prompt))
-        _close(e.logits(), oracle.softcap(raw), 2e-3)
+    _lib.set_tunable("ENG_PREFILL_ROWS", chunk)
+    try:
+        with _engine(cfg, 320, seed, qk) as e:
+            e.set_tokens(prompt)
+            e.prefill(len(prompt))
+            _close(e.logits(), oracle.softcap(raw), 2e-3)
+    finally:
+        _lib.set_tunable("ENG_PREFILL_ROWS", 0)
 
 
 def test_gemma4_engine_decode_graph_equals_steps(dev, g4_resadd):

@@ -43,9 +43,11 @@ def _wx(rng, B, M, K):
 
 # B rows x M x K: 16 rows (the matrix-core threshold), one and several
 # 64-row activation tiles with ragged tails, weight-row tiles that leave a
-# partial group of eight (the XCD-ordered grid), and the per-row fallbacks
-# (B < 16; K not a multiple of 512).
-SHAPES = [(16, 640, 512), (64, 2048, 2048), (130, 640, 1024), (257, 1280, 2048), (5, 640, 512), (40, 384, 1000)]
+# partial group of eight (the XCD-ordered grid), chunk counts 4 does not
+# divide (K = 128, 256: one workgroup chunk; 384, 640: one-chunk splits), and
+# the per-row fallbacks (B < 16; K not a multiple of 128).
+SHAPES = [(16, 640, 512), (64, 2048, 2048), (130, 640, 1024), (257, 1280, 2048), (48, 1536, 256), (20, 640, 128),
+          (70, 384, 384), (33, 640, 640), (5, 640, 512), (40, 384, 1000)]
 
 
 @pytest.mark.parametrize("B,M,K", SHAPES)
@@ -60,11 +62,11 @@ def test_gemm_f16(dev, rng, B, M, K, epi):
     _close(Y.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("B,K", [(7, 2048), (64, 2048), (256, 16384), (40, 520)])
+@pytest.mark.parametrize("B,K", [(7, 2048), (64, 2048), (256, 16384), (64, 256), (40, 520)])
 def test_gemm_f16_fp32_activations(dev, rng, B, K):
     """fp32 X is rounded to fp16 as the product loads it: on the matrix cores
     the result equals the product of the fp16-cast X bit for bit; the per-row
-    matvecs (below 16 rows, or K % 512 != 0) sum the same fp16 values in
+    matvecs (below 16 rows, or K % 128 != 0) sum the same fp16 values in
     another instruction order; both match the oracle on fp16(X)."""
     ops = _ops()
     M = 384
@@ -73,7 +75,7 @@ def test_gemm_f16_fp32_activations(dev, rng, B, K):
     Wd = torch.from_numpy(W).to(dev)
     got = ops.gemm_f16(Wd, torch.from_numpy(X).to(dev)).cpu().numpy()
     cast = ops.gemm_f16(Wd, torch.from_numpy(X.astype(np.float16)).to(dev)).cpu().numpy()
-    if B >= 16 and K % 512 == 0:
+    if B >= 16 and K % 128 == 0:
         assert np.array_equal(got, cast)
     else:
         assert np.abs(got - cast).max() <= 1e-6 * np.abs(cast).max()
@@ -98,7 +100,7 @@ def test_gemm_f16_k_splits(dev, rng, nch):
         _lib.set_tunable("GM_NCH", 0)
 
 
-@pytest.mark.parametrize("B,F,K", [(16, 640, 512), (70, 1024, 2048), (300, 512, 1024), (8, 640, 512)])
+@pytest.mark.parametrize("B,F,K", [(16, 640, 512), (70, 1024, 2048), (300, 512, 1024), (32, 512, 256), (8, 640, 512)])
 @pytest.mark.parametrize("act", ["gelu_tanh", "silu"])
 def test_gemm_gate_up_f16(dev, rng, B, F, K, act):
     ops = _ops()
