@@ -12,8 +12,9 @@
 //
 // Work layout (gfx950, v_mfma_f32_32x32x16_f16):
 //  * a workgroup of 4 waves owns 128 weight rows (32 per wave; for the
-//    gate/up pair 64 rows of each matrix) x 64 activation rows x one split of
-//    K, walked in chunks of 128 k (4 quantisation blocks);
+//    gate/up pair 64 rows of each matrix) x 64 activation rows (128 for large
+//    fp16 prefill products, see pick_bt) x one split of K, walked in chunks
+//    of 128 k (4 quantisation blocks);
 //  * the weights are the B operand, so each lane's 16 results share one
 //    weight row and one scale, and a lane's 16-byte load (row r, bytes
 //    16h..16h+15 of a 32-byte block, h = lane / 32) feeds both MFMAs of the
@@ -312,15 +313,16 @@ __device__ __forceinline__ void static_for(F&& f) {
 // bytes, two 16-byte loads that are the MFMA operands as they stand; products
 // accumulate in the MFMA accumulators). The k order, the activation side and
 // the epilogues are the same for both.
-template <int WF, int NMAT, int OP, int NCH, bool XF32>
+template <int WF, int NMAT, int OP, int NCH, bool XF32, int BT = GM_BATCH>
 __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
     constexpr int WAVES = GM_WAVES, NT = GM_THREADS;
     constexpr int WPM = WAVES / NMAT;
     constexpr int ROWS = 32 * WPM;
-    constexpr int XPT = GM_BATCH * GM2_CK / 8 / NT;
+    constexpr int NB = BT / 32;  // 32-row activation tiles: MFMAs per weight operand
+    constexpr int XPT = BT * GM2_CK / 8 / NT;
     // Two activation buffers (chunk ci in xs[ci & 1]), rows swizzled: piece p
     // of row b sits at slot p ^ (b & 15).
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][GM_BATCH][GM2_CK];
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][BT][GM2_CK];
     // the split's scales of each wave's 32 rows: [wave][row][NCH * 4 (+8 pad,
     // keeping every row 16-byte aligned for the 16-byte stores below)]
     constexpr bool Q8 = WF == MXD_W_Q8B32;
@@ -334,7 +336,7 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
     int split, rt, bz;
     if (!gemm_tile(a, split, rt, bz)) return;
     const int row0 = rt * ROWS + 32 * (wave % WPM);
-    const int b0 = bz * GM_BATCH;
+    const int b0 = bz * BT;
     const int M = a.M, K = a.K;
     const int c0 = split * NCH;  // a.splits * NCH == K / GM2_CK
 
@@ -402,9 +404,9 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
     }
     store_x(ic<0>{});
     __syncthreads();
-    f32x16_t acc[2];
+    f32x16_t acc[NB];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NB; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
 
@@ -438,15 +440,19 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
             if constexpr (ci + 2 < NCH) load_w(ci + 2, j);
             __builtin_amdgcn_sched_barrier(0);
             const int p0 = 4 * j + 2 * h, sw = mc & 15;
-            const h8_t x00 = *reinterpret_cast<const h8_t*>(&xcur[mc][8 * (p0 ^ sw)]);
-            const h8_t x01 = *reinterpret_cast<const h8_t*>(&xcur[mc][8 * ((p0 + 1) ^ sw)]);
-            const h8_t x10 = *reinterpret_cast<const h8_t*>(&xcur[32 + mc][8 * (p0 ^ sw)]);
-            const h8_t x11 = *reinterpret_cast<const h8_t*>(&xcur[32 + mc][8 * ((p0 + 1) ^ sw)]);
-            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x00, w0, acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x10, w0, acc[1], 0, 0, 0);
-            acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x01, w1, acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x11, w1, acc[1], 0, 0, 0);
-            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
+            // (32t + mc) & 15 == mc & 15: one swizzle for every activation tile
+            h8_t x0[NB], x1[NB];
+#pragma unroll
+            for (int t = 0; t < NB; ++t) {
+                x0[t] = *reinterpret_cast<const h8_t*>(&xcur[32 * t + mc][8 * (p0 ^ sw)]);
+                x1[t] = *reinterpret_cast<const h8_t*>(&xcur[32 * t + mc][8 * ((p0 + 1) ^ sw)]);
+            }
+#pragma unroll
+            for (int t = 0; t < NB; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0[t], w0, acc[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < NB; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1[t], w1, acc[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < NB; ++t) asm volatile("" : "+v"(acc[t]));
         }
         if constexpr (ci + 1 < NCH) {
             store_x(ic<ci + 1>{});
@@ -459,7 +465,7 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
     if (a.splits > 1) {
         if (wr_out < M) {
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < NB; ++t)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int b = brow(t, r);
@@ -469,28 +475,30 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
         return;
     }
     if constexpr (NMAT == 2) {
-        float* xf = reinterpret_cast<float*>(&xs[0][0][0]);  // WPM * 2048 floats: 16 KiB for 4 waves
+        // WPM * NB * 1024 floats (16 KiB at 64 rows, 32 KiB at 128), inside xs
+        static_assert(WPM * NB * 1024 * sizeof(float) <= sizeof(xs), "epilogue scratch exceeds the LDS buffer");
+        float* xf = reinterpret_cast<float*>(&xs[0][0][0]);
         __syncthreads();  // every wave is past its last LDS read
         if (m == 1) {
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < NB; ++t)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) xf[(((wave - WPM) * 2 + t) * 16 + r) * 64 + lane] = acc[t][r];
+                for (int r = 0; r < 16; ++r) xf[(((wave - WPM) * NB + t) * 16 + r) * 64 + lane] = acc[t][r];
         }
         __syncthreads();
         if (m == 1 || wr_out >= M) return;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < NB; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int b = brow(t, r);
-                const float u = xf[((wave * 2 + t) * 16 + r) * 64 + lane];
+                const float u = xf[((wave * NB + t) * 16 + r) * 64 + lane];
                 if (b < a.n_rows) a.Y[(size_t)b * M + wr_out] = epilogue<NMAT, OP>(acc[t][r], u, 0.0f);
             }
     } else {
         if (wr_out >= M) return;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < NB; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int b = brow(t, r);
@@ -537,9 +545,9 @@ bool use_mfma(int wf, int n_rows, int K) {
 // loop; 0 (the runtime loop) when none divides. Fewer, longer splits also save
 // the partials and their reduction (gate/up at 64 rows: 62.2 us with one split
 // of 32 chunks against 65.1 us with two of 16).
-int pick_nch(int wf, int n_rows, int M, int K, int nmat) {
+int pick_nch(int wf, int n_rows, int M, int K, int nmat, int bt = GM_BATCH) {
     const int nck = K / GM2_CK;
-    const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + GM_BATCH - 1) / GM_BATCH);
+    const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + bt - 1) / bt);
     const int forced = mxd::tunable("GM_NCH", 0);
     const bool loop_ok = wf == MXD_W_Q8B32;  // the runtime-loop kernel is int8 only
     if (forced == 1 && loop_ok) return 0;
@@ -559,18 +567,37 @@ int pick_nch(int wf, int n_rows, int M, int K, int nmat) {
 // K splits: nck / NCH for the unrolled kernel; for the runtime loop about two
 // workgroups per CU, at most one split per chunk. GM_SPLITS overrides the
 // latter.
-int pick_splits(int wf, int n_rows, int M, int K, int nmat) {
-    const int nch = pick_nch(wf, n_rows, M, K, nmat);
+int pick_splits(int wf, int n_rows, int M, int K, int nmat, int bt = GM_BATCH) {
+    const int nch = pick_nch(wf, n_rows, M, K, nmat, bt);
     if (nch) return (K / GM2_CK) / nch;
-    const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + GM_BATCH - 1) / GM_BATCH);
+    const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + bt - 1) / bt);
     const int s = mxd::tunable("GM_SPLITS", (512 + tiles - 1) / tiles);
     return max(1, min(s, K / GM2_CK));
 }
 
+// Activation rows per workgroup: 128 for fp16 weights against fp16
+// activations from 256 rows on while that still gives 128 or more tiles (half
+// the CUs), so each weight operand feeds four MFMAs; else 64 (int8 weights,
+// fp32 activations: their staging registers would not fit at 128). Measured
+// on MI355X: gate/up 2 x 16384 x 2048 at 256 / 512 / 1024 rows 68.9 / 129.7 /
+// 254 us against 79.7 / 138.4 / 269 at 64; q|k|v 2560 x 2048 at 1024 rows 26.0
+// against 35.8 us, but at 512 rows (80 tiles) 24.7 against 19.6. GM_BT = 64
+// keeps 64 throughout.
+int pick_bt(int wf, bool xf32, int n_rows, int M, int nmat) {
+    if (wf != MXD_W_F16 || xf32 || n_rows < 256 || mxd::tunable("GM_BT", 128) == 64) return GM_BATCH;
+    const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + 127) / 128);
+    return tiles >= 128 ? 128 : GM_BATCH;
+}
+
+// The workspace of either activation dtype (the size queries do not know it).
 size_t ws_bytes_for(int wf, int n_rows, int M, int K, int nmat) {
     if (n_rows <= 0 || M <= 0 || K <= 0 || !use_mfma(wf, n_rows, K)) return 0;
-    const int s = pick_splits(wf, n_rows, M, K, nmat);
-    return s > 1 ? (size_t)s * n_rows * nmat * M * sizeof(float) : 0;
+    size_t need = 0;
+    for (const int bt : {pick_bt(wf, true, n_rows, M, nmat), pick_bt(wf, false, n_rows, M, nmat)}) {
+        const int s = pick_splits(wf, n_rows, M, K, nmat, bt);
+        if (s > 1) need = max(need, (size_t)s * n_rows * nmat * M * sizeof(float));
+    }
+    return need;
 }
 
 // With defer set, the K-split partials are the result: they go to ws as
@@ -578,7 +605,8 @@ size_t ws_bytes_for(int wf, int n_rows, int M, int K, int nmat) {
 // split 0) and the sum is left to the consumer.
 template <int WF, int NMAT, int OP, bool XF32 = false>
 int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char* fn, bool defer = false) {
-    a.splits = pick_splits(WF, a.n_rows, a.M, a.K, NMAT);
+    const int bt = pick_bt(WF, XF32, a.n_rows, a.M, NMAT);
+    a.splits = pick_splits(WF, a.n_rows, a.M, a.K, NMAT, bt);
     const size_t need =
         a.splits > 1 || defer ? (size_t)a.splits * a.n_rows * NMAT * a.M * sizeof(float) : 0;
     MXD_REQUIRE(need == 0 || (ws && ws_bytes >= need), MXD_ERR_WORKSPACE, "%s: workspace of %zu bytes needed (got %zu)",
@@ -586,10 +614,30 @@ int launch_gemm(GemmArgs a, void* ws, size_t ws_bytes, hipStream_t s, const char
     a.part = static_cast<float*>(ws);
     if (defer && a.splits == 1) a.Y = a.part;
     a.row_tiles = (a.M + GM_ROWS / NMAT - 1) / (GM_ROWS / NMAT);
-    a.batch_tiles = (a.n_rows + GM_BATCH - 1) / GM_BATCH;
+    a.batch_tiles = (a.n_rows + bt - 1) / bt;
     const int pairs = a.row_tiles * a.splits;
     const dim3 grid((unsigned)((pairs + 7) / 8 * 8 * a.batch_tiles));  // see gemm_tile
-    const int nch = pick_nch(WF, a.n_rows, a.M, a.K, NMAT);
+    const int nch = pick_nch(WF, a.n_rows, a.M, a.K, NMAT, bt);
+    if constexpr (WF == MXD_W_F16 && !XF32) {
+        if (bt == 128) {
+            switch (nch) {
+                case 1: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 1, XF32, 128>), grid, dim3(GM_THREADS), 0, s, a); break;
+                case 2: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 2, XF32, 128>), grid, dim3(GM_THREADS), 0, s, a); break;
+                case 4: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 4, XF32, 128>), grid, dim3(GM_THREADS), 0, s, a); break;
+                case 8: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 8, XF32, 128>), grid, dim3(GM_THREADS), 0, s, a); break;
+                case 16: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 16, XF32, 128>), grid, dim3(GM_THREADS), 0, s, a); break;
+                case 32: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 32, XF32, 128>), grid, dim3(GM_THREADS), 0, s, a); break;
+                default: return mxd::fail(MXD_ERR_UNSUPPORTED, "%s: K=%d has no chunk count for fp16 weights", fn, a.K);
+            }
+            if (a.splits > 1 && !defer) {
+                const size_t n = (size_t)a.n_rows * a.M;
+                const size_t nb = (n + 255) / 256;
+                const unsigned blocks = (unsigned)(nb < 4096 ? nb : 4096);
+                hipLaunchKernelGGL((gemm_reduce_kernel<NMAT, OP>), dim3(blocks), dim3(256), 0, s, a);
+            }
+            return mxd::check_launch(fn);
+        }
+    }
     switch (nch) {
         case 4: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 4, XF32>), grid, dim3(GM_THREADS), 0, s, a); break;
         case 8: hipLaunchKernelGGL((gemm_mfma_kernel<WF, NMAT, OP, 8, XF32>), grid, dim3(GM_THREADS), 0, s, a); break;

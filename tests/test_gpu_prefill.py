@@ -65,20 +65,30 @@ def test_gemm_f16(dev, rng, B, M, K, epi):
 @pytest.mark.parametrize("B,K", [(7, 2048), (64, 2048), (256, 16384), (64, 256), (40, 520)])
 def test_gemm_f16_fp32_activations(dev, rng, B, K):
     """fp32 X is rounded to fp16 as the product loads it: on the matrix cores
-    the result equals the product of the fp16-cast X bit for bit; the per-row
-    matvecs (below 16 rows, or K % 128 != 0) sum the same fp16 values in
-    another instruction order; both match the oracle on fp16(X)."""
+    the result equals the product of the fp16-cast X bit for bit when both
+    run the same tiling (fp16 X takes 128-row activation tiles from 256 rows,
+    fp32 X keeps 64, so GM_BT = 64 lines them up); the per-row matvecs (below
+    16 rows, or K % 128 != 0) sum the same fp16 values in another instruction
+    order; all match the oracle on fp16(X)."""
+    from gemmagemini4hackathon2026_10_2425_amd import _lib
+
     ops = _ops()
     M = 384
     W = (rng.standard_normal((M, K), dtype=np.float32) * 0.02).astype(np.float16)
     X = rng.standard_normal((B, K), dtype=np.float32) * 3
     Wd = torch.from_numpy(W).to(dev)
     got = ops.gemm_f16(Wd, torch.from_numpy(X).to(dev)).cpu().numpy()
-    cast = ops.gemm_f16(Wd, torch.from_numpy(X.astype(np.float16)).to(dev)).cpu().numpy()
+    cast_default = ops.gemm_f16(Wd, torch.from_numpy(X.astype(np.float16)).to(dev)).cpu().numpy()
+    _lib.set_tunable("GM_BT", 64)
+    try:
+        cast = ops.gemm_f16(Wd, torch.from_numpy(X.astype(np.float16)).to(dev)).cpu().numpy()
+    finally:
+        _lib.set_tunable("GM_BT", 0)
     if B >= 16 and K % 128 == 0:
         assert np.array_equal(got, cast)
     else:
         assert np.abs(got - cast).max() <= 1e-6 * np.abs(cast).max()
+    assert np.abs(cast_default - cast).max() <= 1e-6 * np.abs(cast).max()
     _close(got, ref.matvec(W, X.astype(np.float16).T).T)
 
 
