@@ -44,10 +44,11 @@ def _wx(rng, B, M, K):
 # B rows x M x K: 16 rows (the matrix-core threshold), one and several
 # 64-row activation tiles with ragged tails, weight-row tiles that leave a
 # partial group of eight (the XCD-ordered grid), chunk counts 4 does not
-# divide (K = 128, 256: one workgroup chunk; 384, 640: one-chunk splits), and
-# the per-row fallbacks (B < 16; K not a multiple of 128).
+# divide (K = 128, 256: one workgroup chunk; 384, 640: one-chunk splits),
+# 12 and 6 chunks per workgroup (K = 1536, 768), and the per-row fallbacks
+# (B < 16; K not a multiple of 128).
 SHAPES = [(16, 640, 512), (64, 2048, 2048), (130, 640, 1024), (257, 1280, 2048), (48, 1536, 256), (20, 640, 128),
-          (70, 384, 384), (33, 640, 640), (5, 640, 512), (40, 384, 1000)]
+          (70, 384, 384), (33, 640, 640), (256, 4096, 1536), (256, 4096, 768), (5, 640, 512), (40, 384, 1000)]
 
 
 @pytest.mark.parametrize("B,M,K", SHAPES)
@@ -110,7 +111,8 @@ def test_gemm_f16_k_splits(dev, rng, nch):
         _lib.set_tunable("GM_NCH", 0)
 
 
-@pytest.mark.parametrize("B,F,K", [(16, 640, 512), (70, 1024, 2048), (300, 512, 1024), (32, 512, 256), (8, 640, 512)])
+@pytest.mark.parametrize("B,F,K", [(16, 640, 512), (70, 1024, 2048), (300, 512, 1024), (32, 512, 256), (256, 4096, 1536),
+                                   (8, 640, 512)])
 @pytest.mark.parametrize("act", ["gelu_tanh", "silu"])
 def test_gemm_gate_up_f16(dev, rng, B, F, K, act):
     ops = _ops()
