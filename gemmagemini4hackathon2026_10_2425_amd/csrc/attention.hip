@@ -49,6 +49,7 @@
 #include <vector>
 
 #include "attn_core.hpp"
+#include "internal.hpp"
 
 namespace {
 
@@ -58,7 +59,8 @@ namespace {
 // sequence writes a zero output.
 template <int HD, int W, bool PF, typename KV>
 __device__ __forceinline__ void attn_split(const AttnArgs& a, const KV& src, int n, int S, int split, int kvh,
-                                           const float* qrow, float* orow, float* ws_o, float* ws_ml) {
+                                           const float* qrow, float* orow, float* ws_o, float* ws_ml,
+                                           uint16_t* orow_h = nullptr) {
     const int nblocks = (n + BLK - 1) / BLK;
     const int lo = window_lo(a, n), blo = lo / BLK;
     const size_t g0 = (size_t)kvh * a.G;
@@ -70,14 +72,20 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a, const KV& src, int
                 ws_ml[(g0 + idx) * 2 + 1] = 1.0f;
             }
         } else if (split == 0) {
-            for (int idx = threadIdx.x; idx < a.G * HD; idx += W * 64) orow[g0 * HD + idx] = 0.0f;
+            for (int idx = threadIdx.x; idx < a.G * HD; idx += W * 64) {
+                if (orow_h)
+                    orow_h[g0 * HD + idx] = 0;
+                else
+                    orow[g0 * HD + idx] = 0.0f;
+            }
         }
         return;
     }
     const int n_active = min(S, nblocks - blo);
     if (split >= n_active) return;  // an empty split
     const size_t prow = (size_t)split * a.n_heads + g0;
-    const CoreOut out{orow + g0 * HD, ws_o + prow * HD, ws_ml + prow * 2, n_active == 1 && !a.partials_only};
+    const CoreOut out{orow ? orow + g0 * HD : nullptr, ws_o + prow * HD, ws_ml + prow * 2,
+                      n_active == 1 && !a.partials_only, nullptr, nullptr, orow_h ? orow_h + g0 * HD : nullptr};
     attn_core<HD, W, PF>(a, src, n, blo + split, S, nblocks, qrow + g0 * HD, out, 0, lo);
 }
 
@@ -100,8 +108,9 @@ __global__ void __launch_bounds__(W * 64) attn_prefill_kernel(AttnArgs a) {
     const int t = blockIdx.x, kvh = blockIdx.y;
     const ContigKV<HD> src{a.k + (size_t)kvh * a.max_ctx * HD, a.v + (size_t)kvh * a.max_ctx * HD};
     const int n = min(a.n_keys + t, a.max_ctx);
-    attn_split<HD, W, PF>(a, src, n, 1, 0, kvh, a.q + (size_t)t * a.q_stride, a.out + (size_t)t * a.out_stride,
-                          a.ws_o, a.ws_ml);
+    attn_split<HD, W, PF>(a, src, n, 1, 0, kvh, a.q + (size_t)t * a.q_stride,
+                          a.out ? a.out + (size_t)t * a.out_stride : nullptr, a.ws_o, a.ws_ml,
+                          a.out_h ? a.out_h + (size_t)t * a.out_stride : nullptr);
 }
 
 // Keys and splits of paged sequence seq (clamped so a bad length can never
@@ -683,8 +692,8 @@ namespace {
 int attention_prefill_impl(const char* name, const float* q, int q_stride, const uint16_t* kcache,
                            const uint16_t* vcache, float* out, int out_stride, int n_heads, int n_kv_heads,
                            int head_dim, int max_ctx, int pos0, int rows, int window, float scale,
-                           mxd_stream_t stream) {
-    MXD_REQUIRE(q && kcache && vcache && out, MXD_ERR_INVALID_ARG, "%s: null pointer", name);
+                           mxd_stream_t stream, uint16_t* out_h = nullptr) {
+    MXD_REQUIRE(q && kcache && vcache && (out || out_h), MXD_ERR_INVALID_ARG, "%s: null pointer", name);
     MXD_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, MXD_ERR_INVALID_ARG,
                 "%s: n_heads=%d must be a positive multiple of n_kv_heads=%d", name, n_heads, n_kv_heads);
     const int G = n_heads / n_kv_heads;
@@ -707,7 +716,8 @@ int attention_prefill_impl(const char* name, const float* q, int q_stride, const
     a.q = q;
     a.k = kcache;
     a.v = vcache;
-    a.out = out;
+    a.out = out_h ? nullptr : out;
+    a.out_h = out_h;
     a.ws_o = nullptr;
     a.ws_ml = nullptr;
     a.pos_dev = nullptr;
@@ -745,6 +755,16 @@ extern "C" int mxd_attention_prefill_window(const float* q, int q_stride, const 
                                             int window, float scale, mxd_stream_t stream) {
     return attention_prefill_impl("mxd_attention_prefill_window", q, q_stride, kcache, vcache, out, out_stride,
                                   n_heads, n_kv_heads, head_dim, max_ctx, pos0, rows, window, scale, stream);
+}
+
+// mxd_attention_prefill_window with fp16 output rows (the engines' prefill,
+// whose o projection takes the attention rows rounded to fp16).
+int mxd::attention_prefill_h16(const float* q, int q_stride, const uint16_t* kcache, const uint16_t* vcache,
+                               uint16_t* out, int out_stride, int n_heads, int n_kv_heads, int head_dim, int max_ctx,
+                               int pos0, int rows, int window, float scale, hipStream_t stream) {
+    return attention_prefill_impl("attention_prefill_h16", q, q_stride, kcache, vcache, nullptr, out_stride, n_heads,
+                                  n_kv_heads, head_dim, max_ctx, pos0, rows, window, scale,
+                                  reinterpret_cast<mxd_stream_t>(stream), out);
 }
 
 extern "C" size_t mxd_attention_paged_workspace_size(int n_heads, int n_kv_heads, int head_dim, int n_seqs,

@@ -24,6 +24,9 @@ struct AttnArgs {
     const uint16_t* k;  // contiguous tiled cache, or the page pool
     const uint16_t* v;
     float* out;
+    // prefill: the output rows in fp16 instead (out's strides), rounded to
+    // nearest even as mxd_f32_to_f16 rounds
+    uint16_t* out_h = nullptr;
     float* ws_o;   // [seqs][n_splits][n_heads][HD]
     float* ws_ml;  // [seqs][n_splits][n_heads][2]
     const int32_t* pos_dev;
@@ -183,6 +186,8 @@ struct CoreOut {
     // tagged mode: the same values as tagged words (rows, then (max, sum) pairs)
     uint64_t* trow = nullptr;
     uint64_t* tml = nullptr;
+    // a direct output in fp16 at these rows instead of orow
+    uint16_t* orow_h = nullptr;
 };
 
 // Tagged mode: put the new key and value of position a.patch_pos (fp16 of the
@@ -466,6 +471,8 @@ __device__ __forceinline__ void attn_core(const AttnArgs& a, const KV& src, int 
         for (int w = 0; w < W; ++w) v += sm_c[w][h] * (sm_o[w][h][dim] + sm_o[w][h + 8][dim]);
         if constexpr (TAGGED)
             mxd::tag_put(out.trow + idx, a.tag, v);
+        else if (out.direct && out.orow_h)
+            out.orow_h[idx] = mxd::f2h_bits(v);
         else
             dst[idx] = v;
     }

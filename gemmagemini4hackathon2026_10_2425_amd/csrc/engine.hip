@@ -138,15 +138,23 @@ int encode_prefill(mxd_engine* e, int pos0, int T, bool sample) {
         if ((rc = mxd_rmsnorm(e->bx, Lp.attn_norm, e->bxn, MXD_F16, T, D, c.rms_eps, c.norm_plus_one, ms))) return rc;
         if ((rc = mxd_gemm_f16(Lp.wqkv, e->bxn, MXD_F16, e->bqkv, T, QKV, D, MXD_EPI_STORE, ws, wsb, ms))) return rc;
         if ((rc = mxd_rope_kv(e->bqkv, Lp.kc, Lp.vc, e->invf, NH, NKV, HD, e->max_ctx, pos0, T, ms))) return rc;
-        if ((rc = mxd_attention_prefill(e->bqkv, QKV, Lp.kc, Lp.vc, e->batt, QD, NH, NKV, HD, e->max_ctx, pos0, T,
-                                        ascale, ms)))
+        // The attention rows and the hidden rows are rounded to fp16 where
+        // they are written (the reference's attHalf / hidHalf casts), in the
+        // fp32 buffers' memory, so the o and down products stage fp16 rows.
+        uint16_t* batt_h = reinterpret_cast<uint16_t*>(e->batt);
+        if ((rc = mxd::attention_prefill_h16(e->bqkv, QKV, Lp.kc, Lp.vc, batt_h, QD, NH, NKV, HD, e->max_ctx, pos0, T,
+                                             0, ascale, s)))
             return rc;
-        // the fp32 attention rows and hidden rows are rounded to fp16 as the
-        // products load them (the reference's attHalf / hidHalf casts)
-        if ((rc = mxd_gemm_f16(Lp.wo, e->batt, MXD_F32, e->bx, T, D, QD, MXD_EPI_ADD, ws, wsb, ms))) return rc;
+        if ((rc = mxd_gemm_f16(Lp.wo, batt_h, MXD_F16, e->bx, T, D, QD, MXD_EPI_ADD, ws, wsb, ms))) return rc;
         if ((rc = mxd_rmsnorm(e->bx, Lp.ffn_norm, e->bxn, MXD_F16, T, D, c.rms_eps, c.norm_plus_one, ms))) return rc;
-        if ((rc = mxd_gemm_gate_up_f16(Lp.wgate, Lp.wup, e->bxn, e->bh, T, F, D, c.act, ws, wsb, ms))) return rc;
-        if ((rc = mxd_gemm_f16(Lp.wdown, e->bh, MXD_F32, e->bx, T, D, F, MXD_EPI_ADD, ws, wsb, ms))) return rc;
+        if (mxd::gemm_on_matrix_cores(T, D)) {
+            uint16_t* bh_h = reinterpret_cast<uint16_t*>(e->bh);
+            if ((rc = mxd::gemm_gate_up_f16_h16(Lp.wgate, Lp.wup, e->bxn, bh_h, T, F, D, c.act, ws, wsb, s))) return rc;
+            if ((rc = mxd_gemm_f16(Lp.wdown, bh_h, MXD_F16, e->bx, T, D, F, MXD_EPI_ADD, ws, wsb, ms))) return rc;
+        } else {  // per-row matvecs: fp32 hidden rows, rounded as the down product loads them
+            if ((rc = mxd_gemm_gate_up_f16(Lp.wgate, Lp.wup, e->bxn, e->bh, T, F, D, c.act, ws, wsb, ms))) return rc;
+            if ((rc = mxd_gemm_f16(Lp.wdown, e->bh, MXD_F32, e->bx, T, D, F, MXD_EPI_ADD, ws, wsb, ms))) return rc;
+        }
     }
     if (!sample) return MXD_OK;
     // Only the last row needs logits: it takes the decode path's head.

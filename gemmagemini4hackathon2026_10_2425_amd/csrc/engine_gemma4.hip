@@ -246,15 +246,25 @@ int g4_prefill_chunk(mxd_engine* e, int pos0, int T, bool sample) {
                                       own ? Lp.k_norm : nullptr, e->invf + (size_t)l * G4_FREQS, NH, own ? NKV : 0,
                                       hd, y.rope_pairs, e->max_ctx, eps, pos0, T, nullptr, ms)))
             return rc;
-        if ((rc = mxd_attention_prefill_window(e->bqkv, QKV, Lp.kc, Lp.vc, e->batt, QD, NH, NKV, hd, e->max_ctx, pos0,
-                                               T, y.sliding ? c.window : 0, 1.0f, ms)))
+        // attention and hidden rows rounded to fp16 where they are written, in
+        // the fp32 buffers' memory (the o and down products stage fp16 rows)
+        uint16_t* batt_h = reinterpret_cast<uint16_t*>(e->batt);
+        if ((rc = mxd::attention_prefill_h16(e->bqkv, QKV, Lp.kc, Lp.vc, batt_h, QD, NH, NKV, hd, e->max_ctx, pos0, T,
+                                             y.sliding ? c.window : 0, 1.0f, s)))
             return rc;
-        if ((rc = mxd_gemm_f16(Lp.wo, e->batt, MXD_F32, e->btmp, T, D, QD, MXD_EPI_STORE, ws, wsb, ms))) return rc;
+        if ((rc = mxd_gemm_f16(Lp.wo, batt_h, MXD_F16, e->btmp, T, D, QD, MXD_EPI_STORE, ws, wsb, ms))) return rc;
         if ((rc = mxd_rmsnorm_add(e->btmp, Lp.post_attn_norm, e->bx, T, D, eps, 1.0f, ms))) return rc;
         if ((rc = mxd_rmsnorm(e->bx, Lp.ffn_norm, e->bxn, MXD_F16, T, D, eps, 0, ms))) return rc;
-        if ((rc = mxd_gemm_gate_up_f16(Lp.wgate, Lp.wup, e->bxn, e->bh, T, F, D, MXD_ACT_GELU_TANH, ws, wsb, ms)))
-            return rc;
-        if ((rc = mxd_gemm_f16(Lp.wdown, e->bh, MXD_F32, e->btmp, T, D, F, MXD_EPI_STORE, ws, wsb, ms))) return rc;
+        if (mxd::gemm_on_matrix_cores(T, D)) {
+            uint16_t* bh_h = reinterpret_cast<uint16_t*>(e->bh);
+            if ((rc = mxd::gemm_gate_up_f16_h16(Lp.wgate, Lp.wup, e->bxn, bh_h, T, F, D, MXD_ACT_GELU_TANH, ws, wsb, s)))
+                return rc;
+            if ((rc = mxd_gemm_f16(Lp.wdown, bh_h, MXD_F16, e->btmp, T, D, F, MXD_EPI_STORE, ws, wsb, ms))) return rc;
+        } else {  // per-row matvecs: fp32 hidden rows, rounded as the down product loads them
+            if ((rc = mxd_gemm_gate_up_f16(Lp.wgate, Lp.wup, e->bxn, e->bh, T, F, D, MXD_ACT_GELU_TANH, ws, wsb, ms)))
+                return rc;
+            if ((rc = mxd_gemm_f16(Lp.wdown, e->bh, MXD_F32, e->btmp, T, D, F, MXD_EPI_STORE, ws, wsb, ms))) return rc;
+        }
         if ((rc = mxd_rmsnorm_add(e->btmp, Lp.post_ffn_norm, e->bx, T, D, eps, 1.0f, ms))) return rc;
         // the gate reads the un-normalized residual, rounded to fp16 (KG/main.swift:507)
         if ((rc = mxd_gemm_f16(Lp.ple_gate, e->bx, MXD_F32, e->bpleg, T, P, D, MXD_EPI_STORE, ws, wsb, ms))) return rc;

@@ -57,6 +57,7 @@ struct GemmArgs {
     const uint16_t* X;  // fp16 [n_rows][K]
     const float* Xf;    // or fp32 [n_rows][K], rounded to fp16 as it is staged (XF32 kernels)
     float* Y;           // fp32 [n_rows][M]
+    uint16_t* Yh;       // or fp16 [n_rows][M] (nearest even), the store / activation epilogues only
     float* part;        // fp32 [splits][n_rows][NMAT][M] when splits > 1
     int n_rows, M, K, splits;
     int row_tiles, batch_tiles;  // weight-row tiles of GM_ROWS / NMAT, activation tiles of GM_BATCH
@@ -493,7 +494,13 @@ __global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
             for (int r = 0; r < 16; ++r) {
                 const int b = brow(t, r);
                 const float u = xf[((wave * NB + t) * 16 + r) * 64 + lane];
-                if (b < a.n_rows) a.Y[(size_t)b * M + wr_out] = epilogue<NMAT, OP>(acc[t][r], u, 0.0f);
+                if (b < a.n_rows) {
+                    const float y = epilogue<NMAT, OP>(acc[t][r], u, 0.0f);
+                    if (a.Yh)
+                        a.Yh[(size_t)b * M + wr_out] = mxd::f2h_bits(y);
+                    else
+                        a.Y[(size_t)b * M + wr_out] = y;
+                }
             }
     } else {
         if (wr_out >= M) return;
@@ -523,7 +530,10 @@ __global__ void __launch_bounds__(256) gemm_reduce_kernel(GemmArgs a) {
             s0 += p[sp * stride];
             if (NMAT == 2) s1 += p[sp * stride + a.M];
         }
-        a.Y[e] = epilogue<NMAT, OP>(s0, s1, OP == MXD_EPI_ADD && NMAT == 1 ? a.Y[e] : 0.0f);
+        if (NMAT == 2 && a.Yh)
+            a.Yh[e] = mxd::f2h_bits(epilogue<NMAT, OP>(s0, s1, 0.0f));
+        else
+            a.Y[e] = epilogue<NMAT, OP>(s0, s1, OP == MXD_EPI_ADD && NMAT == 1 ? a.Y[e] : 0.0f);
     }
 }
 
@@ -891,4 +901,26 @@ extern "C" int mxd_gemm_gate_up_f16(const uint16_t* Wg, const uint16_t* Wu, cons
     if (act == MXD_ACT_SILU)
         return launch_gemm<MXD_W_F16, 2, MXD_ACT_SILU>(a, workspace, ws_bytes, s, "mxd_gemm_gate_up_f16");
     return launch_gemm<MXD_W_F16, 2, MXD_ACT_GELU_TANH>(a, workspace, ws_bytes, s, "mxd_gemm_gate_up_f16");
+}
+
+bool mxd::gemm_on_matrix_cores(int n_rows, int K) { return use_mfma(MXD_W_F16, n_rows, K); }
+
+int mxd::gemm_gate_up_f16_h16(const uint16_t* Wg, const uint16_t* Wu, const uint16_t* X, uint16_t* H, int n_rows,
+                              int F, int K, int act, void* workspace, size_t ws_bytes, hipStream_t s) {
+    const char* fn = "gemm_gate_up_f16_h16";
+    MXD_REQUIRE(Wg && Wu && X && H, MXD_ERR_INVALID_ARG, "%s: null pointer", fn);
+    MXD_REQUIRE(act == MXD_ACT_GELU_TANH || act == MXD_ACT_SILU, MXD_ERR_INVALID_ARG, "%s: unknown activation %d", fn,
+                act);
+    MXD_REQUIRE(F > 0 && use_mfma(MXD_W_F16, n_rows, K), MXD_ERR_UNSUPPORTED,
+                "%s: n_rows=%d K=%d is not a matrix-core product", fn, n_rows, K);
+    GemmArgs a{};
+    a.W[0] = reinterpret_cast<const int8_t*>(Wg);
+    a.W[1] = reinterpret_cast<const int8_t*>(Wu);
+    a.X = X;
+    a.Yh = H;
+    a.n_rows = n_rows;
+    a.M = F;
+    a.K = K;
+    if (act == MXD_ACT_SILU) return launch_gemm<MXD_W_F16, 2, MXD_ACT_SILU>(a, workspace, ws_bytes, s, fn);
+    return launch_gemm<MXD_W_F16, 2, MXD_ACT_GELU_TANH>(a, workspace, ws_bytes, s, fn);
 }

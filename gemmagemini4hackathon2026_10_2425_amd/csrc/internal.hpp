@@ -43,4 +43,18 @@ int fill_normal_dev(void* dst, int dtype, uint64_t n, uint64_t seed, uint64_t te
 int matvec_xr16(int w_format, const void* W, const uint16_t* scales, const float* x, float* y, int M, int K,
                 int epilogue, hipStream_t s);
 
+// Prefill with fp16 activation rows between ops (the engines' prefill rounds
+// the attention and hidden rows to fp16 before the products that read them;
+// writing them as fp16 lets those products stage fp16 rows):
+// mxd_attention_prefill_window with fp16 output rows (out_stride halfs apart),
+// and mxd_gemm_gate_up_f16 with fp16 H.
+int attention_prefill_h16(const float* q, int q_stride, const uint16_t* kcache, const uint16_t* vcache, uint16_t* out,
+                          int out_stride, int n_heads, int n_kv_heads, int head_dim, int max_ctx, int pos0, int rows,
+                          int window, float scale, hipStream_t stream);
+int gemm_gate_up_f16_h16(const uint16_t* Wg, const uint16_t* Wu, const uint16_t* X, uint16_t* H, int n_rows, int F,
+                         int K, int act, void* workspace, size_t ws_bytes, hipStream_t stream);
+// Whether an fp16 product of n_rows rows and depth K runs on the matrix cores
+// (gemm_gate_up_f16_h16 needs it; below, the products run one matvec per row).
+bool gemm_on_matrix_cores(int n_rows, int K);
+
 }  // namespace mxd
