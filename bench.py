@@ -523,6 +523,9 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
         log("ragged batch leg")
         detail["ragged_layer_llama8b_64seq"] = ragged_layer_leg(args.steps, args.warmup, dev)
+        torch.cuda.empty_cache()
+        log("prefill leg (Gemma-2B, 512-token prompt)")
+        detail["prefill_gemma2b_pp512"] = prefill_leg(512)
     detail["gemv_f16"] = g["per_shape"]
     detail["gemv_f16_stream_launched_gbs"] = round(g["stream_launched_gbs"], 1)
     cpu = None
