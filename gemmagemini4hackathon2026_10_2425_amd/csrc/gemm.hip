@@ -314,8 +314,13 @@ __device__ __forceinline__ void static_for(F&& f) {
 // bytes, two 16-byte loads that are the MFMA operands as they stand; products
 // accumulate in the MFMA accumulators). The k order, the activation side and
 // the epilogues are the same for both.
+// At 128 activation rows the kernel asks for two waves per SIMD (256 VGPRs;
+// the compiler spills 2 dwords per lane at 8-16 chunks): left to itself it
+// took 257-280 registers and one wave per SIMD, and the two-wave form ran
+// gate/up 2 x 16384 x 2048 at 512 / 1024 rows in 117.6 / 197 us against 142 /
+// 260 (measured on MI355X).
 template <int WF, int NMAT, int OP, int NCH, bool XF32, int BT = GM_BATCH>
-__global__ void __launch_bounds__(GM_THREADS) gemm_mfma_kernel(GemmArgs a) {
+__global__ void __launch_bounds__(GM_THREADS, BT == 128 ? 2 : 1) gemm_mfma_kernel(GemmArgs a) {
     constexpr int WAVES = GM_WAVES, NT = GM_THREADS;
     constexpr int WPM = WAVES / NMAT;
     constexpr int ROWS = 32 * WPM;
