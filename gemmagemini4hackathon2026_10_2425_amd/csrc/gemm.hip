@@ -560,7 +560,7 @@ bool use_mfma(int wf, int n_rows, int K) {
 // loop; 0 (the runtime loop) when none divides. Fewer, longer splits also save
 // the partials and their reduction (gate/up at 64 rows: 62.2 us with one split
 // of 32 chunks against 65.1 us with two of 16).
-int pick_nch(int wf, int n_rows, int M, int K, int nmat, int bt = GM_BATCH) {
+int pick_nch(int wf, int n_rows, int M, int K, int nmat, int bt) {
     const int nck = K / GM2_CK;
     const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + bt - 1) / bt);
     const int forced = mxd::tunable("GM_NCH", 0);
@@ -595,17 +595,22 @@ int pick_splits(int wf, int n_rows, int M, int K, int nmat, int bt = GM_BATCH) {
 }
 
 // Activation rows per workgroup: 128 for fp16 weights against fp16
-// activations from 256 rows on while that still gives 128 or more tiles (half
-// the CUs), so each weight operand feeds four MFMAs; else 64 (int8 weights,
-// fp32 activations: their staging registers would not fit at 128). Measured
-// on MI355X: gate/up 2 x 16384 x 2048 at 256 / 512 / 1024 rows 68.9 / 129.7 /
-// 254 us against 79.7 / 138.4 / 269 at 64; q|k|v 2560 x 2048 at 1024 rows 26.0
-// against 35.8 us, but at 512 rows (80 tiles) 24.7 against 19.6. GM_BT = 64
-// keeps 64 throughout.
+// activations from 256 rows on while that leaves 128 or more tiles (half the
+// CUs), and from 512 rows on while it leaves GM_BT_TILES (16) or more, so each
+// weight operand feeds four MFMAs; else 64 (int8 weights, fp32 activations:
+// their staging registers would not fit at 128). Measured on MI355X: gate/up
+// 2 x 16384 x 2048 at 256 / 512 / 1024 rows 68.9 / 129.7 / 254 us against
+// 79.7 / 138.4 / 269 at 64; down 2048 x 16384 at 512 rows 59.6 against 77.1.
+// Alone, q|k|v 2560 x 2048 and o 2048 x 2048 at 512 rows ran slower at 128
+// (25.2 / 22.5 against 20.8 / 19.2 us), but the Gemma-2B pp512 prefill ran
+// 102.6-103.1k tok/s with every product at 128 rows against 93.6-94.0k with
+// only gate/up at 128 (E2B pp512 57.0k against 54.3k); at 256 rows every
+// product at 128 ran pp256 at 67.7k against 74.0k. GM_BT = 64 keeps 64.
 int pick_bt(int wf, bool xf32, int n_rows, int M, int nmat) {
     if (wf != MXD_W_F16 || xf32 || n_rows < 256 || mxd::tunable("GM_BT", 128) == 64) return GM_BATCH;
     const int tiles = ((M + GM_ROWS / nmat - 1) / (GM_ROWS / nmat)) * ((n_rows + 127) / 128);
-    return tiles >= 128 ? 128 : GM_BATCH;
+    if (tiles >= 128) return 128;
+    return n_rows >= 512 && tiles >= mxd::tunable("GM_BT_TILES", 16) ? 128 : GM_BATCH;
 }
 
 // The workspace of either activation dtype (the size queries do not know it).
