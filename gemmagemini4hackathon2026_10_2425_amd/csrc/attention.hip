@@ -102,10 +102,12 @@ __global__ void __launch_bounds__(W * 64) attn_split_kernel(AttnArgs a) {
 // contiguous cache (their keys and values already appended); query t sees
 // keys [0, pos0 + t] (a.n_keys = pos0 + 1). Grid (rows, n_kv): one workgroup
 // per (query, kv head), one split, so each writes its output rows directly;
-// the kv head's G query heads share every K/V tile as in decode.
+// the kv head's G query heads share every K/V tile as in decode. Workgroups
+// start with the last (longest) rows, so the short ones fill the tail
+// (Gemma-2B pp1024 on MI355X: 124.5-124.8k against 122.6-123.2k tok/s).
 template <int HD, int W, bool PF>
 __global__ void __launch_bounds__(W * 64) attn_prefill_kernel(AttnArgs a) {
-    const int t = blockIdx.x, kvh = blockIdx.y;
+    const int t = gridDim.x - 1 - blockIdx.x, kvh = blockIdx.y;
     const ContigKV<HD> src{a.k + (size_t)kvh * a.max_ctx * HD, a.v + (size_t)kvh * a.max_ctx * HD};
     const int n = min(a.n_keys + t, a.max_ctx);
     attn_split<HD, W, PF>(a, src, n, 1, 0, kvh, a.q + (size_t)t * a.q_stride,
