@@ -89,8 +89,20 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a, const KV& src, int
     attn_core<HD, W, PF>(a, src, n, blo + split, S, nblocks, qrow + g0 * HD, out, 0, lo);
 }
 
+// Waves per SIMD the register allocation must allow. Left to itself the
+// head_dim 256 core takes 224 VGPRs + 64 AGPRs, one wave per SIMD; capped at
+// 256 registers (a spill of 7-9 dwords per lane) it runs two. The prefetch
+// variant would spill 132 dwords and keeps its one wave. Measured on MI355X,
+// two alternating runs: Gemma-4-E2B pp512 58.1-58.3k against 57.3-57.4k
+// tok/s, Gemma-2B pp1024 122.0-122.2k against 120.6-121.6k; decode, whose
+// head_dim 256 attention is 6 workgroups, unchanged.
+template <int HD, bool PF>
+constexpr int att_min_waves() {
+    return HD == 256 && !PF ? 2 : 1;
+}
+
 template <int HD, int W, bool PF>
-__global__ void __launch_bounds__(W * 64) attn_split_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(W * 64, (att_min_waves<HD, PF>())) attn_split_kernel(AttnArgs a) {
     const int kvh = blockIdx.y;
     const ContigKV<HD> src{a.k + (size_t)kvh * a.max_ctx * HD, a.v + (size_t)kvh * a.max_ctx * HD};
     const int n = n_keys_of(a);
@@ -106,7 +118,7 @@ __global__ void __launch_bounds__(W * 64) attn_split_kernel(AttnArgs a) {
 // start with the last (longest) rows, so the short ones fill the tail
 // (Gemma-2B pp1024 on MI355X: 124.5-124.8k against 122.6-123.2k tok/s).
 template <int HD, int W, bool PF>
-__global__ void __launch_bounds__(W * 64) attn_prefill_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(W * 64, (att_min_waves<HD, PF>())) attn_prefill_kernel(AttnArgs a) {
     const int t = gridDim.x - 1 - blockIdx.x, kvh = blockIdx.y;
     const ContigKV<HD> src{a.k + (size_t)kvh * a.max_ctx * HD, a.v + (size_t)kvh * a.max_ctx * HD};
     const int n = min(a.n_keys + t, a.max_ctx);
